@@ -1,0 +1,259 @@
+/*
+ * s3dx_sparse.h -- C ABI of the MI355X (gfx950) sparse-voxel convolution path
+ * of the sam3d.cpp Objects runtime (SLat flow sparse blocks and the mesh
+ * decoder's sparse upsample stack).
+ *
+ * Conventions (mirroring include/sam3d.h:20-41 and src/error.hpp:15-22 of the
+ * reference):
+ *   - every fallible call returns s3dx_status and takes a caller-owned error
+ *     buffer (error, error_capacity); success clears it, failure truncates and
+ *     NUL-terminates the message; NULL,0 discards diagnostics, NULL,nonzero is
+ *     S3DX_INVALID_ARGUMENT;
+ *   - no exception, public struct layout or global last-error crosses the ABI;
+ *   - every data pointer is a caller-owned DEVICE buffer unless the parameter
+ *     says "host";
+ *   - work is enqueued on the caller's stream (a hipStream_t, NULL = the
+ *     default stream); calls that must report a data-dependent result to the
+ *     host (a row count, a rejected input) synchronize that stream and say so;
+ *   - distinct streams/requests may be used concurrently; one workspace must
+ *     not be shared by calls in flight at the same time.
+ *
+ * Data layouts (as in the reference):
+ *   coords   int32 [n][4] = (b, x, y, z), 16-byte aligned
+ *   kmap     int32 [n][27], offset o = (dx+1)*9 + (dy+1)*3 + (dz+1)
+ *            (sparse_ops.cpp:132); any entry outside [0, n_in) is a missing
+ *            neighbour and contributes zero, which covers both the SLat
+ *            sentinel n (sparse_ops.cpp:128) and the mesh sentinel -1
+ *            (sparse_ops.cpp:367)
+ *   features row-major [rows][C] (ggml (C, N), graph_builder.hpp:3-7),
+ *            float32 or bfloat16
+ */
+#ifndef S3DX_SPARSE_H
+#define S3DX_SPARSE_H
+
+#include <stdint.h>
+
+#define S3DX_API __attribute__((visibility("default")))
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef uint32_t s3dx_status;
+#define S3DX_OK UINT32_C(0)
+#define S3DX_INVALID_ARGUMENT UINT32_C(1)
+#define S3DX_OUT_OF_MEMORY UINT32_C(2)
+#define S3DX_INTERNAL_ERROR UINT32_C(3)
+
+typedef void *s3dx_stream; /* hipStream_t */
+typedef void *s3dx_event;  /* hipEvent_t */
+
+/* element types */
+#define S3DX_F32 0
+#define S3DX_BF16 1
+
+/* source weight layouts accepted by s3dx_conv_set_weights (float32, host) */
+#define S3DX_WEIGHT_SLAT 0 /* [Cout][kvol][Cin]: the converter's (Cout, 27*Cin) rows,
+                              scripts/objects/gguf_schema.py:326-334 */
+#define S3DX_WEIGHT_MESH 1 /* [kvol][Cout][Cin]: packed ne{Cin*Cout, 27},
+                              scripts/objects/convert_sam3d_to_gguf.py:486-492 */
+
+#define S3DX_ABI_VERSION UINT32_C(1)
+S3DX_API uint32_t s3dx_abi_version(void);
+
+/* ------------------------------------------------------------------------
+ * Device plumbing: the Backend seam of the reference
+ * (src/objects_runtime/backend.hpp:16-58: alloc, set_input_*, run,
+ * get_tensor_*), reduced to what a caller of this library needs.
+ * ---------------------------------------------------------------------- */
+S3DX_API s3dx_status s3dx_device_info(int32_t *device_count, char *name, uint64_t name_capacity,
+                                      char *error, uint64_t error_capacity);
+S3DX_API s3dx_status s3dx_malloc(void **out, uint64_t bytes, char *error, uint64_t error_capacity);
+S3DX_API void s3dx_free(void *ptr);
+/* Copies enqueue on `stream` and then synchronize it (set_input_* / get_tensor_*). */
+S3DX_API s3dx_status s3dx_memcpy_h2d(void *dst, const void *host_src, uint64_t bytes,
+                                     s3dx_stream stream, char *error, uint64_t error_capacity);
+S3DX_API s3dx_status s3dx_memcpy_d2h(void *host_dst, const void *src, uint64_t bytes,
+                                     s3dx_stream stream, char *error, uint64_t error_capacity);
+S3DX_API s3dx_status s3dx_stream_create(s3dx_stream *out, char *error, uint64_t error_capacity);
+S3DX_API s3dx_status s3dx_stream_destroy(s3dx_stream stream, char *error, uint64_t error_capacity);
+S3DX_API s3dx_status s3dx_stream_synchronize(s3dx_stream stream, char *error, uint64_t error_capacity);
+S3DX_API s3dx_status s3dx_event_create(s3dx_event *out, char *error, uint64_t error_capacity);
+S3DX_API s3dx_status s3dx_event_destroy(s3dx_event event, char *error, uint64_t error_capacity);
+S3DX_API s3dx_status s3dx_event_record(s3dx_event event, s3dx_stream stream, char *error,
+                                       uint64_t error_capacity);
+/* Waits for `stop`, then writes the milliseconds between the two events. */
+S3DX_API s3dx_status s3dx_event_elapsed_ms(s3dx_event start, s3dx_event stop, float *ms,
+                                           char *error, uint64_t error_capacity);
+
+/* ------------------------------------------------------------------------
+ * Kernel maps (the host table builders of sparse_ops.{hpp,cpp}, on device)
+ * ---------------------------------------------------------------------- */
+
+/* Workspace bytes for s3dx_kmap_subm3 on n voxels (host query). */
+S3DX_API s3dx_status s3dx_kmap_workspace_size(int64_t n, uint64_t *bytes, char *error,
+                                              uint64_t error_capacity);
+
+/* Submanifold 3x3x3 neighbour table.  Replaces build_conv
+ * (sparse_ops.cpp:117-142) for the fine and coarse SLat maps (missing_value
+ * = n) and the mesh neighbour rows (missing_value = -1).  kmap[i][o] is the
+ * row of the FIRST voxel with coordinates coords[i] + delta(o), or
+ * missing_value; rows of later duplicates of a coordinate stay entirely
+ * missing_value (sparse_ops.cpp:120-141).  Byte-identical to the reference.
+ * Requires 0 < n <= INT32_MAX / 27.  Asynchronous on `stream`. */
+S3DX_API s3dx_status s3dx_kmap_subm3(const int32_t *coords, int64_t n, int32_t missing_value,
+                                     int32_t *kmap, void *workspace, uint64_t workspace_bytes,
+                                     s3dx_stream stream, char *error, uint64_t error_capacity);
+
+/* Workspace bytes for s3dx_coarsen2 on n fine voxels (host query). */
+S3DX_API s3dx_status s3dx_coarsen2_workspace_size(int64_t n, uint64_t *bytes, char *error,
+                                                  uint64_t error_capacity);
+
+/* 2x OR-pool of the SLat downsample tables (sparse_ops.cpp:53-104).  Coarse
+ * keys are (b, x/2, y/2, z/2) with C++ truncating division; coarse rows are
+ * their lexicographic rank.  Outputs (capacities for nc <= n):
+ *   coarse_coords   int32 [n][4]   (first nc rows written)
+ *   fine_to_coarse  int32 [n]
+ *   coarse_children int32 [8n]     (first 8*nc written; c*8+j = j-th smallest
+ *                                   fine row of coarse row c, sentinel n)
+ *   coarse_inv_count float [n]     (1/(count+1), the scatter-mean quirk)
+ *   *nc_out         host int64
+ * The coarse kernel map is s3dx_kmap_subm3(coarse_coords, nc, nc, ...)
+ * (sparse_ops.cpp:142).  Synchronizes `stream` to return nc. */
+S3DX_API s3dx_status s3dx_coarsen2(const int32_t *coords, int64_t n, int32_t *coarse_coords,
+                                   int32_t *fine_to_coarse, int32_t *coarse_children,
+                                   float *coarse_inv_count, int64_t *nc_out, void *workspace,
+                                   uint64_t workspace_bytes, s3dx_stream stream, char *error,
+                                   uint64_t error_capacity);
+
+/* Workspace bytes for s3dx_subdivide2 on `parent_count` parents (host query). */
+S3DX_API s3dx_status s3dx_subdivide2_workspace_size(int64_t parent_count, uint64_t *bytes,
+                                                    char *error, uint64_t error_capacity);
+
+/* Exact 2x subdivide + child neighbour table, replacing
+ * MeshSubdivideTables::build (sparse_ops.cpp:272-404).  child_coords
+ * [8p][4]: row p*8 + (bx*4 + by*2 + bz) = (b, 2x+bx, 2y+by, 2z+bz), z fastest.
+ * child_kmap [8p][27] (may be NULL): neighbour rows, -1 when missing.
+ * Rejects p <= 0, p > INT32_MAX/8 and duplicate parents with
+ * S3DX_INVALID_ARGUMENT (the reference returns false).  Synchronizes
+ * `stream` to check for duplicates. */
+S3DX_API s3dx_status s3dx_subdivide2(const int32_t *parent_coords, int64_t parent_count,
+                                     int32_t *child_coords, int32_t *child_kmap, void *workspace,
+                                     uint64_t workspace_bytes, s3dx_stream stream, char *error,
+                                     uint64_t error_capacity);
+
+/* ------------------------------------------------------------------------
+ * Sparse convolution layer: the SLat `conv` lambda + gb_linear
+ * (slat_flow_graph.cpp:105-155, graph_builder.cpp:44-54) and the mesh
+ * `convolution` lambda (mesh_decoder_graph.cpp:81-103), as one
+ * gather-GEMM kernel with fused prologue/epilogue.  kvol 1 with a NULL kmap is
+ * a linear layer (1x1 skip, 96->101 head, build_mesh_output_layer
+ * mesh_decoder_graph.cpp:134-140).
+ *
+ * Per output row i:  v = bias + sum_o W_o . in(kmap[i][o])
+ *   in(j)   = x[j]                               (default)
+ *           = x[j >> 3] + slot_offset[j & 7]     (gather_parent: repeat_children
+ *                                                 mesh_decoder_graph.cpp:32-38
+ *                                                 fused into the gather)
+ *           then silu(in*pre_scale + pre_shift)  (input affine+SiLU: GroupNorm
+ *                                                 apply + ggml_silu, fused; missing
+ *                                                 rows stay zero)
+ *   v -> LayerNorm over Cout (eps, optional affine), optional modulate
+ *        v*scale + v + shift (slat_flow_graph.cpp:55-59) -> optional SiLU
+ *        -> optional + residual[i] -> y[i]
+ * Arithmetic: float32 inputs use FP32 MFMA/VALU; bfloat16 inputs use BF16 MFMA;
+ * both accumulate in float32.  Deterministic (no atomics on outputs).
+ * ---------------------------------------------------------------------- */
+typedef struct s3dx_conv s3dx_conv;
+
+/* dtype: S3DX_F32 or S3DX_BF16 (the input feature type and the arithmetic). */
+S3DX_API s3dx_status s3dx_conv_create(int32_t cin, int32_t cout, int32_t kvol, int32_t dtype,
+                                      s3dx_conv **out, char *error, uint64_t error_capacity);
+S3DX_API void s3dx_conv_free(s3dx_conv *conv);
+/* host float32 weights in `layout` and optional host bias [cout]; packed once
+ * into the device layout the kernel reads. */
+S3DX_API s3dx_status s3dx_conv_set_weights(s3dx_conv *conv, const float *host_weight,
+                                           int32_t layout, const float *host_bias,
+                                           char *error, uint64_t error_capacity);
+/* Fused repeat_children; host slot_offset [8][cin] float32 may be NULL. */
+S3DX_API s3dx_status s3dx_conv_set_gather_parent(s3dx_conv *conv, int32_t enable,
+                                                 const float *host_slot_offset, char *error,
+                                                 uint64_t error_capacity);
+/* Fused input affine + SiLU; DEVICE scale/shift [cin] float32, read at run
+ * time (s3dx_groupnorm_stats writes them).  NULL,NULL disables. */
+S3DX_API s3dx_status s3dx_conv_set_input_affine_silu(s3dx_conv *conv, const float *scale,
+                                                     const float *shift, char *error,
+                                                     uint64_t error_capacity);
+/* Fused epilogue LayerNorm (enable 0/1), host affine weight/bias [cout] and
+ * host modulate scale/shift [cout], each may be NULL. */
+S3DX_API s3dx_status s3dx_conv_set_layernorm(s3dx_conv *conv, int32_t enable, float eps,
+                                             const float *host_weight, const float *host_bias,
+                                             const float *host_mod_scale,
+                                             const float *host_mod_shift, char *error,
+                                             uint64_t error_capacity);
+S3DX_API s3dx_status s3dx_conv_set_silu(s3dx_conv *conv, int32_t enable, char *error,
+                                        uint64_t error_capacity);
+/* Runs the layer.  x [n_in or n_in parents][cin] in the conv's dtype; kmap
+ * [n_out][kvol] (NULL only for kvol 1); residual [n_out][cout] in y_dtype or
+ * NULL; y [n_out][cout] in y_dtype.  Asynchronous on `stream`. */
+S3DX_API s3dx_status s3dx_conv_run(const s3dx_conv *conv, const void *x, int64_t n_in,
+                                   const int32_t *kmap, int64_t n_out, const void *residual,
+                                   void *y, int32_t y_dtype, s3dx_stream stream, char *error,
+                                   uint64_t error_capacity);
+
+/* ------------------------------------------------------------------------
+ * Standalone row ops (graph_builder.cpp:56-62, mesh_decoder_graph.cpp:16-30,
+ * slat_flow_graph.cpp:157-190).  x and y may alias where noted.
+ * ---------------------------------------------------------------------- */
+
+/* y = [silu]( modulate( LayerNorm_rows(x, eps) * w + b ) ); w, b, mod_scale,
+ * mod_shift are device [c] float32 or NULL.  x/y dtype F32 or BF16; x == y
+ * allowed. */
+S3DX_API s3dx_status s3dx_layernorm_rows(const void *x, int32_t x_dtype, int64_t n, int32_t c,
+                                         float eps, const float *w, const float *b,
+                                         const float *mod_scale, const float *mod_shift,
+                                         int32_t silu, void *y, int32_t y_dtype,
+                                         s3dx_stream stream, char *error,
+                                         uint64_t error_capacity);
+
+/* Workspace bytes for s3dx_groupnorm_stats (host query). */
+S3DX_API s3dx_status s3dx_groupnorm_workspace_size(int64_t n, int32_t c, int32_t groups,
+                                                   uint64_t *bytes, char *error,
+                                                   uint64_t error_capacity);
+/* SparseGroupNorm statistics over all n rows (eps, groups | c): writes the
+ * per-channel affine scale[c] = gamma*rstd, shift[c] = beta - mean*gamma*rstd
+ * (device float32 [c]) that s3dx_conv_set_input_affine_silu or
+ * s3dx_affine_rows consume.  gamma/beta device [c] or NULL.  Two-pass,
+ * deterministic. */
+S3DX_API s3dx_status s3dx_groupnorm_stats(const void *x, int32_t x_dtype, int64_t n, int32_t c,
+                                          int32_t groups, float eps, const float *gamma,
+                                          const float *beta, float *scale, float *shift,
+                                          void *workspace, uint64_t workspace_bytes,
+                                          s3dx_stream stream, char *error,
+                                          uint64_t error_capacity);
+/* y = [silu](x*scale + shift) per channel; x == y allowed. */
+S3DX_API s3dx_status s3dx_affine_rows(const void *x, int32_t x_dtype, int64_t n, int32_t c,
+                                      const float *scale, const float *shift, int32_t silu,
+                                      void *y, int32_t y_dtype, s3dx_stream stream, char *error,
+                                      uint64_t error_capacity);
+
+/* SLat downsample (slat_flow_graph.cpp:159-183): y[r] = inv_count[r] *
+ * sum_j x[children[r*8+j]], entries outside [0, nf) contribute zero. */
+S3DX_API s3dx_status s3dx_downsample_mean(const void *x, int32_t dtype, int64_t nf, int32_t c,
+                                          const int32_t *children, const float *inv_count,
+                                          int64_t nc, void *y, s3dx_stream stream, char *error,
+                                          uint64_t error_capacity);
+/* SLat upsample (slat_flow_graph.cpp:186-190): y[i] = coarse[fine_to_coarse[i]]. */
+S3DX_API s3dx_status s3dx_upsample_nearest(const void *coarse, int32_t dtype, int64_t nc,
+                                           int32_t c, const int32_t *fine_to_coarse, int64_t nf,
+                                           void *y, s3dx_stream stream, char *error,
+                                           uint64_t error_capacity);
+/* dtype conversion F32 <-> BF16 (round to nearest even), count elements. */
+S3DX_API s3dx_status s3dx_convert(const void *x, int32_t x_dtype, int64_t count, void *y,
+                                  int32_t y_dtype, s3dx_stream stream, char *error,
+                                  uint64_t error_capacity);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

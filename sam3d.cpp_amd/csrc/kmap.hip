@@ -1,0 +1,640 @@
+// Kernel maps on the GPU: the coordinate hash, the 27-offset submanifold
+// neighbour table, the 2x OR-pool (coarse set) and the exact 2x subdivide.
+//
+// Reference semantics (all host C++ in sam3d.cpp):
+//   build_conv            src/objects_runtime/sparse_ops.cpp:117-142
+//   SlatTables downsample src/objects_runtime/sparse_ops.cpp:53-104
+//   MeshSubdivideTables   src/objects_runtime/sparse_ops.cpp:272-404
+//
+// The hash is open addressing with linear probing over 64-bit slots holding
+// (32-bit key tag << 32 | row).  A slot is claimed with a 64-bit CAS; a
+// second row with the same coordinates lowers the row half with a 64-bit
+// atomicMin, so after the insert kernel every key maps to its smallest row --
+// exactly std::map::emplace's "first occurrence wins".  Keys are the full
+// (b, x, y, z) int32 tuple: a tag match is confirmed against the coordinate
+// array, so any int32 coordinates are handled exactly.
+#include "common.hpp"
+
+#include <vector>
+
+namespace s3dx {
+namespace {
+
+constexpr uint64_t kEmpty = ~0ull;
+constexpr int kThreads = 256;
+
+// Workspace flag words.
+constexpr int kFlagDuplicate = 0;  // some coordinate occurs twice
+constexpr int kFlagOverflow = 1;   // probe sequence exhausted (never at load <= 1/2)
+
+__device__ __forceinline__ uint64_t fmix64(uint64_t k) {
+    k ^= k >> 33;
+    k *= 0xff51afd7ed558ccdULL;
+    k ^= k >> 33;
+    k *= 0xc4ceb9fe1a85ec53ULL;
+    k ^= k >> 33;
+    return k;
+}
+
+__device__ __forceinline__ uint64_t key_hash(int4 c) {
+    const uint64_t xy = static_cast<uint64_t>(static_cast<uint32_t>(c.y)) |
+                        (static_cast<uint64_t>(static_cast<uint32_t>(c.z)) << 32);
+    const uint64_t zb = static_cast<uint64_t>(static_cast<uint32_t>(c.w)) |
+                        (static_cast<uint64_t>(static_cast<uint32_t>(c.x)) << 32);
+    return fmix64(xy ^ fmix64(zb + 0x9E3779B97F4A7C15ULL));
+}
+
+__device__ __forceinline__ bool same_key(int4 a, int4 b) {
+    return a.x == b.x && a.y == b.y && a.z == b.z && a.w == b.w;
+}
+
+// Smallest inserted row whose key equals c, or -1.
+__device__ __forceinline__ int32_t hash_find(const uint64_t *__restrict__ slots, uint64_t mask,
+                                             const int4 *__restrict__ keys, int4 c) {
+    const uint64_t h = key_hash(c);
+    const uint32_t tag = static_cast<uint32_t>(h >> 32);
+    uint64_t pos = h & mask;
+    for (uint64_t probe = 0; probe <= mask; ++probe) {
+        const uint64_t cur = slots[pos];
+        if (cur == kEmpty) return -1;
+        if (static_cast<uint32_t>(cur >> 32) == tag) {
+            const int32_t row = static_cast<int32_t>(static_cast<uint32_t>(cur));
+            if (same_key(keys[row], c)) return row;
+        }
+        pos = (pos + 1) & mask;
+    }
+    return -1;
+}
+
+__global__ void __launch_bounds__(kThreads)
+hash_insert_kernel(const int4 *__restrict__ keys, int32_t n, uint64_t *slots, uint64_t mask,
+                   int32_t *flags) {
+    const int32_t i = blockIdx.x * kThreads + threadIdx.x;
+    if (i >= n) return;
+    const int4 c = keys[i];
+    const uint64_t h = key_hash(c);
+    const uint64_t tag = h >> 32;
+    const uint64_t mine = (tag << 32) | static_cast<uint32_t>(i);
+    uint64_t pos = h & mask;
+    for (uint64_t probe = 0; probe <= mask; ++probe) {
+        uint64_t cur = slots[pos];
+        if (cur == kEmpty) {
+            cur = atomicCAS(reinterpret_cast<unsigned long long *>(&slots[pos]), kEmpty, mine);
+            if (cur == kEmpty) return;
+        }
+        // Every row ever stored in this slot carries the same key, so any
+        // (possibly stale) row half identifies the key correctly.
+        if ((cur >> 32) == tag &&
+            same_key(keys[static_cast<uint32_t>(cur)], c)) {
+            atomicMin(reinterpret_cast<unsigned long long *>(&slots[pos]),
+                      static_cast<unsigned long long>(mine));
+            flags[kFlagDuplicate] = 1;
+            return;
+        }
+        pos = (pos + 1) & mask;
+    }
+    flags[kFlagOverflow] = 1;
+}
+
+__device__ __forceinline__ bool add_fits(int32_t v, int32_t d, int32_t *out) {
+    const int64_t s = static_cast<int64_t>(v) + d;
+    *out = static_cast<int32_t>(s);
+    return s >= INT32_MIN && s <= INT32_MAX;
+}
+
+// One thread per (voxel, offset): kmap[i*27+o] = first row at coords[i]+d(o).
+__global__ void __launch_bounds__(kThreads)
+kmap_lookup_kernel(const int4 *__restrict__ coords, int32_t n, const uint64_t *__restrict__ slots,
+                   uint64_t mask, const int32_t *__restrict__ flags, int32_t missing,
+                   int32_t *__restrict__ kmap) {
+    const int32_t g = blockIdx.x * kThreads + threadIdx.x;
+    if (g >= n * 27) return;
+    const int32_t i = g / 27;
+    const int32_t o = g - i * 27;
+    const int4 c = coords[i];
+    int32_t result = missing;
+    // Later duplicates of a coordinate keep an all-missing row
+    // (sparse_ops.cpp:129-139 only visits each key's first row).
+    const bool owner = flags[kFlagDuplicate] == 0 || hash_find(slots, mask, coords, c) == i;
+    int4 q = c;
+    if (owner && add_fits(c.y, o / 9 - 1, &q.y) && add_fits(c.z, (o / 3) % 3 - 1, &q.z) &&
+        add_fits(c.w, o % 3 - 1, &q.w)) {
+        const int32_t r = hash_find(slots, mask, coords, q);
+        if (r >= 0) result = r;
+    }
+    kmap[g] = result;
+}
+
+// ---- subdivide ------------------------------------------------------------
+// For child slot ch (bits bx,by,bz) and offset o, the neighbour lives in the
+// parent at parent-offset kAdjOffset and at child slot kAdjChild
+// (sparse_ops.cpp:346-365): coordinate bits+d in {-1,0,1,2} splits into a
+// parent step floor((bits+d)/2) and a child bit (bits+d) mod 2.
+__device__ __forceinline__ void adjacent(int ch, int o, int *parent_offset, int *child_slot) {
+    const int b[3] = {ch >> 2, (ch >> 1) & 1, ch & 1};
+    const int d[3] = {o / 9 - 1, (o / 3) % 3 - 1, o % 3 - 1};
+    int po = 0, cs = 0;
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        const int v = b[a] + d[a];
+        const int step = v < 0 ? -1 : (v > 1 ? 1 : 0);
+        po = po * 3 + (step + 1);
+        cs = cs * 2 + (v - 2 * step);
+    }
+    *parent_offset = po;
+    *child_slot = cs;
+}
+
+__global__ void __launch_bounds__(kThreads)
+child_coords_kernel(const int4 *__restrict__ parents, int32_t p, int4 *__restrict__ children) {
+    const int32_t r = blockIdx.x * kThreads + threadIdx.x;
+    if (r >= p * 8) return;
+    const int4 c = parents[r >> 3];
+    const int ch = r & 7;
+    int4 out;
+    out.x = c.x;
+    out.y = static_cast<int32_t>(static_cast<uint32_t>(c.y) * 2u + static_cast<uint32_t>(ch >> 2));
+    out.z = static_cast<int32_t>(static_cast<uint32_t>(c.z) * 2u +
+                                 static_cast<uint32_t>((ch >> 1) & 1));
+    out.w = static_cast<int32_t>(static_cast<uint32_t>(c.w) * 2u + static_cast<uint32_t>(ch & 1));
+    children[r] = out;
+}
+
+// One thread per (child, offset): neighbour = parent_nbr*8 + child slot.
+__global__ void __launch_bounds__(kThreads)
+child_kmap_kernel(const int32_t *__restrict__ parent_kmap, int32_t p, int32_t *__restrict__ kmap) {
+    const int64_t g = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (g >= static_cast<int64_t>(p) * 8 * 27) return;
+    const int32_t r = static_cast<int32_t>(g / 27);
+    const int32_t o = static_cast<int32_t>(g - static_cast<int64_t>(r) * 27);
+    int po, cs;
+    adjacent(r & 7, o, &po, &cs);
+    const int32_t t = parent_kmap[static_cast<int64_t>(r >> 3) * 27 + po];
+    kmap[g] = t >= 0 ? t * 8 + cs : -1;
+}
+
+// ---- coarsen ---------------------------------------------------------------
+__global__ void __launch_bounds__(kThreads)
+coarse_keys_kernel(const int4 *__restrict__ coords, int32_t n, int4 *__restrict__ ckeys,
+                   int32_t *bbox) {
+    const int32_t i = blockIdx.x * kThreads + threadIdx.x;
+    int4 k = make_int4(INT32_MAX, INT32_MAX, INT32_MAX, INT32_MAX);
+    int4 kmax = make_int4(INT32_MIN, INT32_MIN, INT32_MIN, INT32_MIN);
+    if (i < n) {
+        const int4 c = coords[i];
+        // C++ integer division truncates toward zero (sparse_ops.cpp:63-64).
+        k = make_int4(c.x, c.y / 2, c.z / 2, c.w / 2);
+        ckeys[i] = k;
+        kmax = k;
+    }
+    int v[8] = {k.x, k.y, k.z, k.w, kmax.x, kmax.y, kmax.z, kmax.w};
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+#pragma unroll
+        for (int a = 0; a < 4; ++a) v[a] = min(v[a], __shfl_xor(v[a], d, 64));
+#pragma unroll
+        for (int a = 4; a < 8; ++a) v[a] = max(v[a], __shfl_xor(v[a], d, 64));
+    }
+    if ((threadIdx.x & 63) == 0) {
+#pragma unroll
+        for (int a = 0; a < 4; ++a) atomicMin(&bbox[a], v[a]);
+#pragma unroll
+        for (int a = 4; a < 8; ++a) atomicMax(&bbox[a], v[a]);
+    }
+}
+
+struct DenseGrid {
+    int32_t lo[4];
+    int64_t ext[4];
+};
+
+__device__ __forceinline__ int64_t dense_cell(const DenseGrid &g, int4 k) {
+    return ((static_cast<int64_t>(k.x) - g.lo[0]) * g.ext[1] + (static_cast<int64_t>(k.y) - g.lo[1])) *
+               g.ext[2] * g.ext[3] +
+           (static_cast<int64_t>(k.z) - g.lo[2]) * g.ext[3] + (static_cast<int64_t>(k.w) - g.lo[3]);
+}
+
+// Dense path: every occupied coarse cell is marked; the exclusive scan over
+// the row-major (b, x, y, z) cell index is then the lexicographic rank.
+__global__ void __launch_bounds__(kThreads)
+dense_mark_kernel(const int4 *__restrict__ ckeys, int32_t n, DenseGrid g, int32_t *mark) {
+    const int32_t i = blockIdx.x * kThreads + threadIdx.x;
+    if (i < n) mark[dense_cell(g, ckeys[i])] = 1;
+}
+
+__global__ void __launch_bounds__(kThreads)
+dense_assign_kernel(const int4 *__restrict__ ckeys, int32_t n, DenseGrid g,
+                    const int32_t *__restrict__ rank, int32_t *__restrict__ f2c,
+                    int4 *__restrict__ coarse_coords) {
+    const int32_t i = blockIdx.x * kThreads + threadIdx.x;
+    if (i >= n) return;
+    const int4 k = ckeys[i];
+    const int32_t r = rank[dense_cell(g, k)];
+    f2c[i] = r;
+    coarse_coords[r] = k;  // every writer of row r stores the same key
+}
+
+// General path (bounding box too large for a dense grid): representatives
+// (the smallest fine row of each coarse key) are ranked by counting smaller
+// keys, O(nc^2) comparisons tiled through LDS.
+__global__ void __launch_bounds__(kThreads)
+rep_flag_kernel(const int4 *__restrict__ ckeys, int32_t n, const uint64_t *__restrict__ slots,
+                uint64_t mask, int32_t *__restrict__ rep, int32_t *__restrict__ is_rep) {
+    const int32_t i = blockIdx.x * kThreads + threadIdx.x;
+    if (i >= n) return;
+    const int32_t r = hash_find(slots, mask, ckeys, ckeys[i]);
+    rep[i] = r;
+    is_rep[i] = r == i ? 1 : 0;
+}
+
+__global__ void __launch_bounds__(kThreads)
+rep_compact_kernel(const int32_t *__restrict__ is_rep, const int32_t *__restrict__ pos, int32_t n,
+                   int32_t *__restrict__ reps) {
+    const int32_t i = blockIdx.x * kThreads + threadIdx.x;
+    if (i < n && is_rep[i]) reps[pos[i]] = i;
+}
+
+__device__ __forceinline__ bool key_less(int4 a, int4 b) {
+    if (a.x != b.x) return a.x < b.x;
+    if (a.y != b.y) return a.y < b.y;
+    if (a.z != b.z) return a.z < b.z;
+    return a.w < b.w;
+}
+
+__global__ void __launch_bounds__(kThreads)
+rank_count_kernel(const int4 *__restrict__ ckeys, const int32_t *__restrict__ reps, int32_t nc,
+                  int32_t *__restrict__ rank_of) {
+    __shared__ int4 tile[kThreads];
+    const int32_t u = blockIdx.x * kThreads + threadIdx.x;
+    const int4 mine = u < nc ? ckeys[reps[u]] : make_int4(0, 0, 0, 0);
+    int32_t rank = 0;
+    for (int32_t t0 = 0; t0 < nc; t0 += kThreads) {
+        const int32_t v = t0 + threadIdx.x;
+        __syncthreads();
+        if (v < nc) tile[threadIdx.x] = ckeys[reps[v]];
+        __syncthreads();
+        const int32_t m = min(kThreads, nc - t0);
+        for (int32_t j = 0; j < m; ++j) rank += key_less(tile[j], mine) ? 1 : 0;
+    }
+    if (u < nc) rank_of[u] = rank;
+}
+
+__global__ void __launch_bounds__(kThreads)
+general_assign_kernel(const int4 *__restrict__ ckeys, int32_t n, const int32_t *__restrict__ rep,
+                      const int32_t *__restrict__ pos, const int32_t *__restrict__ rank_of,
+                      int32_t *__restrict__ f2c, int4 *__restrict__ coarse_coords) {
+    const int32_t i = blockIdx.x * kThreads + threadIdx.x;
+    if (i >= n) return;
+    const int32_t r = rank_of[pos[rep[i]]];
+    f2c[i] = r;
+    if (rep[i] == i) coarse_coords[r] = ckeys[i];
+}
+
+// Children lists: counts -> offsets -> bucketed fine rows -> the 8 smallest
+// per coarse row in ascending order (sparse_ops.cpp:82-104).
+__global__ void __launch_bounds__(kThreads)
+child_count_kernel(const int32_t *__restrict__ f2c, int32_t n, int32_t *counts) {
+    const int32_t i = blockIdx.x * kThreads + threadIdx.x;
+    if (i < n) atomicAdd(&counts[f2c[i]], 1);
+}
+
+__global__ void __launch_bounds__(kThreads)
+child_bucket_kernel(const int32_t *__restrict__ f2c, int32_t n, const int32_t *__restrict__ start,
+                    int32_t *fill, int32_t *__restrict__ bucket) {
+    const int32_t i = blockIdx.x * kThreads + threadIdx.x;
+    if (i >= n) return;
+    const int32_t c = f2c[i];
+    bucket[start[c] + atomicAdd(&fill[c], 1)] = i;
+}
+
+__global__ void __launch_bounds__(kThreads)
+child_select_kernel(const int32_t *__restrict__ bucket, const int32_t *__restrict__ start,
+                    const int32_t *__restrict__ counts, int32_t nc, int32_t n,
+                    int32_t *__restrict__ children, float *__restrict__ inv_count) {
+    const int32_t c = blockIdx.x * kThreads + threadIdx.x;
+    if (c >= nc) return;
+    const int32_t s = start[c], k = counts[c];
+    int32_t prev = -1;
+    for (int j = 0; j < 8; ++j) {
+        // j-th smallest: the smallest entry greater than the previous pick
+        // (entries are distinct fine rows).
+        int32_t best = INT32_MAX;
+        for (int32_t t = 0; t < k; ++t) {
+            const int32_t v = bucket[s + t];
+            if (v > prev && v < best) best = v;
+        }
+        const bool have = j < k;
+        children[static_cast<int64_t>(c) * 8 + j] = have ? best : n;
+        if (have) prev = best;
+    }
+    inv_count[c] = 1.0f / static_cast<float>(k + 1);
+}
+
+unsigned blocks_for(int64_t items) { return static_cast<unsigned>((items + kThreads - 1) / kThreads); }
+
+uint64_t hash_capacity(int64_t n) {
+    uint64_t cap = 256;
+    while (cap < static_cast<uint64_t>(n) * 2) cap <<= 1;
+    return cap;
+}
+
+// Dense coarse grids up to this many cells use the scan path.
+uint64_t dense_cell_cap(int64_t n) {
+    const uint64_t a = uint64_t(1) << 21;
+    const uint64_t b = static_cast<uint64_t>(n) * 64;
+    return a > b ? a : b;
+}
+
+template <class W>
+void kmap_layout(W &w, int64_t n, uint64_t **slots, int32_t **flags) {
+    if constexpr (std::is_same_v<W, Carver>) {
+        *slots = w.template take<uint64_t>(hash_capacity(n));
+        *flags = w.template take<int32_t>(64);
+    } else {
+        w.template take<uint64_t>(hash_capacity(n));
+        w.template take<int32_t>(64);
+    }
+}
+
+// Hash insert + lookup, leaving the flags in the workspace.
+void run_kmap(const int4 *coords, int32_t n, int32_t missing, int32_t *kmap, uint64_t *slots,
+              int32_t *flags, hipStream_t stream) {
+    const uint64_t cap = hash_capacity(n);
+    fill_u64(slots, cap, kEmpty, stream);
+    fill_u32(reinterpret_cast<uint32_t *>(flags), 64, 0, stream);
+    hash_insert_kernel<<<blocks_for(n), kThreads, 0, stream>>>(coords, n, slots, cap - 1, flags);
+    launch_check("hash_insert");
+    kmap_lookup_kernel<<<blocks_for(static_cast<int64_t>(n) * 27), kThreads, 0, stream>>>(
+        coords, n, slots, cap - 1, flags, missing, kmap);
+    launch_check("kmap_lookup");
+}
+
+void check_coords(const int32_t *coords, int64_t n) {
+    require(coords != nullptr, "coords is NULL");
+    require(aligned(coords, 16), "coords must be 16-byte aligned");
+    require(n > 0, "voxel count must be positive");
+    require(n <= INT32_MAX / 27, "voxel count exceeds INT32_MAX / 27");
+}
+
+}  // namespace
+}  // namespace s3dx
+
+namespace s3dx {
+namespace {
+struct SubdivideLayout {
+    uint64_t *slots;
+    int32_t *flags;
+    int32_t *parent_kmap;
+};
+template <class W>
+void subdivide_layout(W &w, int64_t p, SubdivideLayout *l) {
+    if constexpr (std::is_same_v<W, Carver>) {
+        kmap_layout(w, p, &l->slots, &l->flags);
+        l->parent_kmap = w.template take<int32_t>(static_cast<uint64_t>(p) * 27);
+    } else {
+        kmap_layout(w, p, nullptr, nullptr);
+        w.template take<int32_t>(static_cast<uint64_t>(p) * 27);
+    }
+}
+}  // namespace
+namespace {
+struct CoarsenLayout {
+    int4 *ckeys;
+    uint64_t *slots;
+    int32_t *flags;
+    int32_t *bbox;
+    int32_t *totals;
+    int32_t *a, *b, *c, *d;  // n-sized scratch
+    int32_t *counts, *start, *fill, *bucket;
+    int32_t *dense_mark, *dense_rank;
+    void *scan_ws;
+};
+template <class W>
+void coarsen_layout(W &w, int64_t n, CoarsenLayout *l) {
+    const uint64_t un = static_cast<uint64_t>(n);
+    const uint64_t cells = dense_cell_cap(n);
+    const uint64_t scan_items = cells > un ? cells : un;
+    if constexpr (std::is_same_v<W, Carver>) {
+        l->ckeys = w.template take<int4>(un);
+        kmap_layout(w, n, &l->slots, &l->flags);
+        l->bbox = w.template take<int32_t>(8);
+        l->totals = w.template take<int32_t>(8);
+        l->a = w.template take<int32_t>(un);
+        l->b = w.template take<int32_t>(un);
+        l->c = w.template take<int32_t>(un);
+        l->d = w.template take<int32_t>(un);
+        l->counts = w.template take<int32_t>(un);
+        l->start = w.template take<int32_t>(un);
+        l->fill = w.template take<int32_t>(un);
+        l->bucket = w.template take<int32_t>(un);
+        l->dense_mark = w.template take<int32_t>(cells);
+        l->dense_rank = w.template take<int32_t>(cells);
+        l->scan_ws = w.template take<char>(scan_workspace_bytes(static_cast<int64_t>(scan_items)));
+    } else {
+        w.template take<int4>(un);
+        kmap_layout(w, n, nullptr, nullptr);
+        w.template take<int32_t>(8);
+        w.template take<int32_t>(8);
+        for (int k = 0; k < 8; ++k) w.template take<int32_t>(un);
+        w.template take<int32_t>(cells);
+        w.template take<int32_t>(cells);
+        w.template take<char>(scan_workspace_bytes(static_cast<int64_t>(scan_items)));
+    }
+}
+}  // namespace
+}  // namespace s3dx
+
+using namespace s3dx;
+
+extern "C" {
+
+S3DX_API s3dx_status s3dx_kmap_workspace_size(int64_t n, uint64_t *bytes, char *error,
+                                              uint64_t error_capacity) {
+    return boundary(error, error_capacity, [&] {
+        require(bytes != nullptr, "bytes is NULL");
+        require(n > 0 && n <= INT32_MAX / 27, "voxel count out of range");
+        Sizer s;
+        kmap_layout(s, n, nullptr, nullptr);
+        *bytes = s.used;
+    });
+}
+
+S3DX_API s3dx_status s3dx_kmap_subm3(const int32_t *coords, int64_t n, int32_t missing_value,
+                                     int32_t *kmap, void *workspace, uint64_t workspace_bytes,
+                                     s3dx_stream stream, char *error, uint64_t error_capacity) {
+    return boundary(error, error_capacity, [&] {
+        check_coords(coords, n);
+        require(kmap != nullptr, "kmap is NULL");
+        require(workspace != nullptr, "workspace is NULL");
+        Carver w(workspace, workspace_bytes);
+        uint64_t *slots;
+        int32_t *flags;
+        kmap_layout(w, n, &slots, &flags);
+        run_kmap(reinterpret_cast<const int4 *>(coords), static_cast<int32_t>(n), missing_value,
+                 kmap, slots, flags, as_stream(stream));
+    });
+}
+
+
+S3DX_API s3dx_status s3dx_subdivide2_workspace_size(int64_t parent_count, uint64_t *bytes,
+                                                    char *error, uint64_t error_capacity) {
+    return boundary(error, error_capacity, [&] {
+        require(bytes != nullptr, "bytes is NULL");
+        require(parent_count > 0 && parent_count <= INT32_MAX / 27,
+                "parent count out of range");
+        Sizer s;
+        subdivide_layout(s, parent_count, nullptr);
+        *bytes = s.used;
+    });
+}
+
+S3DX_API s3dx_status s3dx_subdivide2(const int32_t *parent_coords, int64_t parent_count,
+                                     int32_t *child_coords, int32_t *child_kmap, void *workspace,
+                                     uint64_t workspace_bytes, s3dx_stream stream, char *error,
+                                     uint64_t error_capacity) {
+    return boundary(error, error_capacity, [&] {
+        // sparse_ops.cpp:273 rejects count <= 0 and count > INT32_MAX / 8; the
+        // child kmap additionally needs 8 * 27 * count to index in int32.
+        require(parent_coords != nullptr, "parent_coords is NULL");
+        require(parent_count > 0, "parent count must be positive");
+        require(parent_count <= INT32_MAX / 8, "parent count exceeds INT32_MAX / 8");
+        require(parent_count <= INT32_MAX / 27, "parent count exceeds INT32_MAX / 27");
+        require(child_coords != nullptr, "child_coords is NULL");
+        require(aligned(parent_coords, 16) && aligned(child_coords, 16),
+                "coordinates must be 16-byte aligned");
+        require(workspace != nullptr, "workspace is NULL");
+        const hipStream_t s = as_stream(stream);
+        const int32_t p = static_cast<int32_t>(parent_count);
+        Carver w(workspace, workspace_bytes);
+        SubdivideLayout l;
+        subdivide_layout(w, parent_count, &l);
+        run_kmap(reinterpret_cast<const int4 *>(parent_coords), p, -1, l.parent_kmap, l.slots,
+                 l.flags, s);
+        child_coords_kernel<<<blocks_for(static_cast<int64_t>(p) * 8), kThreads, 0, s>>>(
+            reinterpret_cast<const int4 *>(parent_coords), p, reinterpret_cast<int4 *>(child_coords));
+        launch_check("child_coords");
+        if (child_kmap) {
+            child_kmap_kernel<<<blocks_for(static_cast<int64_t>(p) * 8 * 27), kThreads, 0, s>>>(
+                l.parent_kmap, p, child_kmap);
+            launch_check("child_kmap");
+        }
+        int32_t flags[2] = {0, 0};
+        hip_check(hipMemcpyAsync(flags, l.flags, sizeof(flags), hipMemcpyDeviceToHost, s),
+                  "hipMemcpyAsync flags");
+        hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
+        require(flags[kFlagDuplicate] == 0, "duplicate parent coordinates");
+        if (flags[kFlagOverflow]) throw std::runtime_error("hash table overflow");
+    });
+}
+
+
+S3DX_API s3dx_status s3dx_coarsen2_workspace_size(int64_t n, uint64_t *bytes, char *error,
+                                                  uint64_t error_capacity) {
+    return boundary(error, error_capacity, [&] {
+        require(bytes != nullptr, "bytes is NULL");
+        require(n > 0 && n <= INT32_MAX / 27, "voxel count out of range");
+        Sizer s;
+        coarsen_layout(s, n, nullptr);
+        *bytes = s.used;
+    });
+}
+
+S3DX_API s3dx_status s3dx_coarsen2(const int32_t *coords, int64_t n, int32_t *coarse_coords,
+                                   int32_t *fine_to_coarse, int32_t *coarse_children,
+                                   float *coarse_inv_count, int64_t *nc_out, void *workspace,
+                                   uint64_t workspace_bytes, s3dx_stream stream, char *error,
+                                   uint64_t error_capacity) {
+    return boundary(error, error_capacity, [&] {
+        check_coords(coords, n);
+        require(coarse_coords && fine_to_coarse && coarse_children && coarse_inv_count && nc_out,
+                "NULL output");
+        require(aligned(coarse_coords, 16), "coarse_coords must be 16-byte aligned");
+        require(workspace != nullptr, "workspace is NULL");
+        const hipStream_t s = as_stream(stream);
+        const int32_t ni = static_cast<int32_t>(n);
+        Carver w(workspace, workspace_bytes);
+        CoarsenLayout l;
+        coarsen_layout(w, n, &l);
+        const int4 *c4 = reinterpret_cast<const int4 *>(coords);
+        int4 *cc4 = reinterpret_cast<int4 *>(coarse_coords);
+
+        // 1. coarse keys + their bounding box.
+        fill_u32(reinterpret_cast<uint32_t *>(l.bbox), 4, static_cast<uint32_t>(INT32_MAX), s);
+        fill_u32(reinterpret_cast<uint32_t *>(l.bbox) + 4, 4, static_cast<uint32_t>(INT32_MIN), s);
+        coarse_keys_kernel<<<blocks_for(ni), kThreads, 0, s>>>(c4, ni, l.ckeys, l.bbox);
+        launch_check("coarse_keys");
+        int32_t bbox[8];
+        hip_check(hipMemcpyAsync(bbox, l.bbox, sizeof(bbox), hipMemcpyDeviceToHost, s),
+                  "hipMemcpyAsync bbox");
+        hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
+
+        DenseGrid g;
+        bool dense = true;
+        uint64_t cells = 1;
+        for (int a = 0; a < 4; ++a) {
+            g.lo[a] = bbox[a];
+            g.ext[a] = static_cast<int64_t>(bbox[4 + a]) - bbox[a] + 1;
+            const uint64_t e = static_cast<uint64_t>(g.ext[a]);
+            if (cells > dense_cell_cap(n) / e) dense = false;
+            else cells *= e;
+        }
+        dense = dense && cells <= dense_cell_cap(n);
+
+        int32_t nc = 0;
+        if (dense) {
+            // 2a. mark occupied cells, scan -> lexicographic rank.
+            fill_u32(reinterpret_cast<uint32_t *>(l.dense_mark), cells, 0, s);
+            dense_mark_kernel<<<blocks_for(ni), kThreads, 0, s>>>(l.ckeys, ni, g, l.dense_mark);
+            launch_check("dense_mark");
+            exclusive_scan_i32(l.dense_mark, l.dense_rank, static_cast<int64_t>(cells), l.totals,
+                               l.scan_ws, s);
+            dense_assign_kernel<<<blocks_for(ni), kThreads, 0, s>>>(l.ckeys, ni, g, l.dense_rank,
+                                                                    fine_to_coarse, cc4);
+            launch_check("dense_assign");
+        } else {
+            // 2b. dedupe through the hash, rank representatives by counting.
+            const uint64_t cap = hash_capacity(n);
+            fill_u64(l.slots, cap, kEmpty, s);
+            fill_u32(reinterpret_cast<uint32_t *>(l.flags), 64, 0, s);
+            hash_insert_kernel<<<blocks_for(ni), kThreads, 0, s>>>(l.ckeys, ni, l.slots, cap - 1,
+                                                                   l.flags);
+            launch_check("coarse_insert");
+            int32_t *rep = l.a, *is_rep = l.b, *pos = l.c, *rank_of = l.d;
+            rep_flag_kernel<<<blocks_for(ni), kThreads, 0, s>>>(l.ckeys, ni, l.slots, cap - 1, rep,
+                                                                is_rep);
+            launch_check("rep_flag");
+            exclusive_scan_i32(is_rep, pos, ni, l.totals, l.scan_ws, s);
+            int32_t *reps = l.bucket;  // free until the children pass
+            rep_compact_kernel<<<blocks_for(ni), kThreads, 0, s>>>(is_rep, pos, ni, reps);
+            launch_check("rep_compact");
+            hip_check(hipMemcpyAsync(&nc, l.totals, sizeof(nc), hipMemcpyDeviceToHost, s),
+                      "hipMemcpyAsync nc");
+            hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
+            rank_count_kernel<<<blocks_for(nc), kThreads, 0, s>>>(l.ckeys, reps, nc, rank_of);
+            launch_check("rank_count");
+            general_assign_kernel<<<blocks_for(ni), kThreads, 0, s>>>(l.ckeys, ni, rep, pos, rank_of,
+                                                                      fine_to_coarse, cc4);
+            launch_check("general_assign");
+        }
+        hip_check(hipMemcpyAsync(&nc, l.totals, sizeof(nc), hipMemcpyDeviceToHost, s),
+                  "hipMemcpyAsync nc");
+        hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
+        require(nc > 0 && nc <= ni, "coarse row count out of range");
+
+        // 3. children (8 smallest fine rows per coarse row) and 1/(count+1).
+        fill_u32(reinterpret_cast<uint32_t *>(l.counts), static_cast<uint64_t>(nc), 0, s);
+        fill_u32(reinterpret_cast<uint32_t *>(l.fill), static_cast<uint64_t>(nc), 0, s);
+        child_count_kernel<<<blocks_for(ni), kThreads, 0, s>>>(fine_to_coarse, ni, l.counts);
+        launch_check("child_count");
+        exclusive_scan_i32(l.counts, l.start, nc, l.totals + 1, l.scan_ws, s);
+        child_bucket_kernel<<<blocks_for(ni), kThreads, 0, s>>>(fine_to_coarse, ni, l.start, l.fill,
+                                                                l.bucket);
+        launch_check("child_bucket");
+        child_select_kernel<<<blocks_for(nc), kThreads, 0, s>>>(l.bucket, l.start, l.counts, nc, ni,
+                                                                coarse_children, coarse_inv_count);
+        launch_check("child_select");
+        *nc_out = nc;
+    });
+}
+
+}  // extern "C"

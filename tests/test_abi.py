@@ -1,0 +1,108 @@
+"""The C ABI library loads, exports every declared symbol, and rejects bad
+arguments on the host (no device needed)."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "s3dx_sparse.h"
+
+
+def declared():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"S3DX_API\s+[\w\s\*]+?\b(s3dx_\w+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported(s3dx):
+    names = declared()
+    assert len(names) >= 30
+    lib = s3dx.lib()
+    for name in names:
+        assert hasattr(lib, name), name
+        assert name in s3dx.SIGNATURES, f"{name} missing from the Python binding"
+    assert set(s3dx.SIGNATURES) == set(names)
+
+
+def test_abi_version(s3dx):
+    assert s3dx.lib().s3dx_abi_version() == 1
+
+
+def _status(s3dx, name, *args, cap=256):
+    buf = C.create_string_buffer(cap)
+    st = getattr(s3dx.lib(), name)(*args, buf, cap)
+    return st, buf.value.decode()
+
+
+def test_error_buffer_contract(s3dx):
+    lib = s3dx.lib()
+    b = C.c_uint64(0)
+    # NULL buffer with nonzero capacity is itself invalid
+    assert lib.s3dx_kmap_workspace_size(100, C.byref(b), None, 16) == s3dx.INVALID_ARGUMENT
+    # NULL,0 discards diagnostics
+    assert lib.s3dx_kmap_workspace_size(100, C.byref(b), None, 0) == s3dx.OK
+    # success clears the buffer; failure NUL-terminates a truncated message
+    buf = C.create_string_buffer(b"stale text", 32)
+    assert lib.s3dx_kmap_workspace_size(100, C.byref(b), buf, 32) == s3dx.OK and buf.value == b""
+    small = C.create_string_buffer(8)
+    assert lib.s3dx_kmap_workspace_size(0, C.byref(b), small, 8) == s3dx.INVALID_ARGUMENT
+    assert len(small.value) == 7
+
+
+def test_workspace_sizes_grow(s3dx):
+    a = s3dx.kmap_workspace_size(1000)
+    b = s3dx.kmap_workspace_size(100000)
+    assert 0 < a < b
+    assert b >= 2 * 100000 * 8  # hash slots at load <= 1/2
+
+
+@pytest.mark.parametrize("call", [
+    ("s3dx_kmap_workspace_size", 0),
+    ("s3dx_kmap_workspace_size", 2**31 // 27 + 1),
+    ("s3dx_subdivide2_workspace_size", 0),
+    ("s3dx_subdivide2_workspace_size", 2**31 // 27 + 1),
+    ("s3dx_coarsen2_workspace_size", -5),
+])
+def test_size_queries_reject_bad_counts(s3dx, call):
+    b = C.c_uint64(0)
+    st, msg = _status(s3dx, call[0], C.c_int64(call[1]), C.byref(b))
+    assert st == s3dx.INVALID_ARGUMENT and msg
+
+
+def test_kmap_rejects_bad_pointers(s3dx):
+    st, msg = _status(s3dx, "s3dx_kmap_subm3", None, 10, 10, None, None, 0, None)
+    assert st == s3dx.INVALID_ARGUMENT and "coords" in msg
+    st, msg = _status(s3dx, "s3dx_kmap_subm3", C.c_void_p(0x1004), 10, 10, C.c_void_p(0x2000),
+                      C.c_void_p(0x3000), 1 << 20, None)
+    assert st == s3dx.INVALID_ARGUMENT and "aligned" in msg
+    st, msg = _status(s3dx, "s3dx_kmap_subm3", C.c_void_p(0x1000), 10, 10, C.c_void_p(0x2000),
+                      C.c_void_p(0x3000), 64, None)
+    assert st == s3dx.INVALID_ARGUMENT and "workspace" in msg
+
+
+def test_subdivide_rejects_reference_limits(s3dx):
+    # sparse_ops.cpp:273: count <= 0 and count > INT32_MAX / 8 are rejected
+    for p in (0, -1, 2**31 // 8 + 1):
+        st, msg = _status(s3dx, "s3dx_subdivide2", C.c_void_p(0x1000), C.c_int64(p), C.c_void_p(0x2000),
+                          None, C.c_void_p(0x3000), 1 << 20, None)
+        assert st == s3dx.INVALID_ARGUMENT, (p, msg)
+
+
+def test_conv_create_validation(s3dx):
+    p = C.c_void_p()
+    for args in [(0, 8, 27, 0), (8, 8, 5, 0), (8, 8, 27, 7), (8, -1, 1, 1)]:
+        st, msg = _status(s3dx, "s3dx_conv_create", *args, C.byref(p))
+        assert st == s3dx.INVALID_ARGUMENT and msg, args
+    st, _ = _status(s3dx, "s3dx_conv_create", 128, 128, 27, 1, C.byref(p))
+    assert st == s3dx.OK and p.value
+    st, msg = _status(s3dx, "s3dx_conv_run", p, C.c_void_p(0x1000), 10, C.c_void_p(0x2000), 10,
+                      None, C.c_void_p(0x3000), 1, None)
+    assert st == s3dx.INVALID_ARGUMENT and "weights" in msg
+    s3dx.lib().s3dx_conv_free(p)
+
+
+def test_missing_library_fails_loudly(s3dx, monkeypatch, tmp_path):
+    monkeypatch.setattr(s3dx, "_lib", None)
+    monkeypatch.setattr(s3dx, "LIB_PATH", tmp_path / "absent.so")
+    with pytest.raises(RuntimeError, match="not built"):
+        s3dx.lib()

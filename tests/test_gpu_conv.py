@@ -1,0 +1,187 @@
+"""GPU sparse convolution through the C ABI against the oracle.
+
+Tolerances (rel-L2): FP32 <= 1e-5; BF16 <= 1e-2 against the FP32 oracle run
+on the BF16-rounded inputs and weights."""
+import numpy as np
+import pytest
+
+from helpers import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+TOL = {0: 1e-5, 1: 1e-2}
+
+
+def to_dev(s3dx, x, dtype):
+    W = s3dx.workloads
+    if dtype == s3dx.BF16:
+        return s3dx.DeviceArray.from_host(W.f32_to_bf16_bits(x))
+    return s3dx.DeviceArray.from_host(np.ascontiguousarray(x, np.float32))
+
+
+def from_dev(s3dx, d, dtype):
+    h = d.download()
+    return s3dx.workloads.bf16_bits_to_f32(h).reshape(h.shape) if dtype == s3dx.BF16 else h
+
+
+def rnd(s3dx, a, dtype):
+    return s3dx.workloads.round_bf16(a) if dtype == s3dx.BF16 and a is not None else a
+
+
+def gpu_conv(s3dx, x, kmap, n_in, w, layout, bias, dtype, cout, kvol=27, n_out=None,
+             y_dtype=None, residual=None, setup=None):
+    cin = x.shape[1]
+    conv = s3dx.SparseConv(cin, cout, kvol, dtype).set_weights(w, layout, bias)
+    if setup:
+        setup(conv)
+    n_out = n_out if n_out is not None else (kmap.shape[0] if kmap is not None else x.shape[0])
+    yd = dtype if y_dtype is None else y_dtype
+    y = s3dx.DeviceArray((n_out, cout), np.uint16 if yd == s3dx.BF16 else np.float32)
+    dk = s3dx.DeviceArray.from_host(kmap) if kmap is not None else None
+    dr = to_dev(s3dx, residual, yd) if residual is not None else None
+    conv.run(to_dev(s3dx, x, dtype), n_in, dk, n_out, y, yd, dr)
+    return from_dev(s3dx, y, yd)
+
+
+@pytest.mark.parametrize("dtype", [0, 1])
+@pytest.mark.parametrize("cin,cout", [(32, 32), (64, 64), (128, 96), (128, 128), (64, 160),
+                                      (96, 192), (256, 256), (16, 32)])
+def test_linear_layer_lane_layout(s3dx, W, dtype, cin, cout):
+    # kvol 1, no map: a plain GEMM, so any A/B/D lane-layout mistake shows.
+    n = 517
+    print(f"linear dtype={dtype} cin={cin} cout={cout}", flush=True)
+    x = W.normal_f32(3, 1, (n, cin))
+    w = W.normal_f32(3, 2, (cout, 1, cin), 1.0 / np.sqrt(cin))
+    b = W.normal_f32(3, 3, (cout,))
+    got = gpu_conv(s3dx, x, None, n, w, s3dx.WEIGHT_SLAT, b, dtype, cout, kvol=1)
+    xr, wr = rnd(s3dx, x, dtype), rnd(s3dx, w, dtype)
+    ref = xr.astype(np.float64) @ wr[:, 0, :].T.astype(np.float64) + b
+    assert rel_l2(got, ref) <= TOL[dtype] / (10 if dtype == 0 else 1)
+
+
+@pytest.mark.parametrize("dtype", [0, 1])
+@pytest.mark.parametrize("cin,cout", [(64, 64), (128, 128), (32, 96), (192, 192), (96, 96),
+                                      (256, 256), (8, 128), (20, 36), (128, 101)])
+def test_subm_conv_matches_oracle(s3dx, O, W, dtype, cin, cout):
+    coords = W.shells_union(1)[:3000]
+    n = coords.shape[0]
+    print(f"subm conv dtype={dtype} cin={cin} cout={cout} n={n}", flush=True)
+    kmap = O.kmap_subm3(coords, n)
+    x = W.normal_f32(4, 1, (n, cin))
+    w = W.conv_weight(4, 2, cin, cout)
+    b = W.normal_f32(4, 3, (cout,), 0.5)
+    got = gpu_conv(s3dx, x, kmap, n, w, s3dx.WEIGHT_SLAT, b, dtype, cout)
+    ref = O.conv(rnd(s3dx, x, dtype), kmap, n, rnd(s3dx, w, dtype), 0, cout, b)
+    assert rel_l2(got, ref) <= TOL[dtype]
+
+
+def test_config1_fp32_conv(s3dx, O, W):
+    coords = W.shell_64()
+    n = coords.shape[0]
+    kmap = O.kmap_subm3(coords, n)
+    x = W.normal_f32(0, 1, (n, 64))
+    w = W.conv_weight(0, 2, 64, 64)
+    b = np.zeros(64, np.float32)
+    got = gpu_conv(s3dx, x, kmap, n, w, s3dx.WEIGHT_SLAT, b, s3dx.F32, 64)
+    ref = O.conv(x, kmap, n, w, 0, 64, b)
+    assert rel_l2(got, ref) <= 1e-5
+
+
+@pytest.mark.parametrize("dtype", [0, 1])
+def test_mesh_layout_minus_one_sentinel(s3dx, O, W, dtype):
+    coords = W.shell_64(res=32, centre=(16.0, 16.0, 16.0), radius=9.0)
+    n = coords.shape[0]
+    kmap = O.kmap_subm3(coords, -1)
+    cin, cout = 96, 192
+    x = W.normal_f32(5, 1, (n, cin))
+    w = W.conv_weight(5, 2, cin, cout, layout="mesh")
+    b = W.normal_f32(5, 3, (cout,))
+    got = gpu_conv(s3dx, x, kmap, n, w, s3dx.WEIGHT_MESH, b, dtype, cout)
+    ref = O.conv(rnd(s3dx, x, dtype), kmap, n, rnd(s3dx, w, dtype), 1, cout, b)
+    assert rel_l2(got, ref) <= TOL[dtype]
+
+
+@pytest.mark.parametrize("dtype", [0, 1])
+@pytest.mark.parametrize("cin,cout", [(64, 64), (24, 40)])
+def test_gather_parent_slot_offset_and_input_affine(s3dx, O, W, dtype, cin, cout):
+    # conv over subdivided children whose features are silu(GN-affine(parent))
+    # repeated x8 plus a per-slot offset, without materialising the repeat.
+    parents = W.shell_64(res=24, centre=(12.0, 12.0, 12.0), radius=7.0)
+    p = parents.shape[0]
+    child, kmap = O.subdivide2(parents)
+    n = 8 * p
+    print(f"gather-parent dtype={dtype} p={p} cin={cin}", flush=True)
+    xp = W.normal_f32(6, 1, (p, cin))
+    slot = W.normal_f32(6, 2, (8, cin), 0.02)
+    scale = W.normal_f32(6, 3, (cin,), 0.5) + 1.0
+    shift = W.normal_f32(6, 4, (cin,), 0.5)
+    w = W.conv_weight(6, 5, cin, cout, layout="mesh")
+    b = W.normal_f32(6, 6, (cout,))
+    ds, dh = s3dx.DeviceArray.from_host(scale), s3dx.DeviceArray.from_host(shift)
+
+    def setup(conv):
+        conv.set_gather_parent(True, slot)
+        conv.set_input_affine_silu(ds, dh)
+
+    got = gpu_conv(s3dx, xp, kmap, p, w, s3dx.WEIGHT_MESH, b, dtype, cout, n_out=n, setup=setup)
+    xr = rnd(s3dx, xp, dtype)
+    xc = O.repeat_children(xr) + np.tile(slot, (p, 1))
+    act = O.silu(xc * scale + shift)
+    ref = O.conv(rnd(s3dx, act, dtype), kmap, n, rnd(s3dx, w, dtype), 1, cout, b)
+    assert rel_l2(got, ref) <= TOL[dtype] * (2 if dtype == 0 else 1)
+
+
+@pytest.mark.parametrize("dtype", [0, 1])
+@pytest.mark.parametrize("cout", [128, 160, 101])
+def test_layernorm_modulate_silu_residual_epilogue(s3dx, O, W, dtype, cout):
+    # cout 128: fused into the MFMA epilogue; 160 and 101: separate LN pass.
+    coords = W.shells_union(2)[:2500]
+    n = coords.shape[0]
+    print(f"ln epilogue dtype={dtype} cout={cout}", flush=True)
+    kmap = O.kmap_subm3(coords, n)
+    cin = 64
+    x = W.normal_f32(7, 1, (n, cin))
+    w = W.conv_weight(7, 2, cin, cout)
+    b = W.normal_f32(7, 3, (cout,))
+    lw, lb = W.normal_f32(7, 4, (cout,)), W.normal_f32(7, 5, (cout,))
+    ms, mh = W.normal_f32(7, 6, (cout,), 0.3), W.normal_f32(7, 7, (cout,), 0.3)
+    res = W.normal_f32(7, 8, (n, cout))
+
+    def setup(conv):
+        conv.set_layernorm(True, 1e-6, lw, lb, ms, mh)
+        conv.set_silu(True)
+
+    got = gpu_conv(s3dx, x, kmap, n, w, s3dx.WEIGHT_SLAT, b, dtype, cout, residual=res, setup=setup)
+    h = O.conv(rnd(s3dx, x, dtype), kmap, n, rnd(s3dx, w, dtype), 0, cout, b)
+    ref = O.silu(O.modulate(O.layernorm(h, 1e-6, lw, lb), ms, mh)) + rnd(s3dx, res, dtype)
+    assert rel_l2(got, ref) <= TOL[dtype] * (3 if dtype == 0 else 1)
+
+
+def test_output_dtype_cross(s3dx, O, W):
+    # bf16 arithmetic with fp32 output, and fp32 arithmetic with bf16 output.
+    coords = W.shells_union(0)[:1500]
+    n = coords.shape[0]
+    kmap = O.kmap_subm3(coords, n)
+    x = W.normal_f32(8, 1, (n, 128))
+    w = W.conv_weight(8, 2, 128, 128)
+    b = W.normal_f32(8, 3, (128,))
+    ref = O.conv(W.round_bf16(x), kmap, n, W.round_bf16(w), 0, 128, b)
+    got = gpu_conv(s3dx, x, kmap, n, w, 0, b, s3dx.BF16, 128, y_dtype=s3dx.F32)
+    assert rel_l2(got, ref) <= 1e-2
+    ref32 = O.conv(x, kmap, n, w, 0, 128, b)
+    got2 = gpu_conv(s3dx, x, kmap, n, w, 0, b, s3dx.F32, 128, y_dtype=s3dx.BF16)
+    assert rel_l2(got2, ref32) <= 1e-2
+
+
+def test_deterministic_and_empty_rows(s3dx, O, W):
+    coords = W.shells_union(0)[:2000]
+    n = coords.shape[0]
+    kmap = O.kmap_subm3(coords, n)
+    kmap[::7] = n  # rows with no neighbour at all (bias only)
+    x = W.normal_f32(9, 1, (n, 128))
+    w = W.conv_weight(9, 2, 128, 128)
+    b = W.normal_f32(9, 3, (128,))
+    a1 = gpu_conv(s3dx, x, kmap, n, w, 0, b, s3dx.BF16, 128)
+    a2 = gpu_conv(s3dx, x, kmap, n, w, 0, b, s3dx.BF16, 128)
+    assert np.array_equal(a1, a2)
+    assert np.allclose(a1[::7], W.round_bf16(np.broadcast_to(b, a1[::7].shape)), atol=0)

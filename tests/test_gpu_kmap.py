@@ -1,0 +1,125 @@
+"""GPU kernel maps, coarsen and subdivide through the C ABI: byte-identical to
+the oracle and to the reference golden tables."""
+import numpy as np
+import pytest
+
+from helpers import SMALL, large_sets, sha
+
+pytestmark = pytest.mark.gpu
+
+
+def gpu_kmap(s3dx, coords, missing):
+    n = coords.shape[0]
+    d = s3dx.DeviceArray.from_host(np.ascontiguousarray(coords, np.int32))
+    return s3dx.kmap_subm3(d, n, missing).download()
+
+
+@pytest.mark.parametrize("name", SMALL)
+def test_small_sets_match_reference(s3dx, O, golden, name):
+    arrays, manifest = golden
+    coords = arrays[f"{name}.coords"]
+    n = coords.shape[0]
+    print(f"kmap small set {name} n={n}", flush=True)
+    assert np.array_equal(gpu_kmap(s3dx, coords, n), arrays[f"{name}.conv_fine"])
+    assert np.array_equal(gpu_kmap(s3dx, coords, -1), O.kmap_subm3(coords, -1))
+    nc, cc, f2c, ch, inv = s3dx.coarsen2(s3dx.DeviceArray.from_host(coords), n)
+    assert nc == manifest[name]["nc"]
+    assert np.array_equal(f2c.download(), arrays[f"{name}.fine_to_coarse"])
+    ccoords = cc.download()[:nc]
+    assert np.array_equal(gpu_kmap(s3dx, ccoords, nc), arrays[f"{name}.conv_coarse"])
+    assert np.array_equal(ch.download()[: 8 * nc], arrays[f"{name}.coarse_children"])
+    assert np.array_equal(inv.download()[:nc].view(np.uint32),
+                          arrays[f"{name}.coarse_inv_count"].view(np.uint32))
+    tables = s3dx.MeshSubdivideTables()
+    ok = tables.build(coords)
+    if manifest[name]["subdivide"] == "rejected":
+        assert not ok
+    else:
+        assert ok
+        assert np.array_equal(tables.child_coords.download(), arrays[f"{name}.child_coords"])
+        assert np.array_equal(tables.neighbors.download(), arrays[f"{name}.neighbors"])
+
+
+def test_large_sets_match_reference_sha(s3dx, O, W, golden):
+    arrays, manifest = golden
+    for name, coords in large_sets(W, O, arrays).items():
+        m = manifest[name]
+        n = coords.shape[0]
+        print(f"kmap large set {name} n={n}", flush=True)
+        t = s3dx.SlatTables()
+        assert t.build(coords)
+        assert sha(t.conv_fine.download()) == m["conv_fine_sha256"], name
+        assert t.nc == m["nc"], name
+        assert sha(t.fine_to_coarse.download()) == m["fine_to_coarse_sha256"], name
+        assert sha(t.conv_coarse.download()) == m["conv_coarse_sha256"], name
+        assert sha(t.coarse_children.download()[: 8 * t.nc]) == m["coarse_children_sha256"], name
+        assert sha(t.coarse_inv_count.download()[: t.nc]) == m["coarse_inv_count_sha256"], name
+        mt = s3dx.MeshSubdivideTables()
+        assert mt.build(t.coords, n)
+        assert sha(mt.child_coords.download()) == m["subdivide"]["child_coords_sha256"], name
+        assert sha(mt.neighbors.download()) == m["subdivide"]["neighbors_sha256"], name
+
+
+def test_random_sets_with_duplicates_and_batches(s3dx, O):
+    rng = np.random.default_rng(2024)
+    for trial in range(12):
+        n = int(rng.integers(1, 5000))
+        span = int(rng.integers(2, 40))
+        c = rng.integers(-span, span, size=(n, 4)).astype(np.int32)
+        c[:, 0] = rng.integers(0, 3, size=n)
+        print(f"random trial {trial} n={n} span={span}", flush=True)
+        assert np.array_equal(gpu_kmap(s3dx, c, n), O.kmap_subm3(c, n))
+        nc, cc, f2c, ch, inv = s3dx.coarsen2(s3dx.DeviceArray.from_host(c), n)
+        onc, occ, of2c, och, oinv = O.coarsen2(c)
+        assert nc == onc
+        assert np.array_equal(cc.download()[:nc], occ)
+        assert np.array_equal(f2c.download(), of2c)
+        assert np.array_equal(ch.download()[: 8 * nc], och)
+        assert np.array_equal(inv.download()[:nc], oinv)
+
+
+def test_coarsen_general_path_wide_bbox(s3dx, O):
+    # Coordinates spread over ~2^30: the dense rank grid cannot hold the box,
+    # so the counting-rank path runs.
+    rng = np.random.default_rng(77)
+    n = 3000
+    c = rng.integers(-2**30, 2**30, size=(n, 4)).astype(np.int32)
+    c[:, 0] = rng.integers(0, 2, size=n)
+    c[n // 2:] = c[: n - n // 2]  # duplicates
+    print(f"coarsen wide bbox n={n}", flush=True)
+    nc, cc, f2c, ch, inv = s3dx.coarsen2(s3dx.DeviceArray.from_host(c), n)
+    onc, occ, of2c, och, oinv = O.coarsen2(c)
+    assert nc == onc
+    assert np.array_equal(cc.download()[:nc], occ)
+    assert np.array_equal(f2c.download(), of2c)
+    assert np.array_equal(ch.download()[: 8 * nc], och)
+    assert np.array_equal(gpu_kmap(s3dx, c, n), O.kmap_subm3(c, n))
+
+
+def test_subdivide_rejects_duplicates(s3dx):
+    p = np.array([[0, 1, 2, 3], [0, 4, 4, 4], [0, 1, 2, 3]], np.int32)
+    assert not s3dx.MeshSubdivideTables().build(p)
+    with pytest.raises(s3dx.S3dxError, match="duplicate"):
+        s3dx.subdivide2(s3dx.DeviceArray.from_host(p), 3)
+
+
+def test_two_level_subdivide_properties(s3dx, W):
+    # The mesh-decoder path at full size: 64^3 set -> 128^3 -> 256^3 (~1.8M).
+    parents = W.shells_union(0)
+    t0 = s3dx.MeshSubdivideTables()
+    assert t0.build(parents)
+    t1 = s3dx.MeshSubdivideTables()
+    assert t1.build(t0.child_coords, t0.child_count)
+    n1 = t1.child_count
+    print(f"two-level subdivide children={n1}", flush=True)
+    k = t1.neighbors.download()
+    child = t1.child_coords.download()
+    # centre tap is the row itself; neighbour relation is symmetric
+    assert np.array_equal(k[:, 13], np.arange(n1))
+    for o in (0, 4, 12, 22):
+        have = np.nonzero(k[:, o] >= 0)[0]
+        assert np.array_equal(k[k[have, o], 26 - o], have)
+        d = child[k[have, o], 1:] - child[have, 1:]
+        assert np.all(d == np.array([o // 9 - 1, (o // 3) % 3 - 1, o % 3 - 1]))
+    # the subdivided map equals a from-scratch kernel map over the children
+    assert np.array_equal(s3dx.kmap_subm3(t1.child_coords, n1, -1).download(), k)

@@ -1,0 +1,69 @@
+"""GPU row ops (LayerNorm, GroupNorm statistics, affine+SiLU, SLat
+down/upsample, conversions) against the oracle."""
+import numpy as np
+import pytest
+
+from helpers import rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(s3dx, a):
+    return s3dx.DeviceArray.from_host(np.ascontiguousarray(a))
+
+
+@pytest.mark.parametrize("c", [128, 96, 2048, 101])
+def test_layernorm_rows(s3dx, O, W, c):
+    n = 1000
+    x = W.normal_f32(11, 1, (n, c), 2.0) + 0.5
+    w, b = W.normal_f32(11, 2, (c,)), W.normal_f32(11, 3, (c,))
+    ms, mh = W.normal_f32(11, 4, (c,)), W.normal_f32(11, 5, (c,))
+    y = s3dx.DeviceArray((n, c), np.float32)
+    s3dx.layernorm_rows(dev(s3dx, x), s3dx.F32, n, c, 1e-6, dev(s3dx, w), dev(s3dx, b),
+                        dev(s3dx, ms), dev(s3dx, mh), True, y, s3dx.F32)
+    ref = O.silu(O.modulate(O.layernorm(x, 1e-6, w, b), ms, mh))
+    assert rel_l2(y.download(), ref) <= 1e-5
+    # bf16 in, bf16 out, in place, no affine
+    xb = dev(s3dx, W.f32_to_bf16_bits(x))
+    s3dx.layernorm_rows(xb, s3dx.BF16, n, c, 1e-6)
+    got = W.bf16_bits_to_f32(xb.download()).reshape(n, c)
+    assert rel_l2(got, O.layernorm(W.round_bf16(x), 1e-6)) <= 1e-2
+
+
+@pytest.mark.parametrize("n,c", [(5000, 96), (40000, 192), (3000, 768)])
+def test_groupnorm_stats_and_affine(s3dx, O, W, n, c):
+    x = W.normal_f32(12, 1, (n, c), 1.5) + W.normal_f32(12, 2, (c,), 2.0)
+    g, b = W.normal_f32(12, 3, (c,)), W.normal_f32(12, 4, (c,))
+    dx = dev(s3dx, x)
+    scale, shift, _ = s3dx.groupnorm_stats(dx, s3dx.F32, n, c, 32, 1e-5, dev(s3dx, g), dev(s3dx, b))
+    y = s3dx.DeviceArray((n, c), np.float32)
+    s3dx.affine_rows(dx, s3dx.F32, n, c, scale, shift, True, y, s3dx.F32)
+    ref = O.silu(O.groupnorm(x, 32, 1e-5, g, b))
+    assert rel_l2(y.download(), ref) <= 1e-5
+
+
+def test_down_up_sample(s3dx, O, W):
+    coords = W.shells_union(0)
+    n = coords.shape[0]
+    nc, cc, f2c, ch, inv = s3dx.coarsen2(dev(s3dx, coords), n)
+    c = 64
+    x = W.normal_f32(13, 1, (n, c))
+    dx = dev(s3dx, x)
+    down = s3dx.DeviceArray((nc, c), np.float32)
+    s3dx.downsample_mean(dx, s3dx.F32, n, c, ch, inv, nc, down)
+    ref = O.downsample_mean(x, ch.download()[: 8 * nc], inv.download()[:nc], nc)
+    assert rel_l2(down.download(), ref) <= 1e-6
+    up = s3dx.DeviceArray((n, c), np.float32)
+    s3dx.upsample_nearest(down, s3dx.F32, nc, c, f2c, n, up)
+    assert np.array_equal(up.download(), O.upsample_nearest(down.download(), f2c.download()))
+
+
+def test_convert_roundtrip(s3dx, W):
+    x = W.normal_f32(14, 1, (4096,), 100.0)
+    d = dev(s3dx, x)
+    b = s3dx.DeviceArray((4096,), np.uint16)
+    s3dx.convert(d, s3dx.F32, 4096, b, s3dx.BF16)
+    assert np.array_equal(b.download(), W.f32_to_bf16_bits(x))
+    back = s3dx.DeviceArray((4096,), np.float32)
+    s3dx.convert(b, s3dx.BF16, 4096, back, s3dx.F32)
+    assert np.array_equal(back.download(), W.round_bf16(x))

@@ -1,0 +1,208 @@
+"""Pins the CPU oracle (test infrastructure) to the reference before it is
+trusted as the GPU checker: golden tables from the reference's own
+sparse_ops.cpp, the compiled reference itself where present, and closed
+forms / library routines for what those leave open."""
+import numpy as np
+import pytest
+
+from helpers import SMALL, large_sets, rel_l2, sha
+
+
+# ---- kernel maps, coarse tables, subdivide: reference golden vectors -------
+@pytest.mark.parametrize("name", SMALL)
+def test_small_tables_match_reference_golden(O, golden, name):
+    arrays, manifest = golden
+    coords = arrays[f"{name}.coords"]
+    n = coords.shape[0]
+    assert np.array_equal(O.kmap_subm3(coords, n), arrays[f"{name}.conv_fine"])
+    nc, cc, f2c, ch, inv = O.coarsen2(coords)
+    assert nc == manifest[name]["nc"]
+    assert np.array_equal(f2c, arrays[f"{name}.fine_to_coarse"])
+    assert np.array_equal(O.kmap_subm3(cc, nc), arrays[f"{name}.conv_coarse"])
+    assert np.array_equal(ch, arrays[f"{name}.coarse_children"])
+    assert np.array_equal(inv.view(np.uint32), arrays[f"{name}.coarse_inv_count"].view(np.uint32))
+    sub = O.subdivide2(coords)
+    if manifest[name]["subdivide"] == "rejected":
+        assert sub is None
+    else:
+        assert np.array_equal(sub[0], arrays[f"{name}.child_coords"])
+        assert np.array_equal(sub[1], arrays[f"{name}.neighbors"])
+
+
+def test_large_tables_match_reference_sha(O, W, golden):
+    arrays, manifest = golden
+    for name, coords in large_sets(W, O, arrays).items():
+        m = manifest[name]
+        assert sha(coords) == m["coords_sha256"], f"{name}: generator drift"
+        n = coords.shape[0]
+        kmap = O.kmap_subm3(coords, n)
+        assert sha(kmap) == m["conv_fine_sha256"], name
+        assert int(np.count_nonzero(kmap != n)) == m["pairs"]
+        nc, cc, f2c, ch, inv = O.coarsen2(coords)
+        assert nc == m["nc"] and sha(f2c) == m["fine_to_coarse_sha256"], name
+        assert sha(O.kmap_subm3(cc, nc)) == m["conv_coarse_sha256"], name
+        assert sha(ch) == m["coarse_children_sha256"] and sha(inv) == m["coarse_inv_count_sha256"]
+        child, nbr = O.subdivide2(coords)
+        assert sha(child) == m["subdivide"]["child_coords_sha256"], name
+        assert sha(nbr) == m["subdivide"]["neighbors_sha256"], name
+
+
+def test_real_occupancy_counts(O, golden):
+    arrays, manifest = golden
+    occ = np.unpackbits(arrays["ss_occ.bits"]).reshape(64, 64, 64).astype(np.float32)
+    coords = O.occupancy_coords(occ)
+    surface = O.prune_surface(coords)
+    assert sha(coords) == manifest["ss_occ"]["occupied_sha256"]
+    assert sha(surface) == manifest["ss_occ"]["surface_sha256"]
+    assert (coords.shape[0], surface.shape[0]) == (69537, 67783)
+
+
+@pytest.mark.skipif("not __import__('s3dx_oracle').ref_available()")
+def test_oracle_equals_compiled_reference_random(O):
+    rng = np.random.default_rng(99)
+    for trial in range(20):
+        n = int(rng.integers(1, 300))
+        span = int(rng.integers(2, 12))
+        c = rng.integers(-span, span, size=(n, 4)).astype(np.int32)
+        c[:, 0] = rng.integers(0, 2, size=n)
+        cf, nc, f2c, cc, ch, inv = O.ref_slat_tables(c)
+        assert np.array_equal(O.kmap_subm3(c, n), cf)
+        onc, occ, of2c, och, oinv = O.coarsen2(c)
+        assert onc == nc and np.array_equal(of2c, f2c) and np.array_equal(och, ch)
+        assert np.array_equal(O.kmap_subm3(occ, nc), cc)
+        ref = O.ref_mesh_subdivide(c)
+        mine = O.subdivide2(c)
+        assert (ref is None) == (mine is None)
+        if ref is not None:
+            assert np.array_equal(ref[0], mine[0]) and np.array_equal(ref[1], mine[1])
+
+
+# ---- kernel maps: closed forms and brute force -------------------------------
+def brute_kmap(coords, missing):
+    first = {}
+    for i, c in enumerate(map(tuple, coords)):
+        first.setdefault(c, i)
+    out = np.full((len(coords), 27), missing, np.int32)
+    for i, (b, x, y, z) in enumerate(map(tuple, coords)):
+        if first[(b, x, y, z)] != i:
+            continue
+        for o in range(27):
+            q = (b, x + o // 9 - 1, y + (o // 3) % 3 - 1, z + o % 3 - 1)
+            if q in first:
+                out[i, o] = first[q]
+    return out
+
+
+def test_kmap_brute_force_and_invariants(O):
+    rng = np.random.default_rng(5)
+    c = np.unique(np.concatenate([np.zeros((300, 1), int), rng.integers(0, 8, (300, 3))], 1), axis=0)
+    c = c.astype(np.int32)
+    n = len(c)
+    k = O.kmap_subm3(c, -1)
+    assert np.array_equal(k, brute_kmap(c, -1))
+    assert np.array_equal(k[:, 13], np.arange(n))          # centre is self
+    for o in range(27):                                      # symmetry
+        have = k[:, o] >= 0
+        assert np.array_equal(k[k[have, o], 26 - o], np.nonzero(have)[0])
+
+
+def test_kmap_dense_block_and_isolated(O):
+    xyz = np.stack(np.meshgrid(*[np.arange(5)] * 3, indexing="ij"), -1).reshape(-1, 3)
+    c = np.concatenate([np.zeros((125, 1), int), xyz], 1).astype(np.int32)
+    k = O.kmap_subm3(c, 125)
+    interior = np.all((xyz >= 1) & (xyz <= 3), axis=1)
+    assert np.all(k[interior] != 125)                        # all 27 neighbours
+    lone = np.array([[0, 0, 0, 0], [0, 10, 10, 10]], np.int32)
+    k2 = O.kmap_subm3(lone, 2)
+    assert np.array_equal(k2[:, 13], [0, 1]) and np.count_nonzero(k2 != 2) == 2
+
+
+def test_subdivide_children_closed_form(O):
+    p = np.array([[0, 3, 4, 5], [1, -2, 0, 7]], np.int32)
+    child, nbr = O.subdivide2(p)
+    for r in range(16):
+        ch = r % 8
+        b, x, y, z = p[r // 8]
+        assert tuple(child[r]) == (b, 2 * x + ch // 4, 2 * y + (ch // 2) % 2, 2 * z + ch % 2)
+    assert np.array_equal(nbr, brute_kmap(child, -1))         # all 8 children exist
+
+
+# ---- convolution arithmetic ----------------------------------------------------
+def test_conv_dense_block_equals_conv3d(O, golden):
+    arrays, _ = golden
+    c = arrays["dense_conv.coords"]
+    x = arrays["dense_conv.x"]
+    w = arrays["dense_conv.w_slat"]
+    b = arrays["dense_conv.bias"]
+    n = c.shape[0]
+    y = O.conv(x, O.kmap_subm3(c, n), n, w, 0, w.shape[0], b)
+    assert rel_l2(y, arrays["dense_conv.y"]) < 1e-6
+
+
+def test_conv_layouts_isolated_and_linear(O, W):
+    rng = np.random.default_rng(3)
+    cin, cout = 16, 24
+    w_slat = rng.standard_normal((cout, 27, cin)).astype(np.float32)
+    w_mesh = np.ascontiguousarray(w_slat.transpose(1, 0, 2))
+    coords = W.shell_64(res=16, centre=(8.0, 8.0, 8.0), radius=5.0)
+    n = len(coords)
+    x = rng.standard_normal((n, cin)).astype(np.float32)
+    k = O.kmap_subm3(coords, n)
+    b = rng.standard_normal(cout).astype(np.float32)
+    y0 = O.conv(x, k, n, w_slat, 0, cout, b)
+    y1 = O.conv(x, k, n, w_mesh, 1, cout, b)
+    assert rel_l2(y0, y1) < 1e-7
+    # an isolated voxel sees only the centre tap: W_13 x + b
+    lone = np.array([[0, 1, 1, 1], [0, 9, 9, 9]], np.int32)
+    xl = rng.standard_normal((2, cin)).astype(np.float32)
+    yl = O.conv(xl, O.kmap_subm3(lone, 2), 2, w_slat, 0, cout, b)
+    assert rel_l2(yl, xl @ w_slat[:, 13, :].T + b) < 1e-6
+    # kvol 1 without a map is a linear layer
+    wl = rng.standard_normal((cout, 1, cin)).astype(np.float32)
+    ylin = O.conv(x, None, n, wl, 0, cout, b, kvol=1)
+    assert rel_l2(ylin, x @ wl[:, 0, :].T + b) < 1e-6
+
+
+def test_cpu_baseline_gemm_matches_oracle(O, W):
+    coords = W.shells_union(0)[:3000]
+    n = len(coords)
+    k = O.kmap_subm3(coords, n)
+    x = W.normal_f32(1, 2, (n, 32))
+    w = W.conv_weight(1, 3, 32, 40)
+    b = W.normal_f32(1, 4, (40,))
+    y = O.conv_im2col_gemm_f32(x, k, n, w, 40, b, 4)
+    assert rel_l2(y, O.conv(x, k, n, w, 0, 40, b)) < 1e-6
+
+
+# ---- epilogues -------------------------------------------------------------------
+def test_norms_match_library(O, golden):
+    arrays, _ = golden
+    x, w, b = arrays["norm.x"], arrays["norm.w"], arrays["norm.b"]
+    assert rel_l2(O.layernorm(x, 1e-6, w, b), arrays["norm.layer_norm"]) < 1e-6
+    assert rel_l2(O.groupnorm(x, 32, 1e-5, w, b), arrays["norm.group_norm"]) < 1e-6
+    assert rel_l2(O.silu(x), arrays["norm.silu"]) < 1e-6
+
+
+def test_modulate_down_up_repeat(O):
+    rng = np.random.default_rng(8)
+    h = rng.standard_normal((5, 6)).astype(np.float32)
+    s, t = rng.standard_normal(6).astype(np.float32), rng.standard_normal(6).astype(np.float32)
+    assert np.allclose(O.modulate(h, s, t), h * (1 + s) + t, rtol=1e-6, atol=1e-6)
+    coords = np.array([[0, 0, 0, 0], [0, 1, 0, 0], [0, 2, 2, 2], [0, 1, 1, 1]], np.int32)
+    nc, cc, f2c, ch, inv = O.coarsen2(coords)
+    x = rng.standard_normal((4, 3)).astype(np.float32)
+    down = O.downsample_mean(x, ch, inv, nc)
+    # scatter-mean quirk: sum over children / (count + 1)
+    assert np.allclose(down[0], (x[0] + x[1] + x[3]) / 4, atol=1e-6)
+    assert np.allclose(down[1], x[2] / 2, atol=1e-6)
+    up = O.upsample_nearest(down, f2c)
+    assert np.array_equal(up[1], down[0]) and np.array_equal(up[2], down[1])
+    rep = O.repeat_children(x)
+    assert np.array_equal(rep[8 * 2 + 5], x[2])
+
+
+def test_round_bf16_nearest_even(O):
+    v = np.array([1.0, 1.00390625, 1.01171875, -2.5, 3.0e38, 1e-40], np.float32)
+    r = O.round_bf16(v)
+    assert r[0] == 1.0 and r[1] == 1.0 and r[2] == np.float32(1.015625)
+    assert np.all(r.view(np.uint32) & 0xFFFF == 0)
