@@ -1,0 +1,272 @@
+#!/usr/bin/env python3
+"""Sparse-voxel conv benchmark: effective TFLOP/s + kernel-map Mvox/s.
+
+Workload (one step): on a seeded 64^3 union of 8 sphere shells (~28k voxels,
+int32 coords resident in HBM), build the 27-offset kernel map on the GPU, then
+run one SparseResBlock at C=128:
+    conv3x3x3 -> LayerNorm -> SiLU -> conv3x3x3 -> + x
+in BF16 with FP32 accumulation (LayerNorm/SiLU fused into the first conv's
+epilogue, the residual into the second's).  The same block in FP32 is
+reported beside it.
+
+value        = effective conv TFLOP/s = 2 * (2*Cin*Cout*P) / (conv1 + conv2
+               kernel time), P = present (voxel, offset) pairs of the map,
+               kernel times from HIP events around each launch on its stream
+kmap_mvox_s  = voxels / (device time of the kernel-map build)
+ms_per_step  = wall clock per step (kernel map + block, host launches included)
+
+The CPU baseline (rank 0, N=1 only) times the oracle's restatement of the
+reference CPU path on the same inputs: im2col gather + FP32 GEMM on all host
+threads (the GGML CPU decomposition), and the reference's own SlatTables::build
+compiled from its sources (oracle/_ref) for the kernel map.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+import __graft_entry__ as ge  # noqa: E402
+
+METRIC = "sparse-conv effective TFLOP/s + kernel-map Mvox/s, 64^3 ~30k vox C=128"
+PEAK_BF16_TFLOPS = 2516.6
+PEAK_FP32_TFLOPS = 157.3
+PEAK_HBM_GBS = 8000.0
+KMAP_BYTES_PER_VOXEL = 124  # 16 B coords in + 108 B map out
+
+
+def parse():
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--channels", type=int, default=128)
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="run only a 256 MiB copy kernel (HBM counter calibration)")
+    return p.parse_args()
+
+
+class Block:
+    """SparseResBlock at one dtype: conv(+LN+SiLU) then conv(+residual)."""
+
+    def __init__(self, s3dx, W, dtype, n, c, seed, stream):
+        self.s3dx, self.n, self.c, self.dtype, self.stream = s3dx, n, c, dtype, stream
+        x = W.normal_f32(seed, 100, (n, c))
+        w1 = W.conv_weight(seed, 101, c, c)
+        w2 = W.conv_weight(seed, 102, c, c)
+        b = np.zeros(c, np.float32)
+        self.host = dict(x=x, w1=w1, w2=w2, b=b)
+        store = np.uint16 if dtype == s3dx.BF16 else np.float32
+        xd = W.f32_to_bf16_bits(x) if dtype == s3dx.BF16 else x
+        self.x = s3dx.DeviceArray.from_host(xd)
+        self.h = s3dx.DeviceArray((n, c), store)
+        self.y = s3dx.DeviceArray((n, c), store)
+        self.conv1 = (s3dx.SparseConv(c, c, 27, dtype).set_weights(w1, s3dx.WEIGHT_SLAT, b)
+                      .set_layernorm(True, 1e-6).set_silu(True))
+        self.conv2 = s3dx.SparseConv(c, c, 27, dtype).set_weights(w2, s3dx.WEIGHT_SLAT, b)
+
+    def run(self, kmap, ev=None):
+        s = self.stream
+        if ev:
+            ev[0].record(s)
+        self.conv1.run(self.x, self.n, kmap, self.n, self.h, self.dtype, None, s)
+        if ev:
+            ev[1].record(s)
+        self.conv2.run(self.h, self.n, kmap, self.n, self.y, self.dtype, self.x, s)
+        if ev:
+            ev[2].record(s)
+
+
+def copy_calibration(s3dx):
+    n = 64 * 1024 * 1024  # 256 MiB of f32
+    a = s3dx.DeviceArray((n,), np.float32)
+    b = s3dx.DeviceArray((n,), np.float32)
+    for _ in range(3):
+        s3dx.convert(a, s3dx.F32, n, b, s3dx.F32)
+    s3dx.synchronize()
+    print(json.dumps({"copy_calibration_bytes_read": n * 4, "copy_calibration_bytes_written": n * 4}))
+
+
+def cpu_baseline(block, kmap_host, n, pairs, coords, W):
+    O = ge.load_oracle()
+    threads = min(16, os.cpu_count() or 1)
+    h = block.host
+    c = block.c
+    flops = 2.0 * c * c * pairs
+    O.conv_im2col_gemm_f32(h["x"], kmap_host, n, h["w1"], c, h["b"], threads)  # warm-up
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        O.conv_im2col_gemm_f32(h["x"], kmap_host, n, h["w1"], c, h["b"], threads)
+        times.append(time.perf_counter() - t0)
+    t_conv = statistics.median(times)
+    kmap_kind, kt = "port", []
+    if O.ref_available():
+        kmap_kind = "reference"
+        for _ in range(3):
+            t0 = time.perf_counter()
+            O.ref_slat_tables(coords, 6)
+            kt.append(time.perf_counter() - t0)
+    else:
+        for _ in range(3):
+            t0 = time.perf_counter()
+            O.kmap_subm3(coords, n)
+            kt.append(time.perf_counter() - t0)
+    t_kmap = statistics.median(kt)
+    return {
+        "value": flops / t_conv / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
+        "sample": (f"one {c}->{c} FP32 sparse conv over the same {n} voxels / {pairs} pairs: "
+                   f"im2col gather + FP32 GEMM on {threads} threads (GGML CPU decomposition), "
+                   f"median of 3 after 1 warm-up, {t_conv * 1e3:.1f} ms each"),
+        "conv_ms": t_conv * 1e3,
+        "kmap": {"value": n / t_kmap / 1e6, "unit": "Mvox/s", "cores": 1, "kind": kmap_kind,
+                 "ms": t_kmap * 1e3,
+                 "sample": ("reference SlatTables::build (fine + coarse maps, 6-channel APE) "
+                            "compiled from sparse_ops.cpp" if kmap_kind == "reference" else
+                            "oracle ordered-map kernel map") + ", single thread, median of 3"},
+        "cpu_model": cpu_model(),
+    }
+
+
+def cpu_model():
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported in this build "
+              "(every box has one GPU and the path has no multi-GPU leg)", file=sys.stderr)
+        sys.exit(2)
+    s3dx = ge.load_package()
+    W = s3dx.workloads
+    if args.copy_calibration:
+        copy_calibration(s3dx)
+        return
+    c = args.channels
+    coords = W.shells_union(args.seed)
+    n = coords.shape[0]
+    stream = s3dx.Stream()
+    dc = s3dx.DeviceArray.from_host(coords, stream)
+    kmap = s3dx.DeviceArray((n, 27), np.int32)
+    ws = s3dx.DeviceArray(s3dx.kmap_workspace_size(n), np.uint8)
+    s3dx.kmap_subm3(dc, n, n, kmap, ws, stream)
+    kmap_host = kmap.download(stream)
+    pairs = W.kmap_pairs(kmap_host, n)
+    flops = 2.0 * c * c * pairs  # effective FLOPs per conv
+
+    bf = Block(s3dx, W, s3dx.BF16, n, c, args.seed, stream)
+    f32 = Block(s3dx, W, s3dx.F32, n, c, args.seed, stream)
+
+    def step(ev_k=None, ev_b=None):
+        if ev_k:
+            ev_k[0].record(stream)
+        s3dx.kmap_subm3(dc, n, n, kmap, ws, stream)
+        if ev_k:
+            ev_k[1].record(stream)
+        bf.run(kmap, ev_b)
+
+    for _ in range(args.warmup):
+        step()
+        f32.run(kmap)
+    stream.synchronize()
+
+    K = args.steps
+    evk = [[s3dx.Event(), s3dx.Event()] for _ in range(K)]
+    evb = [[s3dx.Event(), s3dx.Event(), s3dx.Event()] for _ in range(K)]
+    stream.synchronize()
+    t0 = time.perf_counter()
+    for i in range(K):
+        step(evk[i], evb[i])
+    stream.synchronize()
+    wall = time.perf_counter() - t0
+
+    kmap_ms = [evk[i][0].elapsed_ms(evk[i][1]) for i in range(K)]
+    conv1_ms = [evb[i][0].elapsed_ms(evb[i][1]) for i in range(K)]
+    conv2_ms = [evb[i][1].elapsed_ms(evb[i][2]) for i in range(K)]
+    conv_ms = statistics.mean(conv1_ms + conv2_ms)
+    block_ms = statistics.mean(a + b for a, b in zip(conv1_ms, conv2_ms))
+    kmap_avg = statistics.mean(kmap_ms)
+
+    # FP32 block, timed the same way after the BF16 region.
+    evf = [[s3dx.Event(), s3dx.Event(), s3dx.Event()] for _ in range(K)]
+    for i in range(K):
+        f32.run(kmap, evf[i])
+    stream.synchronize()
+    f1 = [evf[i][0].elapsed_ms(evf[i][1]) for i in range(K)]
+    f2 = [evf[i][1].elapsed_ms(evf[i][2]) for i in range(K)]
+    f32_conv_ms = statistics.mean(f1 + f2)
+
+    tflops = 2 * flops / (block_ms * 1e-3) / 1e12
+    achieved = flops / (conv_ms * 1e-3) / 1e12
+    traffic = None
+    tfile = ROOT / "profiles" / "conv_bf16_c128_shells64_traffic.json"
+    if tfile.exists():
+        traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+    out = {
+        "metric": METRIC,
+        "value": tflops,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": wall / K * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": (f"SparseResBlock C={c} (conv3x3x3 -> LayerNorm -> SiLU -> conv3x3x3 -> +x) "
+                         f"plus its kernel-map build, 8-shell union on a 64^3 grid, seed {args.seed}"),
+            "voxels": n, "pairs": pairs, "channels": c, "seed": args.seed,
+            "effective_gflop_per_conv": flops / 1e9,
+            "dense27_gflop_per_conv": 2.0 * 27 * n * c * c / 1e9,
+        },
+        "kmap_mvox_s": n / (kmap_avg * 1e-3) / 1e6,
+        "kmap_ms": kmap_avg,
+        "block_ms": block_ms,
+        "conv_kernel_ms": conv_ms,
+        "roofline": {
+            "bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+            "frac": achieved / PEAK_BF16_TFLOPS, "traffic": traffic,
+            "kernel": "conv_mfma_kernel<bf16, NB=4, KC=128>",
+        },
+        "kmap_roofline": {
+            "bound": "hbm", "achieved": n * KMAP_BYTES_PER_VOXEL / (kmap_avg * 1e-3) / 1e9,
+            "peak": PEAK_HBM_GBS, "unit": "GB/s",
+            "frac": n * KMAP_BYTES_PER_VOXEL / (kmap_avg * 1e-3) / 1e9 / PEAK_HBM_GBS,
+        },
+        "fp32": {
+            "value": flops / (f32_conv_ms * 1e-3) / 1e12, "unit": "TFLOP/s",
+            "conv_kernel_ms": f32_conv_ms, "peak": PEAK_FP32_TFLOPS,
+            "frac": flops / (f32_conv_ms * 1e-3) / 1e12 / PEAK_FP32_TFLOPS,
+        },
+        "device": s3dx.device_name(),
+    }
+    if not args.no_cpu:
+        cb = cpu_baseline(f32, kmap_host, n, pairs, coords, W)
+        out["cpu_baseline"] = cb
+        out["gpu_over_cpu"] = {"conv": out["value"] / cb["value"],
+                               "kmap": out["kmap_mvox_s"] / cb["kmap"]["value"]}
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

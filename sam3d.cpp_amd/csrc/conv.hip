@@ -25,272 +25,14 @@
 //   f32  32x32x2 : each lane carries 1 k; four MFMAs consume one 16-byte
 //                  fragment (channels s*8 + (l/32)*4 + j, j = 0..3), with the
 //                  weight packed in the same permuted order.
-#include "common.hpp"
+#include "conv_kernels.hpp"
 
+#include <cstdlib>
 #include <memory>
 #include <vector>
 
 namespace s3dx {
 namespace {
-
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-
-struct ConvArgs {
-    const void *x;
-    int64_t n_src;  // rows addressable through the kmap (8 * parents when gathering parents)
-    int32_t cin;
-    const int32_t *kmap;
-    int64_t n_out;
-    int32_t kvol;
-    const void *w;
-    const float *bias;
-    int32_t cout;
-    const void *residual;
-    void *y;
-    int32_t y_bf16;
-    int32_t gather_parent;
-    const float *slot_offset;
-    const float *pre_scale;
-    const float *pre_shift;
-    int32_t ln;
-    float eps;
-    const float *ln_w;
-    const float *ln_b;
-    const float *mod_scale;
-    const float *mod_shift;
-    int32_t silu;
-};
-
-constexpr int kBM = 128;      // rows per workgroup (4 waves x 32)
-constexpr int kMaxKvol = 27;
-
-// Workgroups are dealt round-robin over the 8 XCDs; give each XCD a
-// contiguous run of row tiles so neighbouring gathers share its L2.
-__device__ __forceinline__ int xcd_tile(int bid, int nblocks) {
-    const int q = nblocks / 8, r = nblocks % 8;
-    const int xcd = bid % 8, local = bid / 8;
-    return xcd * q + min(xcd, r) + local;
-}
-
-template <class T>
-struct Frag;
-template <>
-struct Frag<uint16_t> {
-    static constexpr int E = 8;  // elements per 16-byte fragment
-};
-template <>
-struct Frag<float> {
-    static constexpr int E = 4;
-};
-
-// Applies the optional input transforms to one 16-byte fragment of row j,
-// channels c0 .. c0+E.  Returns the fragment in T.
-template <class T>
-__device__ __forceinline__ uint4 load_fragment(const ConvArgs &a, int32_t j, int32_t c0) {
-    constexpr int E = Frag<T>::E;
-    if (j < 0) return make_uint4(0, 0, 0, 0);
-    const int64_t src = a.gather_parent ? (j >> 3) : j;
-    const T *xp = static_cast<const T *>(a.x) + src * a.cin + c0;
-    uint4 raw = *reinterpret_cast<const uint4 *>(xp);
-    const bool slot = a.gather_parent && a.slot_offset;
-    const bool affine = a.pre_scale != nullptr;
-    if (!slot && !affine) return raw;
-    float v[E];
-    if constexpr (E == 8) {
-        const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            v[2 * e] = bf16_to_f32(static_cast<uint16_t>(w4[e] & 0xffffu));
-            v[2 * e + 1] = bf16_to_f32(static_cast<uint16_t>(w4[e] >> 16));
-        }
-    } else {
-        v[0] = __builtin_bit_cast(float, raw.x);
-        v[1] = __builtin_bit_cast(float, raw.y);
-        v[2] = __builtin_bit_cast(float, raw.z);
-        v[3] = __builtin_bit_cast(float, raw.w);
-    }
-    if (slot) {
-        const float *so = a.slot_offset + (j & 7) * a.cin + c0;
-#pragma unroll
-        for (int e = 0; e < E; ++e) v[e] += so[e];
-    }
-    if (affine) {
-#pragma unroll
-        for (int e = 0; e < E; ++e) v[e] = silu(v[e] * a.pre_scale[c0 + e] + a.pre_shift[c0 + e]);
-    }
-    if constexpr (E == 8) {
-        uint32_t w4[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-            w4[e] = static_cast<uint32_t>(f32_to_bf16(v[2 * e])) |
-                    (static_cast<uint32_t>(f32_to_bf16(v[2 * e + 1])) << 16);
-        return make_uint4(w4[0], w4[1], w4[2], w4[3]);
-    } else {
-        return make_uint4(__builtin_bit_cast(uint32_t, v[0]), __builtin_bit_cast(uint32_t, v[1]),
-                          __builtin_bit_cast(uint32_t, v[2]), __builtin_bit_cast(uint32_t, v[3]));
-    }
-}
-
-template <class T>
-__device__ __forceinline__ f32x16 mfma_step(uint4 af, uint4 bf, f32x16 acc) {
-    if constexpr (sizeof(T) == 2) {
-        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, af),
-                                                       __builtin_bit_cast(bf16x8, bf), acc, 0, 0,
-                                                       0);
-    } else {
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__builtin_bit_cast(float, af.x),
-                                                   __builtin_bit_cast(float, bf.x), acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__builtin_bit_cast(float, af.y),
-                                                   __builtin_bit_cast(float, bf.y), acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__builtin_bit_cast(float, af.z),
-                                                   __builtin_bit_cast(float, bf.z), acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__builtin_bit_cast(float, af.w),
-                                                   __builtin_bit_cast(float, bf.w), acc, 0, 0, 0);
-        return acc;
-    }
-}
-
-// T: uint16_t (bf16) or float.  NB: 32-column blocks per tile.  KC: Cin
-// channels per staged chunk.
-template <class T, int NB, int KC>
-__global__ void __launch_bounds__(256) conv_mfma_kernel(ConvArgs a) {
-    constexpr int E = Frag<T>::E;
-    constexpr int CPK = 2 * E;       // channels per k-step (both lane halves)
-    constexpr int KS = KC / CPK;     // k-steps per chunk
-    __shared__ uint4 wlds[KS * NB * 64];
-    __shared__ int32_t rows[kBM * kMaxKvol];
-    __shared__ uint32_t omask;
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int tile = xcd_tile(blockIdx.x, gridDim.x);
-    const int64_t m0 = static_cast<int64_t>(tile) * kBM;
-    const int nb0 = blockIdx.y * NB;  // first 32-column block of this tile
-    const int nbtot = a.cout / 32;
-    const int kvol = a.kvol;
-    const int ksteps_total = a.cin / CPK;
-
-    if (tid == 0) omask = 0;
-    __syncthreads();
-    // Stage this tile's neighbour rows; -1 marks a missing neighbour.
-    uint32_t my_mask = 0;
-    for (int idx = tid; idx < kBM * kvol; idx += 256) {
-        const int r = idx / kvol, o = idx - r * kvol;
-        const int64_t row = m0 + r;
-        int64_t j = -1;
-        if (row < a.n_out) j = a.kmap ? a.kmap[row * kvol + o] : row;
-        const bool valid = j >= 0 && j < a.n_src;
-        rows[idx] = valid ? static_cast<int32_t>(j) : -1;
-        if (valid) my_mask |= 1u << o;
-    }
-    if (my_mask) atomicOr(&omask, my_mask);
-    __syncthreads();
-    const uint32_t mask = omask;
-
-    f32x16 acc[NB];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x16{};
-
-    const uint4 *wg = static_cast<const uint4 *>(a.w);
-    const int my_row = wave * 32 + (lane & 31);
-    const int half = lane >> 5;
-
-    for (int o = 0; o < kvol; ++o) {
-        if (!((mask >> o) & 1u)) continue;
-        const int32_t j = rows[my_row * kvol + o];
-        for (int kc = 0; kc < a.cin; kc += KC) {
-            // Gather this wave's A fragments for the chunk.
-            uint4 af[KS];
-#pragma unroll
-            for (int s = 0; s < KS; ++s) af[s] = load_fragment<T>(a, j, kc + s * CPK + half * E);
-            __syncthreads();  // previous chunk's LDS reads are done
-            // Stage the weight chunk: KS k-steps x NB column blocks x 64 lanes.
-            const int64_t kstep0 = static_cast<int64_t>(o) * ksteps_total + kc / CPK;
-            for (int q = tid; q < KS * NB * 64; q += 256) {
-                const int s = q / (NB * 64);
-                const int rem = q - s * (NB * 64);
-                const int nbl = rem >> 6;
-                wlds[q] = wg[((kstep0 + s) * nbtot + nb0 + nbl) * 64 + (rem & 63)];
-            }
-            __syncthreads();
-#pragma unroll
-            for (int s = 0; s < KS; ++s) {
-#pragma unroll
-                for (int nb = 0; nb < NB; ++nb)
-                    acc[nb] = mfma_step<T>(af[s], wlds[(s * NB + nb) * 64 + lane], acc[nb]);
-            }
-        }
-    }
-
-    // ---- epilogue ----
-    const int col_in_blk = lane & 31;
-    float v[NB][16];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-        const int col = (nb0 + nb) * 32 + col_in_blk;
-        const float b = a.bias ? a.bias[col] : 0.0f;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) v[nb][r] = acc[nb][r] + b;
-    }
-    if (a.ln) {
-        // The tile holds whole rows (NT == cout): row statistics reduce over
-        // the NB registers and the 32 lanes of this lane half.
-        const float inv_c = 1.0f / static_cast<float>(a.cout);
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            float s = 0.0f;
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb) s += v[nb][r];
-#pragma unroll
-            for (int d = 1; d < 32; d <<= 1) s += __shfl_xor(s, d, 64);
-            const float mean = s * inv_c;
-            float q = 0.0f;
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb) {
-                const float t = v[nb][r] - mean;
-                q += t * t;
-            }
-#pragma unroll
-            for (int d = 1; d < 32; d <<= 1) q += __shfl_xor(q, d, 64);
-            const float rstd = rsqrtf(q * inv_c + a.eps);
-#pragma unroll
-            for (int nb = 0; nb < NB; ++nb) v[nb][r] = (v[nb][r] - mean) * rstd;
-        }
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-            const int col = (nb0 + nb) * 32 + col_in_blk;
-            const float w = a.ln_w ? a.ln_w[col] : 1.0f;
-            const float b = a.ln_b ? a.ln_b[col] : 0.0f;
-            const float ms = a.mod_scale ? a.mod_scale[col] : 0.0f;
-            const float mh = a.mod_shift ? a.mod_shift[col] : 0.0f;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                float t = v[nb][r] * w + b;
-                if (a.mod_scale) t = (t * ms + t) + mh;
-                v[nb][r] = t;
-            }
-        }
-    }
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-        const int col = (nb0 + nb) * 32 + col_in_blk;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const int64_t row = m0 + wave * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-            if (row >= a.n_out) continue;
-            float t = v[nb][r];
-            if (a.silu) t = silu(t);
-            const int64_t off = row * a.cout + col;
-            if (a.y_bf16) {
-                if (a.residual) t += bf16_to_f32(static_cast<const uint16_t *>(a.residual)[off]);
-                static_cast<uint16_t *>(a.y)[off] = f32_to_bf16(t);
-            } else {
-                if (a.residual) t += static_cast<const float *>(a.residual)[off];
-                static_cast<float *>(a.y)[off] = t;
-            }
-        }
-    }
-}
 
 // ---------------------------------------------------------------------------
 // Generic VALU path: any Cin/Cout.  64 x 64 output tile, 16-channel chunks
@@ -400,32 +142,6 @@ __global__ void __launch_bounds__(256) conv_generic_kernel(ConvArgs a) {
     }
 }
 
-using KernelFn = void (*)(ConvArgs);
-
-template <class T>
-KernelFn pick_mfma(int nb, int kc) {
-#define S3DX_NB_CASES(KCV)                              \
-    switch (nb) {                                       \
-    case 1: return conv_mfma_kernel<T, 1, KCV>;         \
-    case 2: return conv_mfma_kernel<T, 2, KCV>;         \
-    case 3: return conv_mfma_kernel<T, 3, KCV>;         \
-    case 4: return conv_mfma_kernel<T, 4, KCV>;         \
-    case 6: return conv_mfma_kernel<T, 6, KCV>;         \
-    case 8: return conv_mfma_kernel<T, 8, KCV>;         \
-    default: return nullptr;                            \
-    }
-    if constexpr (sizeof(T) == 2) {
-        if (kc == 128) { S3DX_NB_CASES(128) }
-        if (kc == 64) { S3DX_NB_CASES(64) }
-        if (kc == 32) { S3DX_NB_CASES(32) }
-    } else {
-        if (kc == 64) { S3DX_NB_CASES(64) }
-        if (kc == 32) { S3DX_NB_CASES(32) }
-    }
-#undef S3DX_NB_CASES
-    return nullptr;
-}
-
 }  // namespace
 
 // LayerNorm / residual helpers for the generic path live in norm.hip.
@@ -465,6 +181,38 @@ struct s3dx_conv {
 
 namespace s3dx {
 namespace {
+
+KernelFn tiling_kernel(int id, bool bf, int kc, bool xf) {
+    return bf ? pick_mfma_bf16(id, kc, xf) : pick_mfma_f32(id, kc, xf);
+}
+
+// Picks the workgroup tiling for nb 32-column blocks per workgroup.  Waves
+// that own all 128 columns of a row (tiling 10) gather each row once and
+// stream two tasks per stage; otherwise two 32-row blocks per wave halve the
+// LDS traffic per MFMA when that still leaves one workgroup per CU.
+// S3DX_CONV_TILING=<id> overrides the choice (tuning).
+const Tiling *choose_tiling(int64_t n_out, int nb, int ntiles, bool bf, int kc, bool xf) {
+    if (const char *e = std::getenv("S3DX_CONV_TILING")) {
+        const int id = std::atoi(e);
+        for (const Tiling &t : kTilings)
+            if (t.id == id && t.cols() == nb * 32 && tiling_kernel(t.id, bf, kc, xf)) return &t;
+    }
+    auto blocks = [&](const Tiling &t) { return (n_out + t.rows() - 1) / t.rows() * ntiles; };
+    const Tiling *best = nullptr;
+    int best_rank = 1 << 30;
+    for (const Tiling &t : kTilings) {
+        if (t.cols() != nb * 32 || !tiling_kernel(t.id, bf, kc, xf)) continue;
+        int rank;
+        if (t.wn == 1 && t.nbw == 4) rank = blocks(t) >= 192 ? 0 : 10;  // 32x128 wave tiles
+        else if (t.mbw == 2) rank = blocks(t) >= 256 ? 1 : 20;
+        else rank = 5;
+        if (rank < best_rank) {
+            best_rank = rank;
+            best = &t;
+        }
+    }
+    return best;
+}
 
 float *upload_f32(const float *host, size_t count) {
     if (!host) return nullptr;
@@ -514,18 +262,29 @@ S3DX_API s3dx_status s3dx_conv_create(int32_t cin, int32_t cout, int32_t kvol, i
         c->kvol = kvol;
         c->dtype = dtype;
         const bool bf = dtype == S3DX_BF16;
-        int kc = 0;
-        if (bf) kc = cin % 128 == 0 ? 128 : cin % 64 == 0 ? 64 : cin % 32 == 0 ? 32 : 0;
-        else kc = cin % 64 == 0 ? 64 : cin % 32 == 0 ? 32 : 0;
+        // Column blocks per workgroup: the whole row when Cout <= 256 (so a
+        // LayerNorm epilogue sees it), else 128-column tiles.
         int nb = 0;
         if (cout % 32 == 0) {
             const int blocks = cout / 32;
-            for (int cand : {8, 6, 4, 3, 2, 1})
-                if (blocks % cand == 0) {
-                    nb = cand;
-                    break;
-                }
+            if (blocks <= 8) {
+                for (int cand : {8, 6, 4, 3, 2, 1})
+                    if (cand == blocks) nb = cand;
+                if (nb == 0) nb = 1;  // 5 or 7 blocks: 32-column tiles
+            } else {
+                for (int cand : {4, 2, 1})
+                    if (nb == 0 && blocks % cand == 0) nb = cand;
+            }
         }
+        // Channels per task: keep one weight stage <= 32 KiB of LDS.
+        int kc = 0;
+        const int elem = bf ? 2 : 4;
+        for (int cand : {128, 64, 32}) {
+            if (kc == 0 && cin % cand == 0 && (!bf ? cand <= 64 : true) &&
+                cand * nb * 32 * elem <= 32768)
+                kc = cand;
+        }
+        if (kc == 0 && cin % 32 == 0 && nb != 0) kc = 32;
         c->mfma = kc != 0 && nb != 0;
         c->kc = kc;
         c->nb = nb;
@@ -661,6 +420,7 @@ S3DX_API s3dx_status s3dx_conv_run(const s3dx_conv *conv, const void *x, int64_t
         const hipStream_t s = as_stream(stream);
         ConvArgs a{};
         a.x = x;
+        a.x_bytes = n_in * conv->cin * static_cast<int64_t>(dtype_size(conv->dtype));
         a.n_src = n_src;
         a.cin = conv->cin;
         a.kmap = kmap;
@@ -683,17 +443,26 @@ S3DX_API s3dx_status s3dx_conv_run(const s3dx_conv *conv, const void *x, int64_t
         a.mod_scale = conv->mod_scale;
         a.mod_shift = conv->mod_shift;
         const bool bf = conv->dtype == S3DX_BF16;
-        const bool fused_ln = conv->ln && conv->mfma && conv->nb * 32 == conv->cout;
-        if (conv->mfma) {
+        // The MFMA kernel reads the map and writes rows with 16-byte accesses.
+        const bool use_mfma = conv->mfma && aligned(kmap, 16) && aligned(y, 16) && aligned(residual, 16);
+        const bool fused_ln = conv->ln && use_mfma && conv->nb * 32 == conv->cout;
+        if (use_mfma) {
             a.ln = fused_ln;
             if (conv->ln && !fused_ln) {  // LayerNorm as a separate pass
                 a.silu = 0;
                 a.residual = nullptr;
             }
-            const KernelFn fn = bf ? pick_mfma<uint16_t>(conv->nb, conv->kc)
-                                   : pick_mfma<float>(conv->nb, conv->kc);
+            // Buffer-resource gathers address at most 2 GiB; larger inputs and
+            // the input transforms take the XF=1 variant.
+            const bool xf = conv->gather_parent || conv->pre_scale != nullptr ||
+                            a.x_bytes >= (int64_t(1) << 31);
+            const int ntiles = conv->cout / (32 * conv->nb);
+            const Tiling *tl = choose_tiling(n_out, conv->nb, ntiles, bf, conv->kc, xf);
+            require(tl != nullptr, "no MFMA kernel for this shape");
+            const KernelFn fn = tiling_kernel(tl->id, bf, conv->kc, xf);
             require(fn != nullptr, "no MFMA kernel for this shape");
-            const int64_t mt = (n_out + kBM - 1) / kBM;
+            const int bm = tl->rows();
+            const int64_t mt = (n_out + bm - 1) / bm;
             const dim3 grid(static_cast<unsigned>(mt), static_cast<unsigned>(conv->cout / (32 * conv->nb)));
             hipLaunchKernelGGL(fn, grid, dim3(256), 0, s, a);
             launch_check("conv_mfma");

@@ -1,0 +1,15 @@
+// FP32 instantiations of the MFMA sparse-convolution kernel
+// (v_mfma_f32_32x32x2f32).
+#include "conv_kernels.hpp"
+
+namespace s3dx {
+
+KernelFn pick_mfma_f32(int id, int kc, bool xf) {
+    switch (kc) {
+    case 64: return pick_kc<float, 64>(id, xf);
+    case 32: return pick_kc<float, 32>(id, xf);
+    default: return nullptr;
+    }
+}
+
+}  // namespace s3dx

@@ -1,0 +1,588 @@
+// Device side of the MFMA gather-GEMM sparse convolution (see conv.hip for
+// the operator it implements).  Instantiated per element type in
+// conv_bf16.hip and conv_f32.hip.
+#pragma once
+
+#include "common.hpp"
+
+#include <type_traits>
+
+namespace s3dx {
+
+struct ConvArgs {
+    const void *x;
+    int64_t x_bytes;  // bytes addressable at x
+    int64_t n_src;    // rows addressable through the kmap (8 * parents when gathering parents)
+    int32_t cin;
+    const int32_t *kmap;
+    int64_t n_out;
+    int32_t kvol;
+    const void *w;
+    const float *bias;
+    int32_t cout;
+    const void *residual;
+    void *y;
+    int32_t y_bf16;
+    int32_t gather_parent;
+    const float *slot_offset;
+    const float *pre_scale;
+    const float *pre_shift;
+    int32_t ln;
+    float eps;
+    const float *ln_w;
+    const float *ln_b;
+    const float *mod_scale;
+    const float *mod_shift;
+    int32_t silu;
+};
+
+using KernelFn = void (*)(ConvArgs);
+
+// Workgroup tilings of the MFMA kernel: 4 waves in WM x WN (WM = 4/WN), each
+// wave MBW x NBW blocks of 32x32 outputs.
+struct Tiling {
+    int id, mbw, nbw, wn;
+    int rows() const { return 32 * mbw * (4 / wn); }
+    int cols() const { return 32 * nbw * wn; }
+};
+inline constexpr Tiling kTilings[] = {
+    {0, 1, 1, 1}, {1, 1, 1, 2}, {2, 1, 3, 1}, {3, 1, 2, 2}, {4, 1, 3, 2}, {5, 1, 4, 2},
+    {6, 2, 1, 2}, {7, 2, 3, 1}, {8, 2, 2, 2}, {9, 2, 3, 2}, {10, 1, 4, 1},
+};
+
+// MFMA kernel for tiling `id`, kc channels per task, xf input transforms;
+// nullptr if that combination is not compiled.
+KernelFn pick_mfma_bf16(int id, int kc, bool xf);
+KernelFn pick_mfma_f32(int id, int kc, bool xf);
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kMaxKvol = 27;
+
+// Workgroups are dealt round-robin over the 8 XCDs; give each XCD a
+// contiguous run of row tiles so neighbouring gathers share its L2.
+__device__ __forceinline__ int xcd_tile(int bid, int nblocks) {
+    const int q = nblocks / 8, r = nblocks % 8;
+    const int xcd = bid % 8, local = bid / 8;
+    return xcd * q + min(xcd, r) + local;
+}
+
+template <class T>
+struct Frag;
+template <>
+struct Frag<uint16_t> {
+    static constexpr int E = 8;  // elements per 16-byte fragment
+};
+template <>
+struct Frag<float> {
+    static constexpr int E = 4;
+};
+
+// Applies the optional input transforms to one 16-byte fragment of row j,
+// channels c0 .. c0+E.  Returns the fragment in T.
+template <class T>
+__device__ __forceinline__ uint4 load_fragment(const ConvArgs &a, int32_t j, int32_t c0) {
+    constexpr int E = Frag<T>::E;
+    if (j < 0) return make_uint4(0, 0, 0, 0);
+    const int64_t src = a.gather_parent ? (j >> 3) : j;
+    const T *xp = static_cast<const T *>(a.x) + src * a.cin + c0;
+    uint4 raw = *reinterpret_cast<const uint4 *>(xp);
+    const bool slot = a.gather_parent && a.slot_offset;
+    const bool affine = a.pre_scale != nullptr;
+    if (!slot && !affine) return raw;
+    float v[E];
+    if constexpr (E == 8) {
+        const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            v[2 * e] = bf16_to_f32(static_cast<uint16_t>(w4[e] & 0xffffu));
+            v[2 * e + 1] = bf16_to_f32(static_cast<uint16_t>(w4[e] >> 16));
+        }
+    } else {
+        v[0] = __builtin_bit_cast(float, raw.x);
+        v[1] = __builtin_bit_cast(float, raw.y);
+        v[2] = __builtin_bit_cast(float, raw.z);
+        v[3] = __builtin_bit_cast(float, raw.w);
+    }
+    if (slot) {
+        const float *so = a.slot_offset + (j & 7) * a.cin + c0;
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[e] += so[e];
+    }
+    if (affine) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[e] = silu(v[e] * a.pre_scale[c0 + e] + a.pre_shift[c0 + e]);
+    }
+    if constexpr (E == 8) {
+        uint32_t w4[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            w4[e] = static_cast<uint32_t>(f32_to_bf16(v[2 * e])) |
+                    (static_cast<uint32_t>(f32_to_bf16(v[2 * e + 1])) << 16);
+        return make_uint4(w4[0], w4[1], w4[2], w4[3]);
+    } else {
+        return make_uint4(__builtin_bit_cast(uint32_t, v[0]), __builtin_bit_cast(uint32_t, v[1]),
+                          __builtin_bit_cast(uint32_t, v[2]), __builtin_bit_cast(uint32_t, v[3]));
+    }
+}
+
+template <class T>
+__device__ __forceinline__ f32x16 mfma_step(uint4 af, uint4 bf, f32x16 acc) {
+    if constexpr (sizeof(T) == 2) {
+        return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, af),
+                                                       __builtin_bit_cast(bf16x8, bf), acc, 0, 0,
+                                                       0);
+    } else {
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__builtin_bit_cast(float, af.x),
+                                                   __builtin_bit_cast(float, bf.x), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__builtin_bit_cast(float, af.y),
+                                                   __builtin_bit_cast(float, bf.y), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__builtin_bit_cast(float, af.z),
+                                                   __builtin_bit_cast(float, bf.z), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x2f32(__builtin_bit_cast(float, af.w),
+                                                   __builtin_bit_cast(float, bf.w), acc, 0, 0, 0);
+        return acc;
+    }
+}
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// Plain gather of one 16-byte fragment through a raw buffer resource: a
+// missing neighbour (j < 0) gets an offset past the buffer end, which the
+// hardware answers with zeros -- no branch, no wasted bandwidth.
+template <class T>
+__device__ __forceinline__ uint4 gather_plain(const void *base, int32_t bytes, int32_t j, int32_t cin,
+                                              int32_t c0) {
+    const uint32_t off = j >= 0 ? (static_cast<uint32_t>(j) * static_cast<uint32_t>(cin) +
+                                   static_cast<uint32_t>(c0)) * static_cast<uint32_t>(sizeof(T))
+                                : 0x80000000u;
+    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), static_cast<short>(0), bytes,
+                                          0x00020000),
+        off, 0, 0);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// Weight chunk of one task: WFR 16-byte fragments, laid out as k-steps of
+// ROW fragments (NBB column blocks x 64 lanes) that sit `stride` fragments
+// apart in the packed global array.
+template <int WPT, int WFR, int ROW>
+__device__ __forceinline__ void load_weights(u32x4 (&wr)[WPT], const uint4 *src, int stride,
+                                             int tid) {
+    const u32x4 *v = reinterpret_cast<const u32x4 *>(src);
+#pragma unroll
+    for (int q = 0; q < WPT; ++q) {
+        const int idx = tid + q * 256;
+        if (WFR % 256 != 0 && idx >= WFR) continue;
+        const int s = idx / ROW;
+        wr[q] = v[static_cast<int64_t>(s) * stride + (idx - s * ROW)];
+    }
+}
+
+template <int WPT, int WFR>
+__device__ __forceinline__ void store_weights(uint4 *buf, const u32x4 (&wr)[WPT], int tid) {
+    u32x4 *v = reinterpret_cast<u32x4 *>(buf);
+#pragma unroll
+    for (int q = 0; q < WPT; ++q) {
+        const int idx = tid + q * 256;
+        if (WFR % 256 != 0 && idx >= WFR) continue;
+        v[idx] = wr[q];
+    }
+}
+
+// Keeps the compiler from moving memory operations across this point.
+__device__ __forceinline__ void mem_order() { asm volatile("" ::: "memory"); }
+
+// Keeps the instruction scheduler from moving anything across this point
+// (the prefetch loads stay ahead of the MFMAs that hide their latency).
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// Waits for this wave's LDS traffic, then joins the workgroup barrier.  Unlike
+// __syncthreads() it leaves global loads in flight, so the next task's
+// gathers and weight loads overlap the barrier and the MFMAs.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// LDS budget of a tiling: two weight buffers, or (after the main loop) the
+// FP32 output tile plus LayerNorm partials, then the neighbour-row table.
+template <class T, int MBW, int NBW, int WN, int KC, int S>
+struct ConvSmem {
+    static constexpr int E = Frag<T>::E;
+    static constexpr int KS = KC / (2 * E);
+    static constexpr int BM = 32 * MBW * (4 / WN);
+    static constexpr int NT = 32 * NBW * WN;
+    static constexpr int WFR = KS * (NBW * WN) * 64;  // 16-byte weight fragments per task
+    static constexpr int STG_LD = NT + 8;             // padded FP32 row of the output tile
+    static constexpr int TPR = NT / 8;                // epilogue threads per row
+    static constexpr int W_BYTES = 2 * S * WFR * 16;
+    static constexpr int STG_BYTES = BM * STG_LD * 4;
+    static constexpr int PART_BYTES = 2 * BM * TPR * 4;
+    static constexpr int REGION0 = W_BYTES > STG_BYTES + PART_BYTES ? W_BYTES : STG_BYTES + PART_BYTES;
+    static constexpr int ROWS_BYTES = BM * kMaxKvol * 4;
+    static constexpr int TOTAL = REGION0 + ROWS_BYTES + 128;
+    static constexpr int OCC = (TOTAL <= 80 * 1024 && MBW == 1) ? 2 : 1;
+};
+
+// T: uint16_t (bf16) or float.  XF: 0 = plain gathers, 1 = gathers with the
+// parent-repeat / slot-offset / affine+SiLU input transforms.
+//
+// Workgroup = 4 waves arranged WM x WN (WM = 4 / WN).  A wave owns MBW 32-row
+// blocks x NBW 32-column blocks of the output (BM = WM*MBW*32 rows and
+// NT = WN*NBW*32 columns per workgroup).  KC: Cin channels per task; a task is
+// one (present offset, Cin chunk).
+//
+// Pipeline: S consecutive tasks form a stage.  While the MFMAs consume stage
+// g (B fragments from LDS buffer g%2, A fragments in registers), the weight
+// chunks and gathers of stage g+1 land in registers; the weights then go to
+// buffer (g+1)%2.  A stage's weight loads precede its gathers, so the wait
+// before the weights' LDS store leaves the gathers in flight.
+//
+// Epilogue: the FP32 tile goes through LDS and is finished row-major (bias,
+// LayerNorm over the row, modulate, SiLU, residual) with 16-byte stores.
+template <class T, int MBW, int NBW, int WN, int KC, int XF, int S>
+__global__ void __launch_bounds__(256, (ConvSmem<T, MBW, NBW, WN, KC, S>::OCC))
+conv_mfma_kernel(ConvArgs a) {
+    using SM = ConvSmem<T, MBW, NBW, WN, KC, S>;
+    constexpr int E = Frag<T>::E;
+    constexpr int CPK = 2 * E;             // channels per k-step (both lane halves)
+    constexpr int KS = SM::KS;             // k-steps per task
+    constexpr int BM = SM::BM;
+    constexpr int NBB = NBW * WN;          // 32-column blocks per workgroup
+    constexpr int WFR = SM::WFR;
+    constexpr int WPT = (WFR + 255) / 256; // weight fragments per thread per task
+    __shared__ __align__(16) char smem[SM::TOTAL];
+    uint4 *wlds0 = reinterpret_cast<uint4 *>(smem);
+    uint4 *wlds1 = wlds0 + S * WFR;
+    float *stg = reinterpret_cast<float *>(smem);
+    float *part = reinterpret_cast<float *>(smem + SM::STG_BYTES);
+    int32_t *rows = reinterpret_cast<int32_t *>(smem + SM::REGION0);
+    int32_t *olist = rows + BM * kMaxKvol;
+    uint32_t *omask = reinterpret_cast<uint32_t *>(olist + kMaxKvol);
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave - (wave / WN) * WN;
+    const int tile = xcd_tile(blockIdx.x, gridDim.x);
+    const int64_t m0 = static_cast<int64_t>(tile) * BM;
+    const int nb0 = blockIdx.y * NBB;  // first 32-column block of this workgroup
+    const int nbtot = a.cout / 32;
+    const int kvol = a.kvol;
+    const int ksteps_total = a.cin / CPK;
+    const int chunks = a.cin / KC;
+    const int tile_rows = static_cast<int>(min(static_cast<int64_t>(BM), a.n_out - m0));
+
+    // ---- prologue: this tile's neighbour rows (-1 = missing) and offset mask
+    if (tid == 0) *omask = 0;
+    uint32_t my_mask = 0;
+    if (a.kmap) {
+        // The slice kmap[m0*kvol ..) is contiguous; stage it with independent
+        // 16-byte loads (kvol is 27 or 1, divisions by constants).
+        const int count = tile_rows * kvol;
+        const int4 *src = reinterpret_cast<const int4 *>(a.kmap + m0 * kvol);
+        constexpr int Q = (BM * kMaxKvol / 4 + 255) / 256;
+        int4 v[Q];
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+            const int e = (tid + q * 256) * 4;
+            if (e + 3 < count) {
+                v[q] = src[tid + q * 256];
+            } else {
+                v[q] = make_int4(-1, -1, -1, -1);
+                if (e < count) v[q].x = a.kmap[m0 * kvol + e];
+                if (e + 1 < count) v[q].y = a.kmap[m0 * kvol + e + 1];
+                if (e + 2 < count) v[q].z = a.kmap[m0 * kvol + e + 2];
+            }
+        }
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+            const int e0 = (tid + q * 256) * 4;
+            const int jv[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int e = e0 + k;
+                if (e >= BM * kvol) continue;
+                const bool valid = e < count && jv[k] >= 0 && jv[k] < a.n_src;
+                rows[e] = valid ? jv[k] : -1;
+                const int o = kvol == 27 ? e % 27 : 0;
+                if (valid) my_mask |= 1u << o;
+            }
+        }
+    } else {
+        for (int r = tid; r < BM; r += 256) {
+            const int64_t j = m0 + r;
+            const bool valid = r < tile_rows && j < a.n_src;
+            rows[r] = valid ? static_cast<int32_t>(j) : -1;
+            if (valid) my_mask = 1u;
+        }
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) my_mask |= __shfl_xor(my_mask, d, 64);
+    __syncthreads();
+    if (lane == 0 && my_mask) atomicOr(omask, my_mask);
+    __syncthreads();
+    const uint32_t mask = *omask;
+    if (tid == 0) {
+        int k = 0;
+        for (int o = 0; o < kvol; ++o)
+            if ((mask >> o) & 1u) olist[k++] = o;
+    }
+    __syncthreads();
+    const int ntasks = __popc(mask) * chunks;
+
+    f32x16 acc[MBW][NBW];
+#pragma unroll
+    for (int mb = 0; mb < MBW; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NBW; ++nb) acc[mb][nb] = f32x16{};
+
+    const uint4 *wg = static_cast<const uint4 *>(a.w);
+    const int half = lane >> 5;
+    const int row_base = wm * MBW * 32 + (lane & 31);  // + mb*32
+    const int32_t xbytes = static_cast<int32_t>(a.x_bytes < INT32_MAX ? a.x_bytes : INT32_MAX);
+
+    auto load_w = [&](int t, u32x4 (&wr)[WPT]) __attribute__((always_inline)) {
+        const int tq = t / chunks;
+        const int kcv = (t - tq * chunks) * KC;
+        load_weights<WPT, WFR, NBB * 64>(
+            wr, wg + ((static_cast<int64_t>(olist[tq]) * ksteps_total + kcv / CPK) * nbtot + nb0) * 64,
+            nbtot * 64, tid);
+    };
+    auto load_a = [&](int t, uint4 (&af)[MBW][KS]) __attribute__((always_inline)) {
+        const int tq = t / chunks;
+        const int kcv = (t - tq * chunks) * KC;
+        const int o = olist[tq];
+#pragma unroll
+        for (int mb = 0; mb < MBW; ++mb) {
+            const int32_t j = rows[(row_base + mb * 32) * kvol + o];
+#pragma unroll
+            for (int s = 0; s < KS; ++s) {
+                if constexpr (XF == 0)
+                    af[mb][s] = gather_plain<T>(a.x, xbytes, j, a.cin, kcv + s * CPK + half * E);
+                else
+                    af[mb][s] = load_fragment<T>(a, j, kcv + s * CPK + half * E);
+            }
+        }
+    };
+    auto compute = [&](const uint4 (&af)[MBW][KS], const uint4 *buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+            uint4 bw[NBW];
+#pragma unroll
+            for (int nb = 0; nb < NBW; ++nb) bw[nb] = buf[(s * NBB + wn * NBW + nb) * 64 + lane];
+#pragma unroll
+            for (int mb = 0; mb < MBW; ++mb)
+#pragma unroll
+                for (int nb = 0; nb < NBW; ++nb)
+                    acc[mb][nb] = mfma_step<T>(af[mb][s], bw[nb], acc[mb][nb]);
+        }
+    };
+
+    // Stage g = tasks g*S .. g*S+S-1 (indices clamped so every stage issues
+    // the same loads, which keeps the compiler's vmcnt waits exact).
+    auto load_stage = [&](int g, uint4 (&af)[S][MBW][KS], u32x4 (&wr)[S][WPT]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < S; ++i) load_w(min(g * S + i, ntasks - 1), wr[i]);
+        mem_order();
+#pragma unroll
+        for (int i = 0; i < S; ++i) load_a(min(g * S + i, ntasks - 1), af[i]);
+    };
+    auto store_stage = [&](uint4 *buf, const u32x4 (&wr)[S][WPT]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < S; ++i) store_weights<WPT, WFR>(buf + i * WFR, wr[i], tid);
+    };
+    auto compute_stage = [&](int g, const uint4 (&af)[S][MBW][KS], const uint4 *buf) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < S; ++i)
+            if (S == 1 || g * S + i < ntasks) compute(af[i], buf + i * WFR);
+    };
+
+    if (ntasks > 0) {
+        const int nstages = (ntasks + S - 1) / S;
+        uint4 a0[S][MBW][KS], a1[S][MBW][KS];
+        u32x4 wr[S][WPT];
+        load_stage(0, a0, wr);
+        store_stage(wlds0, wr);
+        lds_barrier();
+        for (int g = 0; g < nstages; g += 2) {
+            load_stage(min(g + 1, nstages - 1), a1, wr);
+            sched_fence();
+            compute_stage(g, a0, wlds0);
+            sched_fence();
+            store_stage(wlds1, wr);
+            lds_barrier();
+            if (g + 1 >= nstages) break;
+            load_stage(min(g + 2, nstages - 1), a0, wr);
+            sched_fence();
+            compute_stage(g + 1, a1, wlds1);
+            sched_fence();
+            store_stage(wlds0, wr);
+            lds_barrier();
+        }
+    }
+    // Every wave is done with the weight buffers before the tile reuses them.
+    __syncthreads();
+
+    // ---- epilogue: FP32 tile through LDS, then row-major finish ----
+#pragma unroll
+    for (int mb = 0; mb < MBW; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NBW; ++nb) {
+            const int col = (wn * NBW + nb) * 32 + (lane & 31);
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int rl = (wm * MBW + mb) * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+                stg[rl * SM::STG_LD + col] = acc[mb][nb][r];
+            }
+        }
+    __syncthreads();
+
+    constexpr int TPR = SM::TPR;
+    constexpr int RPP = 256 / TPR;  // rows per pass
+    constexpr int PASSES = (BM + RPP - 1) / RPP;
+    const int cg = tid % TPR, rsub = tid / TPR;
+    const bool active = rsub < RPP;
+    const int col0 = nb0 * 32 + cg * 8;  // global column of this thread's 8 values
+    float bias8[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) bias8[k] = a.bias ? a.bias[col0 + k] : 0.0f;
+
+    auto tile_vals = [&](int rl, float (&v)[8]) __attribute__((always_inline)) {
+        const float4 *p = reinterpret_cast<const float4 *>(stg + rl * SM::STG_LD + cg * 8);
+        const float4 x0 = p[0], x1 = p[1];
+        v[0] = x0.x + bias8[0]; v[1] = x0.y + bias8[1]; v[2] = x0.z + bias8[2]; v[3] = x0.w + bias8[3];
+        v[4] = x1.x + bias8[4]; v[5] = x1.y + bias8[5]; v[6] = x1.z + bias8[6]; v[7] = x1.w + bias8[7];
+    };
+
+    if (a.ln) {
+        // Row statistics (NT == cout): per-thread partials, then per-row sums.
+        float *psum = part, *psq = part + BM * TPR;
+        const float inv_c = 1.0f / static_cast<float>(a.cout);
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const int rl = p * RPP + rsub;
+            if (!active || rl >= BM) continue;
+            float v[8];
+            tile_vals(rl, v);
+            psum[rl * TPR + cg] = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+        }
+        __syncthreads();
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const int rl = p * RPP + rsub;
+            if (!active || rl >= BM) continue;
+            float m = 0.0f;
+            for (int g = 0; g < TPR; ++g) m += psum[rl * TPR + g];
+            m *= inv_c;
+            float v[8];
+            tile_vals(rl, v);
+            float q = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) q += (v[k] - m) * (v[k] - m);
+            psq[rl * TPR + cg] = q;
+        }
+        __syncthreads();
+    }
+
+    float lw[8], lb[8], ms[8], mh[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        lw[k] = a.ln_w ? a.ln_w[col0 + k] : 1.0f;
+        lb[k] = a.ln_b ? a.ln_b[col0 + k] : 0.0f;
+        ms[k] = a.mod_scale ? a.mod_scale[col0 + k] : 0.0f;
+        mh[k] = a.mod_shift ? a.mod_shift[col0 + k] : 0.0f;
+    }
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+        const int rl = p * RPP + rsub;
+        if (!active || rl >= tile_rows) continue;
+        float v[8];
+        tile_vals(rl, v);
+        if (a.ln) {
+            const float inv_c = 1.0f / static_cast<float>(a.cout);
+            float m = 0.0f, q = 0.0f;
+            for (int g = 0; g < TPR; ++g) {
+                m += part[rl * TPR + g];
+                q += part[BM * TPR + rl * TPR + g];
+            }
+            m *= inv_c;
+            const float rstd = rsqrtf(q * inv_c + a.eps);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                float t = (v[k] - m) * rstd * lw[k] + lb[k];
+                if (a.mod_scale) t = (t * ms[k] + t) + mh[k];
+                v[k] = t;
+            }
+        }
+        if (a.silu) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = silu(v[k]);
+        }
+        const int64_t off = (m0 + rl) * a.cout + col0;
+        if (a.y_bf16) {
+            if (a.residual) {
+                const uint4 r4 = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.residual) + off);
+                const uint32_t rw[4] = {r4.x, r4.y, r4.z, r4.w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    v[2 * k] += bf16_to_f32(static_cast<uint16_t>(rw[k] & 0xffffu));
+                    v[2 * k + 1] += bf16_to_f32(static_cast<uint16_t>(rw[k] >> 16));
+                }
+            }
+            uint32_t o4[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                o4[k] = static_cast<uint32_t>(f32_to_bf16(v[2 * k])) |
+                        (static_cast<uint32_t>(f32_to_bf16(v[2 * k + 1])) << 16);
+            *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.y) + off) = make_uint4(o4[0], o4[1], o4[2], o4[3]);
+        } else {
+            float4 *yp = reinterpret_cast<float4 *>(static_cast<float *>(a.y) + off);
+            if (a.residual) {
+                const float4 *rp = reinterpret_cast<const float4 *>(static_cast<const float *>(a.residual) + off);
+                const float4 r0 = rp[0], r1 = rp[1];
+                v[0] += r0.x; v[1] += r0.y; v[2] += r0.z; v[3] += r0.w;
+                v[4] += r1.x; v[5] += r1.y; v[6] += r1.z; v[7] += r1.w;
+            }
+            yp[0] = make_float4(v[0], v[1], v[2], v[3]);
+            yp[1] = make_float4(v[4], v[5], v[6], v[7]);
+        }
+    }
+}
+
+// Compiled tilings (tiling id -> MBW, NBW, WN, S); one task's weight chunk
+// is at most 32 KiB.
+//   0: 1,1,1,1  1: 1,1,2,1  2: 1,3,1,1  3: 1,2,2,1  4: 1,3,2,1  5: 1,4,2,1
+//   6: 2,1,2,1  7: 2,3,1,1  8: 2,2,2,1  9: 2,3,2,1  10: 1,4,1,2
+template <class T, int KC, int XF>
+KernelFn pick_tiling(int id) {
+#define S3DX_T(MBW, NBW, WN, S)                                                     \
+    if constexpr (KC * NBW * WN * 32 * static_cast<int>(sizeof(T)) <= 32768)        \
+        return conv_mfma_kernel<T, MBW, NBW, WN, KC, XF, S>;                         \
+    else                                                                             \
+        return nullptr;
+    switch (id) {
+    case 0: S3DX_T(1, 1, 1, 1)
+    case 1: S3DX_T(1, 1, 2, 1)
+    case 2: S3DX_T(1, 3, 1, 1)
+    case 3: S3DX_T(1, 2, 2, 1)
+    case 4: S3DX_T(1, 3, 2, 1)
+    case 5: S3DX_T(1, 4, 2, 1)
+    case 6: S3DX_T(2, 1, 2, 1)
+    case 7: S3DX_T(2, 3, 1, 1)
+    case 8: S3DX_T(2, 2, 2, 1)
+    case 9: S3DX_T(2, 3, 2, 1)
+    case 10: S3DX_T(1, 4, 1, 2)
+    default: return nullptr;
+    }
+#undef S3DX_T
+}
+
+template <class T, int KC>
+KernelFn pick_kc(int id, bool xf) {
+    return xf ? pick_tiling<T, KC, 1>(id) : pick_tiling<T, KC, 0>(id);
+}
+
+}  // namespace
+}  // namespace s3dx

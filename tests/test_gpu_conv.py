@@ -185,3 +185,34 @@ def test_deterministic_and_empty_rows(s3dx, O, W):
     a2 = gpu_conv(s3dx, x, kmap, n, w, 0, b, s3dx.BF16, 128)
     assert np.array_equal(a1, a2)
     assert np.allclose(a1[::7], W.round_bf16(np.broadcast_to(b, a1[::7].shape)), atol=0)
+
+
+TILINGS = {  # cout -> tiling ids whose workgroup spans the whole row
+    32: ["0"], 64: ["1", "6"], 96: ["2", "7"], 128: ["3", "8", "10"], 192: ["4", "9"], 256: ["5"]}
+
+
+@pytest.mark.parametrize("dtype", [0, 1])
+@pytest.mark.parametrize("cin,cout,tiling", [(c, o, t) for c, o in [(128, 128), (192, 192), (96, 96),
+                                                                   (64, 64), (256, 128), (64, 256)]
+                                             for t in TILINGS[o]])
+def test_row_block_tilings(s3dx, O, W, monkeypatch, dtype, cin, cout, tiling):
+    # Every compiled tiling on a tail-heavy row count, with the fused
+    # LayerNorm + SiLU + residual epilogue.
+    monkeypatch.setenv("S3DX_CONV_TILING", tiling)
+    coords = W.shells_union(0)[:2900]
+    n = coords.shape[0]
+    print(f"tiling {tiling} dtype={dtype} cin={cin} cout={cout}", flush=True)
+    kmap = O.kmap_subm3(coords, n)
+    x = W.normal_f32(15, 1, (n, cin))
+    w = W.conv_weight(15, 2, cin, cout)
+    b = W.normal_f32(15, 3, (cout,))
+    res = W.normal_f32(15, 4, (n, cout))
+
+    def setup(conv):
+        conv.set_layernorm(True, 1e-6)
+        conv.set_silu(True)
+
+    got = gpu_conv(s3dx, x, kmap, n, w, s3dx.WEIGHT_SLAT, b, dtype, cout, residual=res, setup=setup)
+    h = O.conv(rnd(s3dx, x, dtype), kmap, n, rnd(s3dx, w, dtype), 0, cout, b)
+    ref = O.silu(O.layernorm(h, 1e-6)) + rnd(s3dx, res, dtype)
+    assert rel_l2(got, ref) <= TOL[dtype] * (3 if dtype == 0 else 1)
