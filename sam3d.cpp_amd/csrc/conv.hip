@@ -186,11 +186,12 @@ KernelFn tiling_kernel(int id, bool bf, int kc, bool xf) {
     return bf ? pick_mfma_bf16(id, kc, xf) : pick_mfma_f32(id, kc, xf);
 }
 
-// Picks the workgroup tiling for nb 32-column blocks per workgroup.  Waves
-// that own all 128 columns of a row (tiling 10) gather each row once and
-// stream two tasks per stage; otherwise two 32-row blocks per wave halve the
-// LDS traffic per MFMA when that still leaves one workgroup per CU.
-// S3DX_CONV_TILING=<id> overrides the choice (tuning).
+// Picks the workgroup tiling for nb 32-column blocks per workgroup.  The
+// split-K kernel (no LDS traffic in its main loop) is preferred whenever it
+// is compiled for the shape; otherwise waves that own all 128 columns of a
+// row (tiling 10) gather each row once and stream two tasks per stage, and
+// two 32-row blocks per wave halve the LDS traffic per MFMA when that still
+// leaves one workgroup per CU.  S3DX_CONV_TILING=<id> overrides (tuning).
 const Tiling *choose_tiling(int64_t n_out, int nb, int ntiles, bool bf, int kc, bool xf) {
     if (const char *e = std::getenv("S3DX_CONV_TILING")) {
         const int id = std::atoi(e);
@@ -203,8 +204,9 @@ const Tiling *choose_tiling(int64_t n_out, int nb, int ntiles, bool bf, int kc, 
     for (const Tiling &t : kTilings) {
         if (t.cols() != nb * 32 || !tiling_kernel(t.id, bf, kc, xf)) continue;
         int rank;
-        if (t.wn == 1 && t.nbw == 4) rank = blocks(t) >= 192 ? 0 : 10;  // 32x128 wave tiles
-        else if (t.mbw == 2) rank = blocks(t) >= 256 ? 1 : 20;
+        if (t.splitk) rank = 0;
+        else if (t.wn == 1 && t.nbw == 4) rank = blocks(t) >= 192 ? 1 : 10;  // 32x128 wave tiles
+        else if (t.mbw == 2) rank = blocks(t) >= 256 ? 2 : 20;
         else rank = 5;
         if (rank < best_rank) {
             best_rank = rank;

@@ -40,14 +40,17 @@ using KernelFn = void (*)(ConvArgs);
 
 // Workgroup tilings of the MFMA kernel: 4 waves in WM x WN (WM = 4/WN), each
 // wave MBW x NBW blocks of 32x32 outputs.
+// Split-K tilings (splitk = 1): 128 rows x 32*nbw columns, each wave owning
+// the whole tile for a quarter of the k-steps.
 struct Tiling {
-    int id, mbw, nbw, wn;
-    int rows() const { return 32 * mbw * (4 / wn); }
+    int id, mbw, nbw, wn, splitk;
+    int rows() const { return splitk ? 128 : 32 * mbw * (4 / wn); }
     int cols() const { return 32 * nbw * wn; }
 };
 inline constexpr Tiling kTilings[] = {
-    {0, 1, 1, 1}, {1, 1, 1, 2}, {2, 1, 3, 1}, {3, 1, 2, 2}, {4, 1, 3, 2}, {5, 1, 4, 2},
-    {6, 2, 1, 2}, {7, 2, 3, 1}, {8, 2, 2, 2}, {9, 2, 3, 2}, {10, 1, 4, 1},
+    {0, 1, 1, 1, 0}, {1, 1, 1, 2, 0}, {2, 1, 3, 1, 0}, {3, 1, 2, 2, 0}, {4, 1, 3, 2, 0},
+    {5, 1, 4, 2, 0}, {6, 2, 1, 2, 0}, {7, 2, 3, 1, 0}, {8, 2, 2, 2, 0}, {9, 2, 3, 2, 0},
+    {10, 1, 4, 1, 0}, {11, 4, 4, 1, 1}, {12, 4, 2, 1, 1}, {13, 4, 3, 1, 1}, {14, 4, 1, 1, 1},
 };
 
 // MFMA kernel for tiling `id`, kc channels per task, xf input transforms;
@@ -207,6 +210,124 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// Row-major finish of a workgroup's FP32 output tile staged in LDS (stg,
+// BM rows x STG_LD floats): bias, LayerNorm over the row (the tile spans
+// cout), modulate, SiLU, residual; 8 consecutive columns per thread, stored
+// with 16-byte accesses.  `part` holds 2*BM*TPR floats of LayerNorm partials.
+template <int TPR, int BM, int STG_LD>
+__device__ __forceinline__ void finish_rows(const ConvArgs &a, const float *stg, float *part, int64_t m0,
+                                            int nb0, int tile_rows, int tid) {
+    constexpr int RPP = 256 / TPR;  // rows per pass
+    constexpr int PASSES = (BM + RPP - 1) / RPP;
+    const int cg = tid % TPR, rsub = tid / TPR;
+    const bool active = rsub < RPP;
+    const int col0 = nb0 * 32 + cg * 8;  // global column of this thread's 8 values
+    float bias8[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) bias8[k] = a.bias ? a.bias[col0 + k] : 0.0f;
+
+    auto tile_vals = [&](int rl, float (&v)[8]) __attribute__((always_inline)) {
+        const float4 *p = reinterpret_cast<const float4 *>(stg + rl * STG_LD + cg * 8);
+        const float4 x0 = p[0], x1 = p[1];
+        v[0] = x0.x + bias8[0]; v[1] = x0.y + bias8[1]; v[2] = x0.z + bias8[2]; v[3] = x0.w + bias8[3];
+        v[4] = x1.x + bias8[4]; v[5] = x1.y + bias8[5]; v[6] = x1.z + bias8[6]; v[7] = x1.w + bias8[7];
+    };
+
+    if (a.ln) {
+        // Row statistics (NT == cout): per-thread partials, then per-row sums.
+        float *psum = part, *psq = part + BM * TPR;
+        const float inv_c = 1.0f / static_cast<float>(a.cout);
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const int rl = p * RPP + rsub;
+            if (!active || rl >= BM) continue;
+            float v[8];
+            tile_vals(rl, v);
+            psum[rl * TPR + cg] = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+        }
+        __syncthreads();
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const int rl = p * RPP + rsub;
+            if (!active || rl >= BM) continue;
+            float m = 0.0f;
+            for (int g = 0; g < TPR; ++g) m += psum[rl * TPR + g];
+            m *= inv_c;
+            float v[8];
+            tile_vals(rl, v);
+            float q = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) q += (v[k] - m) * (v[k] - m);
+            psq[rl * TPR + cg] = q;
+        }
+        __syncthreads();
+    }
+
+    float lw[8], lb[8], ms[8], mh[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        lw[k] = a.ln_w ? a.ln_w[col0 + k] : 1.0f;
+        lb[k] = a.ln_b ? a.ln_b[col0 + k] : 0.0f;
+        ms[k] = a.mod_scale ? a.mod_scale[col0 + k] : 0.0f;
+        mh[k] = a.mod_shift ? a.mod_shift[col0 + k] : 0.0f;
+    }
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) {
+        const int rl = p * RPP + rsub;
+        if (!active || rl >= tile_rows) continue;
+        float v[8];
+        tile_vals(rl, v);
+        if (a.ln) {
+            const float inv_c = 1.0f / static_cast<float>(a.cout);
+            float m = 0.0f, q = 0.0f;
+            for (int g = 0; g < TPR; ++g) {
+                m += part[rl * TPR + g];
+                q += part[BM * TPR + rl * TPR + g];
+            }
+            m *= inv_c;
+            const float rstd = rsqrtf(q * inv_c + a.eps);
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                float t = (v[k] - m) * rstd * lw[k] + lb[k];
+                if (a.mod_scale) t = (t * ms[k] + t) + mh[k];
+                v[k] = t;
+            }
+        }
+        if (a.silu) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = silu(v[k]);
+        }
+        const int64_t off = (m0 + rl) * a.cout + col0;
+        if (a.y_bf16) {
+            if (a.residual) {
+                const uint4 r4 = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.residual) + off);
+                const uint32_t rw[4] = {r4.x, r4.y, r4.z, r4.w};
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    v[2 * k] += bf16_to_f32(static_cast<uint16_t>(rw[k] & 0xffffu));
+                    v[2 * k + 1] += bf16_to_f32(static_cast<uint16_t>(rw[k] >> 16));
+                }
+            }
+            uint32_t o4[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                o4[k] = static_cast<uint32_t>(f32_to_bf16(v[2 * k])) |
+                        (static_cast<uint32_t>(f32_to_bf16(v[2 * k + 1])) << 16);
+            *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.y) + off) = make_uint4(o4[0], o4[1], o4[2], o4[3]);
+        } else {
+            float4 *yp = reinterpret_cast<float4 *>(static_cast<float *>(a.y) + off);
+            if (a.residual) {
+                const float4 *rp = reinterpret_cast<const float4 *>(static_cast<const float *>(a.residual) + off);
+                const float4 r0 = rp[0], r1 = rp[1];
+                v[0] += r0.x; v[1] += r0.y; v[2] += r0.z; v[3] += r0.w;
+                v[4] += r1.x; v[5] += r1.y; v[6] += r1.z; v[7] += r1.w;
+            }
+            yp[0] = make_float4(v[0], v[1], v[2], v[3]);
+            yp[1] = make_float4(v[4], v[5], v[6], v[7]);
+        }
+    }
+}
+
 // LDS budget of a tiling: two weight buffers, or (after the main loop) the
 // FP32 output tile plus LayerNorm partials, then the neighbour-row table.
 template <class T, int MBW, int NBW, int WN, int KC, int S>
@@ -263,7 +384,8 @@ conv_mfma_kernel(ConvArgs a) {
     int32_t *olist = rows + BM * kMaxKvol;
     uint32_t *omask = reinterpret_cast<uint32_t *>(olist + kMaxKvol);
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     const int wm = wave / WN, wn = wave - (wave / WN) * WN;
     const int tile = xcd_tile(blockIdx.x, gridDim.x);
     const int64_t m0 = static_cast<int64_t>(tile) * BM;
@@ -366,20 +488,28 @@ conv_mfma_kernel(ConvArgs a) {
             }
         }
     };
+    // B fragments are read from LDS one k-step ahead of the MFMAs that use
+    // them (two register sets), so LDS latency hides behind MFMA issue.
     auto compute = [&](const uint4 (&af)[MBW][KS], const uint4 *buf) __attribute__((always_inline)) {
+        uint4 bw[2][NBW];
+#pragma unroll
+        for (int nb = 0; nb < NBW; ++nb) bw[0][nb] = buf[(wn * NBW + nb) * 64 + lane];
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
-            uint4 bw[NBW];
+            if (s + 1 < KS) {
 #pragma unroll
-            for (int nb = 0; nb < NBW; ++nb) bw[nb] = buf[(s * NBB + wn * NBW + nb) * 64 + lane];
+                for (int nb = 0; nb < NBW; ++nb)
+                    bw[(s + 1) & 1][nb] = buf[((s + 1) * NBB + wn * NBW + nb) * 64 + lane];
+            }
+            sched_fence();
 #pragma unroll
             for (int mb = 0; mb < MBW; ++mb)
 #pragma unroll
                 for (int nb = 0; nb < NBW; ++nb)
-                    acc[mb][nb] = mfma_step<T>(af[mb][s], bw[nb], acc[mb][nb]);
+                    acc[mb][nb] = mfma_step<T>(af[mb][s], bw[s & 1][nb], acc[mb][nb]);
+            sched_fence();
         }
     };
-
     // Stage g = tasks g*S .. g*S+S-1 (indices clamped so every stage issues
     // the same loads, which keeps the compiler's vmcnt waits exact).
     auto load_stage = [&](int g, uint4 (&af)[S][MBW][KS], u32x4 (&wr)[S][WPT]) __attribute__((always_inline)) {
@@ -439,122 +569,286 @@ conv_mfma_kernel(ConvArgs a) {
         }
     __syncthreads();
 
-    constexpr int TPR = SM::TPR;
-    constexpr int RPP = 256 / TPR;  // rows per pass
-    constexpr int PASSES = (BM + RPP - 1) / RPP;
-    const int cg = tid % TPR, rsub = tid / TPR;
-    const bool active = rsub < RPP;
-    const int col0 = nb0 * 32 + cg * 8;  // global column of this thread's 8 values
-    float bias8[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) bias8[k] = a.bias ? a.bias[col0 + k] : 0.0f;
+    finish_rows<SM::TPR, BM, SM::STG_LD>(a, stg, part, m0, nb0, tile_rows, tid);
+}
 
-    auto tile_vals = [&](int rl, float (&v)[8]) __attribute__((always_inline)) {
-        const float4 *p = reinterpret_cast<const float4 *>(stg + rl * SM::STG_LD + cg * 8);
-        const float4 x0 = p[0], x1 = p[1];
-        v[0] = x0.x + bias8[0]; v[1] = x0.y + bias8[1]; v[2] = x0.z + bias8[2]; v[3] = x0.w + bias8[3];
-        v[4] = x1.x + bias8[4]; v[5] = x1.y + bias8[5]; v[6] = x1.z + bias8[6]; v[7] = x1.w + bias8[7];
+// ---------------------------------------------------------------------------
+// Split-K variant: each of the 4 waves owns the whole 128 x (32*NB) output
+// tile (4 x NB accumulator blocks) but only k-steps s = wave (mod 4) of every
+// task, so each B fragment is used by one wave only and is loaded straight
+// from the packed weights (1 KiB contiguous per instruction).
+//
+// A (the gathered neighbour rows) is staged through LDS: the workgroup loads
+// a task's 128 rows x KC channels with consecutive lanes on consecutive
+// 16-byte pieces of one row, so every quarter-wave reads whole 128-byte
+// lines.  (Loading MFMA fragments straight from global memory puts 16
+// different rows in each quarter-wave and runs at about a quarter of the L1
+// rate.)  Rows sit at a padded stride, which keeps both the row-major stores
+// and the fragment reads free of bank conflicts.  Tasks run over all kvol
+// offsets (weights of the first task are requested before the kernel map is
+// staged); offsets absent from the tile skip their MFMAs.  The four partial
+// tiles are summed through LDS in a fixed order (deterministic), then
+// finished by the same row-major epilogue.
+// ---------------------------------------------------------------------------
+template <class T, int NB, int KC>
+struct SplitSmem {
+    static constexpr int BM = 128;
+    static constexpr int NT = 32 * NB;
+    static constexpr int ROWB = KC * static_cast<int>(sizeof(T));  // A bytes per row per task
+    static constexpr int A_LD = ROWB + 16;                          // padded LDS row
+    static constexpr int A_BYTES = 2 * BM * A_LD;                   // double buffer
+    static constexpr int STG_LD = NT + 8;
+    static constexpr int TPR = NT / 8;
+    static constexpr int RED_BYTES = 8 * NB * 16 * 64 * 4;  // 8 partial 32-row blocks
+    static constexpr int STG_BYTES = BM * STG_LD * 4;
+    static constexpr int PART_BYTES = 2 * BM * TPR * 4;
+    static constexpr int R0A = RED_BYTES > A_BYTES ? RED_BYTES : A_BYTES;
+    static constexpr int REGION0 = R0A > STG_BYTES + PART_BYTES ? R0A : STG_BYTES + PART_BYTES;
+    static constexpr int ROWS_BYTES = BM * kMaxKvol * 4;
+    static constexpr int TOTAL = REGION0 + ROWS_BYTES + 128;
+};
+
+template <class T, int NB, int KC, int XF>
+__global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
+    using SM = SplitSmem<T, NB, KC>;
+    constexpr int E = Frag<T>::E;
+    constexpr int CPK = 2 * E;
+    constexpr int KS = KC / CPK;  // k-steps per task
+    static_assert(KS % 4 == 0, "k-steps per task must split over 4 waves");
+    static_assert(SM::ROWB % 128 == 0, "A rows must cover whole 128-byte lines");
+    constexpr int KSW = KS / 4;   // k-steps per wave per task
+    constexpr int BM = SM::BM;
+    constexpr int PPR = SM::ROWB / 16;       // 16-byte pieces per row
+    constexpr int APT = BM * PPR / 256;      // pieces per thread per task
+    __shared__ __align__(16) char smem[SM::TOTAL];
+    float *stg = reinterpret_cast<float *>(smem);
+    float *part = reinterpret_cast<float *>(smem + SM::STG_BYTES);
+    float4 *red = reinterpret_cast<float4 *>(smem);
+    char *abuf = smem;
+    int32_t *rows = reinterpret_cast<int32_t *>(smem + SM::REGION0);
+    uint32_t *omask = reinterpret_cast<uint32_t *>(rows + BM * kMaxKvol);
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+    const int half = lane >> 5;
+    const int tile = xcd_tile(blockIdx.x, gridDim.x);
+    const int64_t m0 = static_cast<int64_t>(tile) * BM;
+    const int nb0 = blockIdx.y * NB;
+    const int nbtot = a.cout / 32;
+    const int kvol = a.kvol;
+    const int ksteps_total = a.cin / CPK;
+    const int chunks = a.cin / KC;
+    const int ntasks = kvol * chunks;
+    const int last = ntasks - 1;
+    const int tile_rows = static_cast<int>(min(static_cast<int64_t>(BM), a.n_out - m0));
+    const uint4 *wg = static_cast<const uint4 *>(a.w);
+    const int32_t xbytes = static_cast<int32_t>(a.x_bytes < INT32_MAX ? a.x_bytes : INT32_MAX);
+
+    auto load_b = [&](int t, uint4 (&bf)[KSW][NB]) __attribute__((always_inline)) {
+        const int o = t / chunks;
+        const int kc = t - o * chunks;
+        const int64_t ks0 = static_cast<int64_t>(o) * ksteps_total + kc * KS;
+#pragma unroll
+        for (int i = 0; i < KSW; ++i)
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+                bf[i][nb] = wg[((ks0 + wave + 4 * i) * nbtot + nb0 + nb) * 64 + lane];
+    };
+    // Row-major gather of task t: piece u = tid + 256 q is row u / PPR,
+    // channels kc*KC + (u % PPR)*E .. +E.
+    auto load_a = [&](int t, uint4 (&ra)[APT]) __attribute__((always_inline)) {
+        const int o = t / chunks;
+        const int kc = (t - o * chunks) * KC;
+#pragma unroll
+        for (int q = 0; q < APT; ++q) {
+            const int u = tid + q * 256;
+            const int32_t j = rows[(u / PPR) * kvol + o];
+            const int c0 = kc + (u % PPR) * E;
+            if constexpr (XF == 0) ra[q] = gather_plain<T>(a.x, xbytes, j, a.cin, c0);
+            else ra[q] = load_fragment<T>(a, j, c0);
+        }
+    };
+    auto store_a = [&](char *buf, const uint4 (&ra)[APT]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int q = 0; q < APT; ++q) {
+            const int u = tid + q * 256;
+            *reinterpret_cast<uint4 *>(buf + (u / PPR) * SM::A_LD + (u % PPR) * 16) = ra[q];
+        }
     };
 
-    if (a.ln) {
-        // Row statistics (NT == cout): per-thread partials, then per-row sums.
-        float *psum = part, *psq = part + BM * TPR;
-        const float inv_c = 1.0f / static_cast<float>(a.cout);
+    f32x16 acc[4][NB];
 #pragma unroll
-        for (int p = 0; p < PASSES; ++p) {
-            const int rl = p * RPP + rsub;
-            if (!active || rl >= BM) continue;
-            float v[8];
-            tile_vals(rl, v);
-            psum[rl * TPR + cg] = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f32x16{};
+    // A fragments of k-step (wave + 4 i) from an LDS buffer; lane: row
+    // mb*32 + lane%32, channels (wave + 4 i)*CPK + half*E .. +E.
+    auto compute = [&](const char *buf, const uint4 (&bf)[KSW][NB]) __attribute__((always_inline)) {
+        const char *base = buf + (lane & 31) * SM::A_LD + half * 16 + wave * (CPK * static_cast<int>(sizeof(T)));
+#pragma unroll
+        for (int i = 0; i < KSW; ++i) {
+            uint4 af[4];
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb)
+                af[mb] = *reinterpret_cast<const uint4 *>(base + mb * 32 * SM::A_LD +
+                                                          i * 4 * CPK * static_cast<int>(sizeof(T)));
+#pragma unroll
+            for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+                for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = mfma_step<T>(af[mb], bf[i][nb], acc[mb][nb]);
         }
-        __syncthreads();
+    };
+
+    uint4 b0[KSW][NB], b1[KSW][NB];
+    load_b(0, b0);  // independent of the kernel map: overlaps the staging below
+
+    // ---- stage this tile's neighbour rows (-1 = missing) and offset mask
+    if (tid == 0) *omask = 0;
+    uint32_t my_mask = 0;
+    if (a.kmap) {
+        const int count = tile_rows * kvol;
+        const int4 *src = reinterpret_cast<const int4 *>(a.kmap + m0 * kvol);
+        constexpr int Q = (BM * kMaxKvol / 4 + 255) / 256;
+        int4 v[Q];
 #pragma unroll
-        for (int p = 0; p < PASSES; ++p) {
-            const int rl = p * RPP + rsub;
-            if (!active || rl >= BM) continue;
-            float m = 0.0f;
-            for (int g = 0; g < TPR; ++g) m += psum[rl * TPR + g];
-            m *= inv_c;
-            float v[8];
-            tile_vals(rl, v);
-            float q = 0.0f;
-#pragma unroll
-            for (int k = 0; k < 8; ++k) q += (v[k] - m) * (v[k] - m);
-            psq[rl * TPR + cg] = q;
+        for (int q = 0; q < Q; ++q) {
+            const int e = (tid + q * 256) * 4;
+            if (e + 3 < count) {
+                v[q] = src[tid + q * 256];
+            } else {
+                v[q] = make_int4(-1, -1, -1, -1);
+                if (e < count) v[q].x = a.kmap[m0 * kvol + e];
+                if (e + 1 < count) v[q].y = a.kmap[m0 * kvol + e + 1];
+                if (e + 2 < count) v[q].z = a.kmap[m0 * kvol + e + 2];
+            }
         }
-        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+            const int e0 = (tid + q * 256) * 4;
+            const int jv[4] = {v[q].x, v[q].y, v[q].z, v[q].w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int e = e0 + k;
+                if (e >= BM * kvol) continue;
+                const bool valid = e < count && jv[k] >= 0 && jv[k] < a.n_src;
+                rows[e] = valid ? jv[k] : -1;
+                const int o = kvol == 27 ? e % 27 : 0;
+                if (valid) my_mask |= 1u << o;
+            }
+        }
+    } else {
+        for (int r = tid; r < BM; r += 256) {
+            const int64_t j = m0 + r;
+            const bool valid = r < tile_rows && j < a.n_src;
+            rows[r] = valid ? static_cast<int32_t>(j) : -1;
+            if (valid) my_mask = 1u;
+        }
+    }
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) my_mask |= __shfl_xor(my_mask, d, 64);
+    __syncthreads();
+    if (lane == 0 && my_mask) atomicOr(omask, my_mask);
+    __syncthreads();
+    const uint32_t mask = *omask;
+
+    // ---- main loop.  Entering task t: A(t) in LDS buffer t%2, A(t+1) on its
+    // way into ra, B(t) in registers, B(t+1) on its way.
+    {
+        char *buf0 = abuf, *buf1 = abuf + BM * SM::A_LD;
+        uint4 ra[APT];
+        load_a(0, ra);
+        store_a(buf0, ra);
+        load_a(min(1, last), ra);
+        load_b(min(1, last), b1);
+        lds_barrier();
+        // Two tasks per trip and no exit in between (an odd task count runs
+        // one padding task with its MFMAs masked off), so the compiler's
+        // wait counts see one steady load pattern.
+        for (int t = 0; t < ntasks; t += 2) {
+            if ((mask >> (t / chunks)) & 1u) compute(buf0, b0);
+            sched_fence();
+            store_a(buf1, ra);
+            load_a(min(t + 2, last), ra);
+            load_b(min(t + 2, last), b0);
+            lds_barrier();
+            if (t + 1 < ntasks && ((mask >> ((t + 1) / chunks)) & 1u)) compute(buf1, b1);
+            sched_fence();
+            store_a(buf0, ra);
+            load_a(min(t + 3, last), ra);
+            load_b(min(t + 3, last), b1);
+            lds_barrier();
+        }
     }
 
-    float lw[8], lb[8], ms[8], mh[8];
+    // ---- reduce the 4 partial tiles through LDS, 64 rows per phase ----
+    // Phase p: every wave writes its partial blocks 2p, 2p+1 as float4
+    // [nb][4][lane] into slot (h * 4 + writer) (16-byte lane stride,
+    // conflict-free); then the 2*NB (block, column-block) pairs of the phase
+    // are summed over the 4 writers, pair q by wave q % 4, into registers.
+    // Accumulators are only indexed by compile-time constants here.
+    constexpr int PPW = (2 * NB + 3) / 4;  // pairs per wave per phase
+    float fin[2][PPW][16];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        lw[k] = a.ln_w ? a.ln_w[col0 + k] : 1.0f;
-        lb[k] = a.ln_b ? a.ln_b[col0 + k] : 0.0f;
-        ms[k] = a.mod_scale ? a.mod_scale[col0 + k] : 0.0f;
-        mh[k] = a.mod_shift ? a.mod_shift[col0 + k] : 0.0f;
-    }
+    for (int p = 0; p < 2; ++p) {
+        if (p) __syncthreads();
 #pragma unroll
-    for (int p = 0; p < PASSES; ++p) {
-        const int rl = p * RPP + rsub;
-        if (!active || rl >= tile_rows) continue;
-        float v[8];
-        tile_vals(rl, v);
-        if (a.ln) {
-            const float inv_c = 1.0f / static_cast<float>(a.cout);
-            float m = 0.0f, q = 0.0f;
-            for (int g = 0; g < TPR; ++g) {
-                m += part[rl * TPR + g];
-                q += part[BM * TPR + rl * TPR + g];
-            }
-            m *= inv_c;
-            const float rstd = rsqrtf(q * inv_c + a.eps);
+        for (int h = 0; h < 2; ++h) {
+            float4 *slot = red + (h * 4 + wave) * (NB * 4 * 64);
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                float t = (v[k] - m) * rstd * lw[k] + lb[k];
-                if (a.mod_scale) t = (t * ms[k] + t) + mh[k];
-                v[k] = t;
-            }
+            for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+                    slot[(nb * 4 + g) * 64 + lane] =
+                        make_float4(acc[2 * p + h][nb][4 * g], acc[2 * p + h][nb][4 * g + 1],
+                                    acc[2 * p + h][nb][4 * g + 2], acc[2 * p + h][nb][4 * g + 3]);
         }
-        if (a.silu) {
+        __syncthreads();
 #pragma unroll
-            for (int k = 0; k < 8; ++k) v[k] = silu(v[k]);
-        }
-        const int64_t off = (m0 + rl) * a.cout + col0;
-        if (a.y_bf16) {
-            if (a.residual) {
-                const uint4 r4 = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.residual) + off);
-                const uint32_t rw[4] = {r4.x, r4.y, r4.z, r4.w};
+        for (int i = 0; i < PPW; ++i) {
+            const int q = wave + 4 * i;
+            if (q >= 2 * NB) continue;
+            const int h = q / NB, nb = q - h * NB;
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    v[2 * k] += bf16_to_f32(static_cast<uint16_t>(rw[k] & 0xffffu));
-                    v[2 * k + 1] += bf16_to_f32(static_cast<uint16_t>(rw[k] >> 16));
+            for (int g = 0; g < 4; ++g) {
+                float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                for (int src = 0; src < 4; ++src) {
+                    const float4 v = red[(h * 4 + src) * (NB * 4 * 64) + (nb * 4 + g) * 64 + lane];
+                    s.x += v.x;
+                    s.y += v.y;
+                    s.z += v.z;
+                    s.w += v.w;
                 }
+                fin[p][i][4 * g] = s.x;
+                fin[p][i][4 * g + 1] = s.y;
+                fin[p][i][4 * g + 2] = s.z;
+                fin[p][i][4 * g + 3] = s.w;
             }
-            uint32_t o4[4];
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-                o4[k] = static_cast<uint32_t>(f32_to_bf16(v[2 * k])) |
-                        (static_cast<uint32_t>(f32_to_bf16(v[2 * k + 1])) << 16);
-            *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.y) + off) = make_uint4(o4[0], o4[1], o4[2], o4[3]);
-        } else {
-            float4 *yp = reinterpret_cast<float4 *>(static_cast<float *>(a.y) + off);
-            if (a.residual) {
-                const float4 *rp = reinterpret_cast<const float4 *>(static_cast<const float *>(a.residual) + off);
-                const float4 r0 = rp[0], r1 = rp[1];
-                v[0] += r0.x; v[1] += r0.y; v[2] += r0.z; v[3] += r0.w;
-                v[4] += r1.x; v[5] += r1.y; v[6] += r1.z; v[7] += r1.w;
-            }
-            yp[0] = make_float4(v[0], v[1], v[2], v[3]);
-            yp[1] = make_float4(v[4], v[5], v[6], v[7]);
         }
     }
+    __syncthreads();
+    // Summed blocks -> FP32 tile in LDS (the tile aliases the slots).
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int i = 0; i < PPW; ++i) {
+            const int q = wave + 4 * i;
+            if (q >= 2 * NB) continue;
+            const int h = q / NB, nb = q - h * NB;
+            const int col = nb * 32 + (lane & 31);
+            const int rb = (2 * p + h) * 32 + 4 * half;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) stg[(rb + 8 * (r >> 2) + (r & 3)) * SM::STG_LD + col] = fin[p][i][r];
+        }
+    __syncthreads();
+    finish_rows<SM::TPR, BM, SM::STG_LD>(a, stg, part, m0, nb0, tile_rows, tid);
 }
 
 // Compiled tilings (tiling id -> MBW, NBW, WN, S); one task's weight chunk
 // is at most 32 KiB.
 //   0: 1,1,1,1  1: 1,1,2,1  2: 1,3,1,1  3: 1,2,2,1  4: 1,3,2,1  5: 1,4,2,1
 //   6: 2,1,2,1  7: 2,3,1,1  8: 2,2,2,1  9: 2,3,2,1  10: 1,4,1,2
+//   11-14: split-K, 128 rows x 128 / 64 / 96 / 32 columns
 template <class T, int KC, int XF>
 KernelFn pick_tiling(int id) {
 #define S3DX_T(MBW, NBW, WN, S)                                                     \
@@ -574,6 +868,17 @@ KernelFn pick_tiling(int id) {
     case 8: S3DX_T(2, 2, 2, 1)
     case 9: S3DX_T(2, 3, 2, 1)
     case 10: S3DX_T(1, 4, 1, 2)
+    case 11: case 12: case 13: case 14: {
+        constexpr int KS = KC / (2 * Frag<T>::E);
+        if constexpr (KS % 4 == 0) {
+            if (id == 11) return conv_splitk_kernel<T, 4, KC, XF>;
+            if (id == 12) return conv_splitk_kernel<T, 2, KC, XF>;
+            if (id == 13) return conv_splitk_kernel<T, 3, KC, XF>;
+            return conv_splitk_kernel<T, 1, KC, XF>;
+        } else {
+            return nullptr;
+        }
+    }
     default: return nullptr;
     }
 #undef S3DX_T

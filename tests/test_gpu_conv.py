@@ -187,13 +187,14 @@ def test_deterministic_and_empty_rows(s3dx, O, W):
     assert np.allclose(a1[::7], W.round_bf16(np.broadcast_to(b, a1[::7].shape)), atol=0)
 
 
-TILINGS = {  # cout -> tiling ids whose workgroup spans the whole row
-    32: ["0"], 64: ["1", "6"], 96: ["2", "7"], 128: ["3", "8", "10"], 192: ["4", "9"], 256: ["5"]}
+TILINGS = {  # cout -> tiling ids whose workgroup spans the whole row (11-14: split-K)
+    32: ["0", "14"], 64: ["1", "6", "12"], 96: ["2", "7", "13"], 128: ["3", "8", "10", "11"],
+    192: ["4", "9"], 256: ["5"]}
 
 
 @pytest.mark.parametrize("dtype", [0, 1])
 @pytest.mark.parametrize("cin,cout,tiling", [(c, o, t) for c, o in [(128, 128), (192, 192), (96, 96),
-                                                                   (64, 64), (256, 128), (64, 256)]
+                                                                   (64, 64), (256, 128), (64, 256), (64, 32)]
                                              for t in TILINGS[o]])
 def test_row_block_tilings(s3dx, O, W, monkeypatch, dtype, cin, cout, tiling):
     # Every compiled tiling on a tail-heavy row count, with the fused
