@@ -638,42 +638,54 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
     const int kvol = a.kvol;
     const int ksteps_total = a.cin / CPK;
     const int chunks = a.cin / KC;
-    const int ntasks = kvol * chunks;
-    const int last = ntasks - 1;
     const int tile_rows = static_cast<int>(min(static_cast<int64_t>(BM), a.n_out - m0));
     const uint4 *wg = static_cast<const uint4 *>(a.w);
     const int32_t xbytes = static_cast<int32_t>(a.x_bytes < INT32_MAX ? a.x_bytes : INT32_MAX);
 
-    auto load_b = [&](int t, uint4 (&bf)[KSW][NB]) __attribute__((always_inline)) {
-        const int o = t / chunks;
-        const int kc = t - o * chunks;
-        const int64_t ks0 = static_cast<int64_t>(o) * ksteps_total + kc * KS;
+    // Tasks are the (present offset, Cin chunk) pairs in ascending order.  A
+    // cursor walks them in scalar registers: the offsets not yet visited as a
+    // bit mask, the current offset and chunk.  Past the last task it stays
+    // on the last one (prefetches beyond the end reload it harmlessly).
+    struct Cursor {
+        uint32_t rest;
+        int o, kc;
+    };
+    auto advance = [&](Cursor &c) __attribute__((always_inline)) {
+        const bool wrap = c.kc + 1 == chunks;
+        const bool more = c.rest != 0u;
+        const int next_o = __builtin_ctz(c.rest | 0x80000000u);
+        c.o = wrap && more ? next_o : c.o;
+        c.kc = wrap ? (more ? 0 : c.kc) : c.kc + 1;
+        c.rest = wrap && more ? (c.rest & (c.rest - 1u)) : c.rest;
+    };
+    auto load_b = [&](const Cursor &c, uint4 (&bf)[KSW][NB]) __attribute__((always_inline)) {
+        const int64_t ks0 = static_cast<int64_t>(c.o) * ksteps_total + c.kc * KS;
 #pragma unroll
         for (int i = 0; i < KSW; ++i)
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb)
                 bf[i][nb] = wg[((ks0 + wave + 4 * i) * nbtot + nb0 + nb) * 64 + lane];
     };
-    // Row-major gather of task t: piece u = tid + 256 q is row u / PPR,
-    // channels kc*KC + (u % PPR)*E .. +E.
-    auto load_a = [&](int t, uint4 (&ra)[APT]) __attribute__((always_inline)) {
-        const int o = t / chunks;
-        const int kc = (t - o * chunks) * KC;
+    // Row-major gather: piece u = tid + 256 q is row u / PPR, channels
+    // kc*KC + (u % PPR)*E .. +E.  The row indices come from the staged map.
+    auto rows_of = [&](const Cursor &c, int32_t (&jn)[APT]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int q = 0; q < APT; ++q) {
-            const int u = tid + q * 256;
-            const int32_t j = rows[(u / PPR) * kvol + o];
-            const int c0 = kc + (u % PPR) * E;
-            if constexpr (XF == 0) ra[q] = gather_plain<T>(a.x, xbytes, j, a.cin, c0);
-            else ra[q] = load_fragment<T>(a, j, c0);
-        }
+        for (int q = 0; q < APT; ++q) jn[q] = rows[((tid + q * 256) / PPR) * kvol + c.o];
     };
-    auto store_a = [&](char *buf, const uint4 (&ra)[APT]) __attribute__((always_inline)) {
+    auto gather = [&](const Cursor &c, int32_t j, int q) __attribute__((always_inline)) {
+        const int c0 = c.kc * KC + ((tid + q * 256) % PPR) * E;
+        if constexpr (XF == 0) return gather_plain<T>(a.x, xbytes, j, a.cin, c0);
+        else return load_fragment<T>(a, j, c0);
+    };
+    auto load_a = [&](const Cursor &c, uint4 (&ra)[APT]) __attribute__((always_inline)) {
+        int32_t jn[APT];
+        rows_of(c, jn);
 #pragma unroll
-        for (int q = 0; q < APT; ++q) {
-            const int u = tid + q * 256;
-            *reinterpret_cast<uint4 *>(buf + (u / PPR) * SM::A_LD + (u % PPR) * 16) = ra[q];
-        }
+        for (int q = 0; q < APT; ++q) ra[q] = gather(c, jn[q], q);
+    };
+    auto a_slot = [&](char *buf, int q) __attribute__((always_inline)) {
+        const int u = tid + q * 256;
+        return reinterpret_cast<uint4 *>(buf + (u / PPR) * SM::A_LD + (u % PPR) * 16);
     };
 
     f32x16 acc[4][NB];
@@ -681,26 +693,63 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
     for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f32x16{};
-    // A fragments of k-step (wave + 4 i) from an LDS buffer; lane: row
-    // mb*32 + lane%32, channels (wave + 4 i)*CPK + half*E .. +E.
-    auto compute = [&](const char *buf, const uint4 (&bf)[KSW][NB]) __attribute__((always_inline)) {
+    // A fragments of k-step (wave + 4 i) from an LDS buffer (lane: row
+    // mb*32 + lane%32, channels (wave + 4 i)*CPK + half*E .. +E).
+    auto read_frags = [&](const char *buf, uint4 (&af)[KSW][4]) __attribute__((always_inline)) {
         const char *base = buf + (lane & 31) * SM::A_LD + half * 16 + wave * (CPK * static_cast<int>(sizeof(T)));
 #pragma unroll
-        for (int i = 0; i < KSW; ++i) {
-            uint4 af[4];
+        for (int i = 0; i < KSW; ++i)
 #pragma unroll
             for (int mb = 0; mb < 4; ++mb)
-                af[mb] = *reinterpret_cast<const uint4 *>(base + mb * 32 * SM::A_LD +
-                                                          i * 4 * CPK * static_cast<int>(sizeof(T)));
+                af[i][mb] = *reinterpret_cast<const uint4 *>(base + mb * 32 * SM::A_LD +
+                                                             i * 4 * CPK * static_cast<int>(sizeof(T)));
+    };
+    auto mfmas = [&](const uint4 (&af)[KSW][4], const uint4 (&bf)[KSW][NB]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < KSW; ++i)
 #pragma unroll
             for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-                for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = mfma_step<T>(af[mb], bf[i][nb], acc[mb][nb]);
-        }
+                for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = mfma_step<T>(af[i][mb], bf[i][nb], acc[mb][nb]);
     };
 
-    uint4 b0[KSW][NB], b1[KSW][NB];
-    load_b(0, b0);  // independent of the kernel map: overlaps the staging below
+    // One task body: MFMAs of task t (A from LDS buffer rbuf, B in bc); store
+    // A(t+1) (in ra) to wbuf; issue the gathers and weight loads of task t+2
+    // (cursor nx) into ra and bc.  Instruction order: this task's fragment
+    // reads, the next gather's row-index reads, the first half of the MFMAs,
+    // then MFMAs alternating with (LDS store of a piece, gather into its
+    // registers), the weight loads last (they overwrite this task's B).
+    constexpr int MPS = sizeof(T) == 2 ? 1 : 4;  // MFMA instructions per fragment pair
+    constexpr int NMF = KSW * 4 * NB * MPS;
+    constexpr int M0 = NMF / 2;
+    constexpr int MI = (NMF - M0) / APT;
+    constexpr int MR = NMF - M0 - MI * APT;
+    auto body = [&](const char *rbuf, uint4 (&bc)[KSW][NB], char *wbuf, uint4 (&ra)[APT], Cursor &nx)
+        __attribute__((always_inline)) {
+        uint4 af[KSW][4];
+        read_frags(rbuf, af);
+        int32_t jn[APT];
+        rows_of(nx, jn);
+        mfmas(af, bc);
+#pragma unroll
+        for (int q = 0; q < APT; ++q) {
+            *a_slot(wbuf, q) = ra[q];
+            ra[q] = gather(nx, jn[q], q);
+        }
+        load_b(nx, bc);
+        __builtin_amdgcn_sched_group_barrier(0x100, KSW * 4, 0);  // DS read: fragments
+        __builtin_amdgcn_sched_group_barrier(0x100, APT, 0);      // DS read: row indices
+        __builtin_amdgcn_sched_group_barrier(0x008, M0, 0);       // MFMA
+#pragma unroll
+        for (int q = 0; q < APT; ++q) {
+            if constexpr (MI > 0) __builtin_amdgcn_sched_group_barrier(0x008, MI, 0);
+            __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);    // DS write
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);    // VMEM read: gather
+        }
+        if constexpr (MR > 0) __builtin_amdgcn_sched_group_barrier(0x008, MR, 0);
+        __builtin_amdgcn_sched_group_barrier(0x020, KSW * NB, 0); // VMEM read: weights
+        advance(nx);
+    };
 
     // ---- stage this tile's neighbour rows (-1 = missing) and offset mask
     if (tid == 0) *omask = 0;
@@ -749,33 +798,39 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
     __syncthreads();
     if (lane == 0 && my_mask) atomicOr(omask, my_mask);
     __syncthreads();
-    const uint32_t mask = *omask;
+    const uint32_t mask = __builtin_amdgcn_readfirstlane(*omask);
+    const int ntasks = __popc(mask) * chunks;
 
     // ---- main loop.  Entering task t: A(t) in LDS buffer t%2, A(t+1) on its
-    // way into ra, B(t) in registers, B(t+1) on its way.
-    {
+    // way into ra, B(t) and B(t+1) in registers or on their way.
+    if (ntasks > 0) {
         char *buf0 = abuf, *buf1 = abuf + BM * SM::A_LD;
+        uint4 b0[KSW][NB], b1[KSW][NB];
         uint4 ra[APT];
-        load_a(0, ra);
-        store_a(buf0, ra);
-        load_a(min(1, last), ra);
-        load_b(min(1, last), b1);
+        Cursor nx{mask, -1, chunks - 1};
+        advance(nx);  // task 0
+        load_a(nx, ra);
+        load_b(nx, b0);
+#pragma unroll
+        for (int q = 0; q < APT; ++q) *a_slot(buf0, q) = ra[q];
+        advance(nx);  // task 1
+        load_a(nx, ra);
+        load_b(nx, b1);
+        advance(nx);  // task 2
         lds_barrier();
-        // Two tasks per trip and no exit in between (an odd task count runs
-        // one padding task with its MFMAs masked off), so the compiler's
-        // wait counts see one steady load pattern.
-        for (int t = 0; t < ntasks; t += 2) {
-            if ((mask >> (t / chunks)) & 1u) compute(buf0, b0);
-            sched_fence();
-            store_a(buf1, ra);
-            load_a(min(t + 2, last), ra);
-            load_b(min(t + 2, last), b0);
+        // Two tasks per trip with no exit in between (an odd count finishes
+        // with one compute-only task), so each body is one scheduling region
+        // and the wait counts see one steady load pattern.
+        for (int t = 0; t + 1 < ntasks; t += 2) {
+            body(buf0, b0, buf1, ra, nx);
             lds_barrier();
-            if (t + 1 < ntasks && ((mask >> ((t + 1) / chunks)) & 1u)) compute(buf1, b1);
-            sched_fence();
-            store_a(buf0, ra);
-            load_a(min(t + 3, last), ra);
-            load_b(min(t + 3, last), b1);
+            body(buf1, b1, buf0, ra, nx);
+            lds_barrier();
+        }
+        if (ntasks & 1) {
+            uint4 af[KSW][4];
+            read_frags(buf0, af);
+            mfmas(af, b0);
             lds_barrier();
         }
     }
