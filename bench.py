@@ -246,7 +246,8 @@ def main():
         "roofline": {
             "bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
             "frac": achieved / PEAK_BF16_TFLOPS, "traffic": traffic,
-            "kernel": "conv_mfma_kernel<bf16, NB=4, KC=128>",
+            "kernel": "conv_splitk_kernel (bf16)",
+            "plan": {"conv1": bf.conv1.plan(n, n), "conv2": bf.conv2.plan(n, n)},
         },
         "kmap_roofline": {
             "bound": "hbm", "achieved": n * KMAP_BYTES_PER_VOXEL / (kmap_avg * 1e-3) / 1e9,

@@ -70,6 +70,7 @@ SIGNATURES = {
     "s3dx_conv_set_layernorm": (_u32, [_vp, _i32, _f32, _vp, _vp, _vp, _vp], True),
     "s3dx_conv_set_silu": (_u32, [_vp, _i32], True),
     "s3dx_conv_run": (_u32, [_vp, _vp, _i64, _vp, _i64, _vp, _vp, _i32, _vp], True),
+    "s3dx_conv_plan": (_u32, [_vp, _i64, _i64, C.c_char_p, _u64], True),
     "s3dx_layernorm_rows": (_u32, [_vp, _i32, _i64, _i32, _f32, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp], True),
     "s3dx_groupnorm_workspace_size": (_u32, [_i64, _i32, _i32, C.POINTER(_u64)], True),
     "s3dx_groupnorm_stats": (_u32, [_vp, _i32, _i64, _i32, _i32, _f32, _vp, _vp, _vp, _vp, _vp, _u64, _vp], True),
@@ -355,6 +356,12 @@ class SparseConv:
     def set_silu(self, enable: bool = True):
         call("s3dx_conv_set_silu", _vp(self.handle), _i32(int(enable)))
         return self
+
+    def plan(self, n_in: int, n_out: int) -> str:
+        """The kernel variant run() launches for these row counts (host only)."""
+        buf = C.create_string_buffer(256)
+        call("s3dx_conv_plan", _vp(self.handle), _i64(n_in), _i64(n_out), buf, len(buf))
+        return buf.value.decode()
 
     def run(self, x: DeviceArray, n_in: int, kmap, n_out: int, y: DeviceArray, y_dtype: int = None,
             residual: DeviceArray = None, stream=None):

@@ -27,6 +27,8 @@
 //                  weight packed in the same permuted order.
 #include "conv_kernels.hpp"
 
+#include <cstdio>
+
 #include <cstdlib>
 #include <memory>
 #include <vector>
@@ -187,11 +189,12 @@ KernelFn tiling_kernel(int id, bool bf, int kc, bool xf) {
 }
 
 // Picks the workgroup tiling for nb 32-column blocks per workgroup.  The
-// split-K kernel (no LDS traffic in its main loop) is preferred whenever it
-// is compiled for the shape; otherwise waves that own all 128 columns of a
-// row (tiling 10) gather each row once and stream two tasks per stage, and
-// two 32-row blocks per wave halve the LDS traffic per MFMA when that still
-// leaves one workgroup per CU.  S3DX_CONV_TILING=<id> overrides (tuning).
+// split-K kernel (each weight fragment loaded once per workgroup, straight
+// into the one wave that uses it) is preferred whenever it is compiled for
+// the shape; otherwise waves that own all 128 columns of a row (tiling 10)
+// gather each row once and stream two tasks per stage, and two 32-row blocks
+// per wave halve the LDS traffic per MFMA when that still leaves one
+// workgroup per CU.  S3DX_CONV_TILING=<id> overrides (tuning).
 const Tiling *choose_tiling(int64_t n_out, int nb, int ntiles, bool bf, int kc, bool xf) {
     if (const char *e = std::getenv("S3DX_CONV_TILING")) {
         const int id = std::atoi(e);
@@ -214,6 +217,39 @@ const Tiling *choose_tiling(int64_t n_out, int nb, int ntiles, bool bf, int kc, 
         }
     }
     return best;
+}
+
+// Kernel choice of one launch, shared by s3dx_conv_run and s3dx_conv_plan.
+struct LaunchPlan {
+    bool mfma = false;      // MFMA kernel (else the generic VALU kernel)
+    bool xf = false;        // gathers with input transforms / 64-bit offsets
+    bool fused_ln = false;  // LayerNorm in the MFMA epilogue
+    const Tiling *tl = nullptr;
+    KernelFn fn = nullptr;
+    dim3 grid;
+};
+
+LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bool aligned16) {
+    LaunchPlan p;
+    const bool bf = conv->dtype == S3DX_BF16;
+    p.mfma = conv->mfma && aligned16;
+    if (p.mfma) {
+        p.fused_ln = conv->ln && conv->nb * 32 == conv->cout;
+        // Buffer-resource gathers address at most 2 GiB; larger inputs and
+        // the input transforms take the XF=1 variant.
+        p.xf = conv->gather_parent || conv->pre_scale != nullptr || x_bytes >= (int64_t(1) << 31);
+        const int ntiles = conv->cout / (32 * conv->nb);
+        p.tl = choose_tiling(n_out, conv->nb, ntiles, bf, conv->kc, p.xf);
+        require(p.tl != nullptr, "no MFMA kernel for this shape");
+        p.fn = tiling_kernel(p.tl->id, bf, conv->kc, p.xf);
+        require(p.fn != nullptr, "no MFMA kernel for this shape");
+        const int64_t mt = (n_out + p.tl->rows() - 1) / p.tl->rows();
+        p.grid = dim3(static_cast<unsigned>(mt), static_cast<unsigned>(ntiles));
+    } else {
+        p.grid = dim3(static_cast<unsigned>((n_out + kGM - 1) / kGM),
+                      static_cast<unsigned>((conv->cout + kGN - 1) / kGN));
+    }
+    return p;
 }
 
 float *upload_f32(const float *host, size_t count) {
@@ -404,6 +440,27 @@ S3DX_API s3dx_status s3dx_conv_set_silu(s3dx_conv *conv, int32_t enable, char *e
     });
 }
 
+S3DX_API s3dx_status s3dx_conv_plan(const s3dx_conv *conv, int64_t n_in, int64_t n_out, char *plan,
+                                    uint64_t plan_capacity, char *error, uint64_t error_capacity) {
+    return boundary(error, error_capacity, [&] {
+        require(conv != nullptr, "conv is NULL");
+        require(plan != nullptr && plan_capacity > 0, "plan buffer is empty");
+        require(n_in > 0 && n_out > 0, "row counts must be positive");
+        const int64_t x_bytes = n_in * conv->cin * static_cast<int64_t>(dtype_size(conv->dtype));
+        const LaunchPlan p = plan_launch(conv, x_bytes, n_out, true);
+        char text[256];
+        if (p.mfma)
+            std::snprintf(text, sizeof(text), "mfma tiling=%d%s rows=%d cols=%d kc=%d xf=%d ln=%s grid=%ux%u",
+                          p.tl->id, p.tl->splitk ? " split-k" : "", p.tl->rows(), p.tl->cols(), conv->kc,
+                          p.xf ? 1 : 0, conv->ln ? (p.fused_ln ? "fused" : "separate") : "none", p.grid.x,
+                          p.grid.y);
+        else
+            std::snprintf(text, sizeof(text), "generic rows=%d cols=%d ln=%s grid=%ux%u", kGM, kGN,
+                          conv->ln ? "separate" : "none", p.grid.x, p.grid.y);
+        std::snprintf(plan, plan_capacity, "%s", text);
+    });
+}
+
 S3DX_API s3dx_status s3dx_conv_run(const s3dx_conv *conv, const void *x, int64_t n_in,
                                    const int32_t *kmap, int64_t n_out, const void *residual,
                                    void *y, int32_t y_dtype, s3dx_stream stream, char *error,
@@ -446,27 +503,15 @@ S3DX_API s3dx_status s3dx_conv_run(const s3dx_conv *conv, const void *x, int64_t
         a.mod_shift = conv->mod_shift;
         const bool bf = conv->dtype == S3DX_BF16;
         // The MFMA kernel reads the map and writes rows with 16-byte accesses.
-        const bool use_mfma = conv->mfma && aligned(kmap, 16) && aligned(y, 16) && aligned(residual, 16);
-        const bool fused_ln = conv->ln && use_mfma && conv->nb * 32 == conv->cout;
-        if (use_mfma) {
-            a.ln = fused_ln;
-            if (conv->ln && !fused_ln) {  // LayerNorm as a separate pass
+        const LaunchPlan plan = plan_launch(conv, a.x_bytes, n_out,
+                                            aligned(kmap, 16) && aligned(y, 16) && aligned(residual, 16));
+        if (plan.mfma) {
+            a.ln = plan.fused_ln;
+            if (conv->ln && !plan.fused_ln) {  // LayerNorm as a separate pass
                 a.silu = 0;
                 a.residual = nullptr;
             }
-            // Buffer-resource gathers address at most 2 GiB; larger inputs and
-            // the input transforms take the XF=1 variant.
-            const bool xf = conv->gather_parent || conv->pre_scale != nullptr ||
-                            a.x_bytes >= (int64_t(1) << 31);
-            const int ntiles = conv->cout / (32 * conv->nb);
-            const Tiling *tl = choose_tiling(n_out, conv->nb, ntiles, bf, conv->kc, xf);
-            require(tl != nullptr, "no MFMA kernel for this shape");
-            const KernelFn fn = tiling_kernel(tl->id, bf, conv->kc, xf);
-            require(fn != nullptr, "no MFMA kernel for this shape");
-            const int bm = tl->rows();
-            const int64_t mt = (n_out + bm - 1) / bm;
-            const dim3 grid(static_cast<unsigned>(mt), static_cast<unsigned>(conv->cout / (32 * conv->nb)));
-            hipLaunchKernelGGL(fn, grid, dim3(256), 0, s, a);
+            hipLaunchKernelGGL(plan.fn, plan.grid, dim3(256), 0, s, a);
             launch_check("conv_mfma");
         } else {
             a.ln = 0;
@@ -474,10 +519,8 @@ S3DX_API s3dx_status s3dx_conv_run(const s3dx_conv *conv, const void *x, int64_t
                 a.silu = 0;
                 a.residual = nullptr;
             }
-            const int64_t mt = (n_out + kGM - 1) / kGM;
-            const dim3 grid(static_cast<unsigned>(mt), static_cast<unsigned>((conv->cout + kGN - 1) / kGN));
-            if (bf) hipLaunchKernelGGL(conv_generic_kernel<uint16_t>, grid, dim3(256), 0, s, a);
-            else hipLaunchKernelGGL(conv_generic_kernel<float>, grid, dim3(256), 0, s, a);
+            if (bf) hipLaunchKernelGGL(conv_generic_kernel<uint16_t>, plan.grid, dim3(256), 0, s, a);
+            else hipLaunchKernelGGL(conv_generic_kernel<float>, plan.grid, dim3(256), 0, s, a);
             launch_check("conv_generic");
         }
         if (conv->ln && !a.ln) {

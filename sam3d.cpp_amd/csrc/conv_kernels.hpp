@@ -807,30 +807,34 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
         char *buf0 = abuf, *buf1 = abuf + BM * SM::A_LD;
         uint4 b0[KSW][NB], b1[KSW][NB];
         uint4 ra[APT];
+        // An odd task count peels task 0 before the loop, so the loop always
+        // runs whole pairs and leaves straight into the reduction; task 0's
+        // weights then go to b1 and task 1's to b0.
+        const bool odd = ntasks & 1;
         Cursor nx{mask, -1, chunks - 1};
         advance(nx);  // task 0
         load_a(nx, ra);
-        load_b(nx, b0);
+        if (odd) load_b(nx, b1);
+        else load_b(nx, b0);
 #pragma unroll
         for (int q = 0; q < APT; ++q) *a_slot(buf0, q) = ra[q];
         advance(nx);  // task 1
         load_a(nx, ra);
-        load_b(nx, b1);
+        if (odd) load_b(nx, b0);
+        else load_b(nx, b1);
         advance(nx);  // task 2
         lds_barrier();
-        // Two tasks per trip with no exit in between (an odd count finishes
-        // with one compute-only task), so each body is one scheduling region
-        // and the wait counts see one steady load pattern.
-        for (int t = 0; t + 1 < ntasks; t += 2) {
+        if (odd) {
+            body(buf0, b1, buf1, ra, nx);
+            lds_barrier();
+            char *tmp = buf0;
+            buf0 = buf1;
+            buf1 = tmp;
+        }
+        for (int t = odd ? 1 : 0; t < ntasks; t += 2) {
             body(buf0, b0, buf1, ra, nx);
             lds_barrier();
             body(buf1, b1, buf0, ra, nx);
-            lds_barrier();
-        }
-        if (ntasks & 1) {
-            uint4 af[KSW][4];
-            read_frags(buf0, af);
-            mfmas(af, b0);
             lds_barrier();
         }
     }

@@ -101,6 +101,26 @@ def test_conv_create_validation(s3dx):
     s3dx.lib().s3dx_conv_free(p)
 
 
+def test_conv_plan_names_the_launched_kernel(s3dx, monkeypatch):
+    # Host-only query: which kernel variant s3dx_conv_run would launch.
+    monkeypatch.delenv("S3DX_CONV_TILING", raising=False)
+    n = 28265  # 64^3 eight-shell union, seed 0
+    c128 = s3dx.SparseConv(128, 128, 27, s3dx.BF16)
+    assert c128.plan(n, n) == "mfma tiling=11 split-k rows=128 cols=128 kc=128 xf=0 ln=none grid=221x1"
+    c128.set_layernorm(True, 1e-6)
+    assert "ln=fused" in c128.plan(n, n)
+    f64 = s3dx.SparseConv(64, 64, 27, s3dx.F32)
+    assert f64.plan(n, n).startswith("mfma tiling=12 split-k rows=128 cols=64 kc=64")
+    # 96 bf16 channels: 32-channel tasks do not split over 4 waves.
+    assert s3dx.SparseConv(96, 96, 27, s3dx.BF16).plan(n, n).startswith("mfma tiling=2 ")
+    # Cout not a multiple of 32: the generic kernel.
+    assert s3dx.SparseConv(16, 40, 27, s3dx.F32).plan(100, 100) == "generic rows=64 cols=64 ln=none grid=2x1"
+    monkeypatch.setenv("S3DX_CONV_TILING", "10")
+    assert c128.plan(n, n).startswith("mfma tiling=10 rows=128 cols=128")
+    with pytest.raises(s3dx.S3dxError):
+        c128.plan(0, n)
+
+
 def test_missing_library_fails_loudly(s3dx, monkeypatch, tmp_path):
     monkeypatch.setattr(s3dx, "_lib", None)
     monkeypatch.setattr(s3dx, "LIB_PATH", tmp_path / "absent.so")
