@@ -97,43 +97,46 @@ def copy_calibration(s3dx):
     print(json.dumps({"copy_calibration_bytes_read": n * 4, "copy_calibration_bytes_written": n * 4}))
 
 
-def cpu_baseline(block, kmap_host, n, pairs, coords, W):
+def _timed_runs(fn, budget_s: float, max_runs: int):
+    """Run fn until about budget_s seconds have passed; per-run times."""
+    times, start = [], time.perf_counter()
+    while len(times) < max_runs and (not times or time.perf_counter() - start < budget_s):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return times
+
+
+def cpu_baseline(block, kmap_host, n, pairs, coords, W, conv_budget_s=10.0, kmap_budget_s=5.0):
+    """Bounded CPU sample of the same workload (about 15 s of host work)."""
     O = ge.load_oracle()
     threads = min(16, os.cpu_count() or 1)
     h = block.host
     c = block.c
     flops = 2.0 * c * c * pairs
     O.conv_im2col_gemm_f32(h["x"], kmap_host, n, h["w1"], c, h["b"], threads)  # warm-up
-    times = []
-    for _ in range(3):
-        t0 = time.perf_counter()
-        O.conv_im2col_gemm_f32(h["x"], kmap_host, n, h["w1"], c, h["b"], threads)
-        times.append(time.perf_counter() - t0)
-    t_conv = statistics.median(times)
-    kmap_kind, kt = "port", []
+    conv_t = _timed_runs(lambda: O.conv_im2col_gemm_f32(h["x"], kmap_host, n, h["w1"], c, h["b"], threads),
+                         conv_budget_s, 2000)
+    t_conv = statistics.median(conv_t)
     if O.ref_available():
         kmap_kind = "reference"
-        for _ in range(3):
-            t0 = time.perf_counter()
-            O.ref_slat_tables(coords, 6)
-            kt.append(time.perf_counter() - t0)
+        kmap_t = _timed_runs(lambda: O.ref_slat_tables(coords, 6), kmap_budget_s, 2000)
     else:
-        for _ in range(3):
-            t0 = time.perf_counter()
-            O.kmap_subm3(coords, n)
-            kt.append(time.perf_counter() - t0)
-    t_kmap = statistics.median(kt)
+        kmap_kind = "port"
+        kmap_t = _timed_runs(lambda: O.kmap_subm3(coords, n), kmap_budget_s, 2000)
+    t_kmap = statistics.median(kmap_t)
     return {
         "value": flops / t_conv / 1e12, "unit": "TFLOP/s", "cores": threads, "kind": "port",
-        "sample": (f"one {c}->{c} FP32 sparse conv over the same {n} voxels / {pairs} pairs: "
-                   f"im2col gather + FP32 GEMM on {threads} threads (GGML CPU decomposition), "
-                   f"median of 3 after 1 warm-up, {t_conv * 1e3:.1f} ms each"),
+        "sample": (f"{len(conv_t)} runs ({sum(conv_t):.1f} s) of one {c}->{c} FP32 sparse conv over the "
+                   f"same {n} voxels / {pairs} pairs: im2col gather + FP32 GEMM on {threads} threads "
+                   f"(GGML CPU decomposition), median {t_conv * 1e3:.1f} ms per conv"),
         "conv_ms": t_conv * 1e3,
         "kmap": {"value": n / t_kmap / 1e6, "unit": "Mvox/s", "cores": 1, "kind": kmap_kind,
                  "ms": t_kmap * 1e3,
-                 "sample": ("reference SlatTables::build (fine + coarse maps, 6-channel APE) "
-                            "compiled from sparse_ops.cpp" if kmap_kind == "reference" else
-                            "oracle ordered-map kernel map") + ", single thread, median of 3"},
+                 "sample": (f"{len(kmap_t)} runs ({sum(kmap_t):.1f} s) of " +
+                            ("the reference SlatTables::build (fine + coarse maps, 6-channel APE) "
+                             "compiled from sparse_ops.cpp" if kmap_kind == "reference" else
+                             "the oracle's ordered-map kernel map") + ", single thread, median")},
         "cpu_model": cpu_model(),
     }
 
