@@ -6,13 +6,14 @@
 //   SlatTables downsample src/objects_runtime/sparse_ops.cpp:53-104
 //   MeshSubdivideTables   src/objects_runtime/sparse_ops.cpp:272-404
 //
-// The hash is open addressing with linear probing over 64-bit slots holding
-// (32-bit key tag << 32 | row).  A slot is claimed with a 64-bit CAS; a
-// second row with the same coordinates lowers the row half with a 64-bit
-// atomicMin, so after the insert kernel every key maps to its smallest row --
-// exactly std::map::emplace's "first occurrence wins".  Keys are the full
-// (b, x, y, z) int32 tuple: a tag match is confirmed against the coordinate
-// array, so any int32 coordinates are handled exactly.
+// The hash is open addressing with linear probing at load <= 1/4.  A 32-byte
+// slot holds the full (b, x, y, z) int32 key and its row (0xFFFFFFFF =
+// empty), so one probe is one cache line and verifies a hit by itself.  A
+// wave waits for its longest probe chain, which is what the low load keeps
+// short.  A slot is claimed with a 32-bit CAS on the row; a second row with
+// the same coordinates lowers it with atomicMin, so after the insert kernel
+// every key maps to its smallest row -- exactly std::map::emplace's "first
+// occurrence wins".  Any int32 coordinates are handled exactly.
 #include "common.hpp"
 
 #include <vector>
@@ -20,80 +21,87 @@
 namespace s3dx {
 namespace {
 
-constexpr uint64_t kEmpty = ~0ull;
+constexpr uint32_t kEmpty = 0xFFFFFFFFu;
 constexpr int kThreads = 256;
 
 // Workspace flag words.
 constexpr int kFlagDuplicate = 0;  // some coordinate occurs twice
-constexpr int kFlagOverflow = 1;   // probe sequence exhausted (never at load <= 1/2)
+constexpr int kFlagOverflow = 1;   // probe sequence exhausted (never at load <= 1/4)
 
-__device__ __forceinline__ uint64_t fmix64(uint64_t k) {
-    k ^= k >> 33;
-    k *= 0xff51afd7ed558ccdULL;
-    k ^= k >> 33;
-    k *= 0xc4ceb9fe1a85ec53ULL;
-    k ^= k >> 33;
-    return k;
-}
-
-__device__ __forceinline__ uint64_t key_hash(int4 c) {
-    const uint64_t xy = static_cast<uint64_t>(static_cast<uint32_t>(c.y)) |
-                        (static_cast<uint64_t>(static_cast<uint32_t>(c.z)) << 32);
-    const uint64_t zb = static_cast<uint64_t>(static_cast<uint32_t>(c.w)) |
-                        (static_cast<uint64_t>(static_cast<uint32_t>(c.x)) << 32);
-    return fmix64(xy ^ fmix64(zb + 0x9E3779B97F4A7C15ULL));
+// 32-bit hash of (b, x, y, z): a multiply-add chain over the four words and
+// a murmur3-style finalizer (five 32-bit multiplies).
+__device__ __forceinline__ uint32_t key_hash(int4 c) {
+    uint32_t h = static_cast<uint32_t>(c.x) * 0x9E3779B1u + static_cast<uint32_t>(c.y);
+    h = h * 0x85EBCA77u + static_cast<uint32_t>(c.z);
+    h = h * 0xC2B2AE3Du + static_cast<uint32_t>(c.w);
+    h ^= h >> 16;
+    h *= 0x7FEB352Du;
+    h ^= h >> 15;
+    h *= 0x846CA68Bu;
+    h ^= h >> 16;
+    return h;
 }
 
 __device__ __forceinline__ bool same_key(int4 a, int4 b) {
     return a.x == b.x && a.y == b.y && a.z == b.z && a.w == b.w;
 }
 
-// Smallest inserted row whose key equals c, or -1.
-__device__ __forceinline__ int32_t hash_find(const uint64_t *__restrict__ slots, uint64_t mask,
-                                             const int4 *__restrict__ keys, int4 c) {
-    const uint64_t h = key_hash(c);
-    const uint32_t tag = static_cast<uint32_t>(h >> 32);
-    uint64_t pos = h & mask;
-    for (uint64_t probe = 0; probe <= mask; ++probe) {
-        const uint64_t cur = slots[pos];
-        if (cur == kEmpty) return -1;
-        if (static_cast<uint32_t>(cur >> 32) == tag) {
-            const int32_t row = static_cast<int32_t>(static_cast<uint32_t>(cur));
-            if (same_key(keys[row], c)) return row;
-        }
-        pos = (pos + 1) & mask;
+struct __align__(32) Slot {
+    int4 key;
+    uint32_t row;
+    uint32_t pad[3];
+};
+
+// Device view of the table: cap = mask + 1 slots.
+struct Hash {
+    Slot *slots;
+    int32_t *flags;
+    uint32_t mask;
+};
+
+// Smallest inserted row whose key equals c, or -1 (after the insert kernel).
+__device__ __forceinline__ int32_t hash_find(const Hash &h, int4 c) {
+    uint32_t pos = key_hash(c) & h.mask;
+    for (uint32_t probe = 0; probe <= h.mask; ++probe) {
+        const int4 k = h.slots[pos].key;
+        const uint32_t row = h.slots[pos].row;
+        if (row == kEmpty) return -1;
+        if (same_key(k, c)) return static_cast<int32_t>(row);
+        pos = (pos + 1) & h.mask;
     }
     return -1;
 }
 
+// Empties the slots and zeroes the flag words (one launch for both).
+__global__ void __launch_bounds__(kThreads) hash_clear_kernel(Hash h) {
+    const uint32_t i = blockIdx.x * kThreads + threadIdx.x;
+    if (i <= h.mask) h.slots[i].row = kEmpty;
+    if (i < 64) h.flags[i] = 0;
+}
+
 __global__ void __launch_bounds__(kThreads)
-hash_insert_kernel(const int4 *__restrict__ keys, int32_t n, uint64_t *slots, uint64_t mask,
-                   int32_t *flags) {
+hash_insert_kernel(const int4 *__restrict__ keys, int32_t n, Hash h) {
     const int32_t i = blockIdx.x * kThreads + threadIdx.x;
     if (i >= n) return;
     const int4 c = keys[i];
-    const uint64_t h = key_hash(c);
-    const uint64_t tag = h >> 32;
-    const uint64_t mine = (tag << 32) | static_cast<uint32_t>(i);
-    uint64_t pos = h & mask;
-    for (uint64_t probe = 0; probe <= mask; ++probe) {
-        uint64_t cur = slots[pos];
-        if (cur == kEmpty) {
-            cur = atomicCAS(reinterpret_cast<unsigned long long *>(&slots[pos]), kEmpty, mine);
-            if (cur == kEmpty) return;
-        }
-        // Every row ever stored in this slot carries the same key, so any
-        // (possibly stale) row half identifies the key correctly.
-        if ((cur >> 32) == tag &&
-            same_key(keys[static_cast<uint32_t>(cur)], c)) {
-            atomicMin(reinterpret_cast<unsigned long long *>(&slots[pos]),
-                      static_cast<unsigned long long>(mine));
-            flags[kFlagDuplicate] = 1;
+    uint32_t pos = key_hash(c) & h.mask;
+    for (uint32_t probe = 0; probe <= h.mask; ++probe) {
+        const uint32_t prev = atomicCAS(&h.slots[pos].row, kEmpty, static_cast<uint32_t>(i));
+        if (prev == kEmpty) {
+            h.slots[pos].key = c;
             return;
         }
-        pos = (pos + 1) & mask;
+        // The slot's key is that of its first claimant, read from the input
+        // (its key entry may not be written yet).  Rows sharing a key only
+        // ever lower the row, so any row seen here carries the slot's key.
+        if (same_key(keys[prev], c)) {
+            atomicMin(&h.slots[pos].row, static_cast<uint32_t>(i));
+            h.flags[kFlagDuplicate] = 1;
+            return;
+        }
+        pos = (pos + 1) & h.mask;
     }
-    flags[kFlagOverflow] = 1;
+    h.flags[kFlagOverflow] = 1;
 }
 
 __device__ __forceinline__ bool add_fits(int32_t v, int32_t d, int32_t *out) {
@@ -104,8 +112,7 @@ __device__ __forceinline__ bool add_fits(int32_t v, int32_t d, int32_t *out) {
 
 // One thread per (voxel, offset): kmap[i*27+o] = first row at coords[i]+d(o).
 __global__ void __launch_bounds__(kThreads)
-kmap_lookup_kernel(const int4 *__restrict__ coords, int32_t n, const uint64_t *__restrict__ slots,
-                   uint64_t mask, const int32_t *__restrict__ flags, int32_t missing,
+kmap_lookup_kernel(const int4 *__restrict__ coords, int32_t n, Hash h, int32_t missing,
                    int32_t *__restrict__ kmap) {
     const int32_t g = blockIdx.x * kThreads + threadIdx.x;
     if (g >= n * 27) return;
@@ -115,11 +122,11 @@ kmap_lookup_kernel(const int4 *__restrict__ coords, int32_t n, const uint64_t *_
     int32_t result = missing;
     // Later duplicates of a coordinate keep an all-missing row
     // (sparse_ops.cpp:129-139 only visits each key's first row).
-    const bool owner = flags[kFlagDuplicate] == 0 || hash_find(slots, mask, coords, c) == i;
+    const bool owner = h.flags[kFlagDuplicate] == 0 || hash_find(h, c) == i;
     int4 q = c;
     if (owner && add_fits(c.y, o / 9 - 1, &q.y) && add_fits(c.z, (o / 3) % 3 - 1, &q.z) &&
         add_fits(c.w, o % 3 - 1, &q.w)) {
-        const int32_t r = hash_find(slots, mask, coords, q);
+        const int32_t r = hash_find(h, q);
         if (r >= 0) result = r;
     }
     kmap[g] = result;
@@ -238,11 +245,11 @@ dense_assign_kernel(const int4 *__restrict__ ckeys, int32_t n, DenseGrid g,
 // (the smallest fine row of each coarse key) are ranked by counting smaller
 // keys, O(nc^2) comparisons tiled through LDS.
 __global__ void __launch_bounds__(kThreads)
-rep_flag_kernel(const int4 *__restrict__ ckeys, int32_t n, const uint64_t *__restrict__ slots,
-                uint64_t mask, int32_t *__restrict__ rep, int32_t *__restrict__ is_rep) {
+rep_flag_kernel(const int4 *__restrict__ ckeys, int32_t n, Hash h, int32_t *__restrict__ rep,
+                int32_t *__restrict__ is_rep) {
     const int32_t i = blockIdx.x * kThreads + threadIdx.x;
     if (i >= n) return;
-    const int32_t r = hash_find(slots, mask, ckeys, ckeys[i]);
+    const int32_t r = hash_find(h, ckeys[i]);
     rep[i] = r;
     is_rep[i] = r == i ? 1 : 0;
 }
@@ -334,7 +341,7 @@ unsigned blocks_for(int64_t items) { return static_cast<unsigned>((items + kThre
 
 uint64_t hash_capacity(int64_t n) {
     uint64_t cap = 256;
-    while (cap < static_cast<uint64_t>(n) * 2) cap <<= 1;
+    while (cap < static_cast<uint64_t>(n) * 4) cap <<= 1;
     return cap;
 }
 
@@ -346,26 +353,33 @@ uint64_t dense_cell_cap(int64_t n) {
 }
 
 template <class W>
-void kmap_layout(W &w, int64_t n, uint64_t **slots, int32_t **flags) {
+void kmap_layout(W &w, int64_t n, Hash *h) {
+    const uint64_t cap = hash_capacity(n);
     if constexpr (std::is_same_v<W, Carver>) {
-        *slots = w.template take<uint64_t>(hash_capacity(n));
-        *flags = w.template take<int32_t>(64);
+        h->slots = w.template take<Slot>(cap);
+        h->flags = w.template take<int32_t>(64);
+        h->mask = static_cast<uint32_t>(cap - 1);
     } else {
-        w.template take<uint64_t>(hash_capacity(n));
+        w.template take<Slot>(cap);
         w.template take<int32_t>(64);
     }
 }
 
-// Hash insert + lookup, leaving the flags in the workspace.
-void run_kmap(const int4 *coords, int32_t n, int32_t missing, int32_t *kmap, uint64_t *slots,
-              int32_t *flags, hipStream_t stream) {
-    const uint64_t cap = hash_capacity(n);
-    fill_u64(slots, cap, kEmpty, stream);
-    fill_u32(reinterpret_cast<uint32_t *>(flags), 64, 0, stream);
-    hash_insert_kernel<<<blocks_for(n), kThreads, 0, stream>>>(coords, n, slots, cap - 1, flags);
+// Clears the table and inserts n keys (first occurrence wins).
+void hash_build(const int4 *keys, int32_t n, const Hash &h, hipStream_t stream) {
+    const uint64_t cap = static_cast<uint64_t>(h.mask) + 1;
+    hash_clear_kernel<<<blocks_for(static_cast<int64_t>(cap)), kThreads, 0, stream>>>(h);
+    launch_check("hash_clear");
+    hash_insert_kernel<<<blocks_for(n), kThreads, 0, stream>>>(keys, n, h);
     launch_check("hash_insert");
+}
+
+// Hash insert + lookup, leaving the flags in the workspace.
+void run_kmap(const int4 *coords, int32_t n, int32_t missing, int32_t *kmap, const Hash &h,
+              hipStream_t stream) {
+    hash_build(coords, n, h, stream);
     kmap_lookup_kernel<<<blocks_for(static_cast<int64_t>(n) * 27), kThreads, 0, stream>>>(
-        coords, n, slots, cap - 1, flags, missing, kmap);
+        coords, n, h, missing, kmap);
     launch_check("kmap_lookup");
 }
 
@@ -382,17 +396,16 @@ void check_coords(const int32_t *coords, int64_t n) {
 namespace s3dx {
 namespace {
 struct SubdivideLayout {
-    uint64_t *slots;
-    int32_t *flags;
+    Hash hash;
     int32_t *parent_kmap;
 };
 template <class W>
 void subdivide_layout(W &w, int64_t p, SubdivideLayout *l) {
     if constexpr (std::is_same_v<W, Carver>) {
-        kmap_layout(w, p, &l->slots, &l->flags);
+        kmap_layout(w, p, &l->hash);
         l->parent_kmap = w.template take<int32_t>(static_cast<uint64_t>(p) * 27);
     } else {
-        kmap_layout(w, p, nullptr, nullptr);
+        kmap_layout(w, p, static_cast<Hash *>(nullptr));
         w.template take<int32_t>(static_cast<uint64_t>(p) * 27);
     }
 }
@@ -400,8 +413,7 @@ void subdivide_layout(W &w, int64_t p, SubdivideLayout *l) {
 namespace {
 struct CoarsenLayout {
     int4 *ckeys;
-    uint64_t *slots;
-    int32_t *flags;
+    Hash hash;
     int32_t *bbox;
     int32_t *totals;
     int32_t *a, *b, *c, *d;  // n-sized scratch
@@ -416,7 +428,7 @@ void coarsen_layout(W &w, int64_t n, CoarsenLayout *l) {
     const uint64_t scan_items = cells > un ? cells : un;
     if constexpr (std::is_same_v<W, Carver>) {
         l->ckeys = w.template take<int4>(un);
-        kmap_layout(w, n, &l->slots, &l->flags);
+        kmap_layout(w, n, &l->hash);
         l->bbox = w.template take<int32_t>(8);
         l->totals = w.template take<int32_t>(8);
         l->a = w.template take<int32_t>(un);
@@ -432,7 +444,7 @@ void coarsen_layout(W &w, int64_t n, CoarsenLayout *l) {
         l->scan_ws = w.template take<char>(scan_workspace_bytes(static_cast<int64_t>(scan_items)));
     } else {
         w.template take<int4>(un);
-        kmap_layout(w, n, nullptr, nullptr);
+        kmap_layout(w, n, static_cast<Hash *>(nullptr));
         w.template take<int32_t>(8);
         w.template take<int32_t>(8);
         for (int k = 0; k < 8; ++k) w.template take<int32_t>(un);
@@ -454,7 +466,7 @@ S3DX_API s3dx_status s3dx_kmap_workspace_size(int64_t n, uint64_t *bytes, char *
         require(bytes != nullptr, "bytes is NULL");
         require(n > 0 && n <= INT32_MAX / 27, "voxel count out of range");
         Sizer s;
-        kmap_layout(s, n, nullptr, nullptr);
+        kmap_layout(s, n, static_cast<Hash *>(nullptr));
         *bytes = s.used;
     });
 }
@@ -467,11 +479,10 @@ S3DX_API s3dx_status s3dx_kmap_subm3(const int32_t *coords, int64_t n, int32_t m
         require(kmap != nullptr, "kmap is NULL");
         require(workspace != nullptr, "workspace is NULL");
         Carver w(workspace, workspace_bytes);
-        uint64_t *slots;
-        int32_t *flags;
-        kmap_layout(w, n, &slots, &flags);
+        Hash h;
+        kmap_layout(w, n, &h);
         run_kmap(reinterpret_cast<const int4 *>(coords), static_cast<int32_t>(n), missing_value,
-                 kmap, slots, flags, as_stream(stream));
+                 kmap, h, as_stream(stream));
     });
 }
 
@@ -508,8 +519,7 @@ S3DX_API s3dx_status s3dx_subdivide2(const int32_t *parent_coords, int64_t paren
         Carver w(workspace, workspace_bytes);
         SubdivideLayout l;
         subdivide_layout(w, parent_count, &l);
-        run_kmap(reinterpret_cast<const int4 *>(parent_coords), p, -1, l.parent_kmap, l.slots,
-                 l.flags, s);
+        run_kmap(reinterpret_cast<const int4 *>(parent_coords), p, -1, l.parent_kmap, l.hash, s);
         child_coords_kernel<<<blocks_for(static_cast<int64_t>(p) * 8), kThreads, 0, s>>>(
             reinterpret_cast<const int4 *>(parent_coords), p, reinterpret_cast<int4 *>(child_coords));
         launch_check("child_coords");
@@ -519,7 +529,7 @@ S3DX_API s3dx_status s3dx_subdivide2(const int32_t *parent_coords, int64_t paren
             launch_check("child_kmap");
         }
         int32_t flags[2] = {0, 0};
-        hip_check(hipMemcpyAsync(flags, l.flags, sizeof(flags), hipMemcpyDeviceToHost, s),
+        hip_check(hipMemcpyAsync(flags, l.hash.flags, sizeof(flags), hipMemcpyDeviceToHost, s),
                   "hipMemcpyAsync flags");
         hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
         require(flags[kFlagDuplicate] == 0, "duplicate parent coordinates");
@@ -593,15 +603,9 @@ S3DX_API s3dx_status s3dx_coarsen2(const int32_t *coords, int64_t n, int32_t *co
             launch_check("dense_assign");
         } else {
             // 2b. dedupe through the hash, rank representatives by counting.
-            const uint64_t cap = hash_capacity(n);
-            fill_u64(l.slots, cap, kEmpty, s);
-            fill_u32(reinterpret_cast<uint32_t *>(l.flags), 64, 0, s);
-            hash_insert_kernel<<<blocks_for(ni), kThreads, 0, s>>>(l.ckeys, ni, l.slots, cap - 1,
-                                                                   l.flags);
-            launch_check("coarse_insert");
+            hash_build(l.ckeys, ni, l.hash, s);
             int32_t *rep = l.a, *is_rep = l.b, *pos = l.c, *rank_of = l.d;
-            rep_flag_kernel<<<blocks_for(ni), kThreads, 0, s>>>(l.ckeys, ni, l.slots, cap - 1, rep,
-                                                                is_rep);
+            rep_flag_kernel<<<blocks_for(ni), kThreads, 0, s>>>(l.ckeys, ni, l.hash, rep, is_rep);
             launch_check("rep_flag");
             exclusive_scan_i32(is_rep, pos, ni, l.totals, l.scan_ws, s);
             int32_t *reps = l.bucket;  // free until the children pass
