@@ -195,17 +195,22 @@ KernelFn tiling_kernel(int id, bool bf, int kc, bool xf) {
 // gather each row once and stream two tasks per stage, and two 32-row blocks
 // per wave halve the LDS traffic per MFMA when that still leaves one
 // workgroup per CU.  S3DX_CONV_TILING=<id> overrides (tuning).
-const Tiling *choose_tiling(int64_t n_out, int nb, int ntiles, bool bf, int kc, bool xf) {
+// splitk_ok: the packed weights fit the split-K kernel's 32-bit buffer
+// offsets (< 2 GiB).
+const Tiling *choose_tiling(int64_t n_out, int nb, int ntiles, bool bf, int kc, bool xf, bool splitk_ok) {
+    auto usable = [&](const Tiling &t) {
+        return t.cols() == nb * 32 && (splitk_ok || !t.splitk) && tiling_kernel(t.id, bf, kc, xf);
+    };
     if (const char *e = std::getenv("S3DX_CONV_TILING")) {
         const int id = std::atoi(e);
         for (const Tiling &t : kTilings)
-            if (t.id == id && t.cols() == nb * 32 && tiling_kernel(t.id, bf, kc, xf)) return &t;
+            if (t.id == id && usable(t)) return &t;
     }
     auto blocks = [&](const Tiling &t) { return (n_out + t.rows() - 1) / t.rows() * ntiles; };
     const Tiling *best = nullptr;
     int best_rank = 1 << 30;
     for (const Tiling &t : kTilings) {
-        if (t.cols() != nb * 32 || !tiling_kernel(t.id, bf, kc, xf)) continue;
+        if (!usable(t)) continue;
         int rank;
         if (t.splitk) rank = 0;
         else if (t.wn == 1 && t.nbw == 4) rank = blocks(t) >= 192 ? 1 : 10;  // 32x128 wave tiles
@@ -239,7 +244,8 @@ LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bo
         // the input transforms take the XF=1 variant.
         p.xf = conv->gather_parent || conv->pre_scale != nullptr || x_bytes >= (int64_t(1) << 31);
         const int ntiles = conv->cout / (32 * conv->nb);
-        p.tl = choose_tiling(n_out, conv->nb, ntiles, bf, conv->kc, p.xf);
+        const int64_t w_bytes = static_cast<int64_t>(conv->kvol) * conv->cin * conv->cout * (bf ? 2 : 4);
+        p.tl = choose_tiling(n_out, conv->nb, ntiles, bf, conv->kc, p.xf, w_bytes < (int64_t(1) << 31));
         require(p.tl != nullptr, "no MFMA kernel for this shape");
         p.fn = tiling_kernel(p.tl->id, bf, conv->kc, p.xf);
         require(p.fn != nullptr, "no MFMA kernel for this shape");

@@ -210,18 +210,55 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// Row-major finish of a workgroup's FP32 output tile staged in LDS (stg,
-// BM rows x STG_LD floats): bias, LayerNorm over the row (the tile spans
-// cout), modulate, SiLU, residual; 8 consecutive columns per thread, stored
-// with 16-byte accesses.  `part` holds 2*BM*TPR floats of LayerNorm partials.
+// Row-major finish of a workgroup's FP32 output tile: TPR threads per row,
+// 8 consecutive columns each, RPP rows per pass over BM rows.
+template <int TPR, int BM>
+struct RowMap {
+    static constexpr int RPP = 256 / TPR;
+    static constexpr int PASSES = (BM + RPP - 1) / RPP;
+    static constexpr bool POW2 = (TPR & (TPR - 1)) == 0;  // row groups are aligned lane segments
+};
+
+// Loads the residual values a thread will finish (8 bf16 in [p][0], or 8
+// floats in [p][0..1]); issued early so the latency overlaps other work.
+template <int TPR, int BM>
+__device__ __forceinline__ void load_residual(const ConvArgs &a, int64_t m0, int nb0, int tile_rows, int tid,
+                                              uint4 (&res)[RowMap<TPR, BM>::PASSES][2]) {
+    using RM = RowMap<TPR, BM>;
+    const int cg = tid % TPR, rsub = tid / TPR;
+    const int col0 = nb0 * 32 + cg * 8;
+#pragma unroll
+    for (int p = 0; p < RM::PASSES; ++p) {
+        res[p][0] = res[p][1] = make_uint4(0, 0, 0, 0);
+        const int rl = p * RM::RPP + rsub;
+        if (!a.residual || rsub >= RM::RPP || rl >= tile_rows) continue;
+        const int64_t off = (m0 + rl) * a.cout + col0;
+        if (a.y_bf16) {
+            res[p][0] = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.residual) + off);
+        } else {
+            const uint4 *rp = reinterpret_cast<const uint4 *>(static_cast<const float *>(a.residual) + off);
+            res[p][0] = rp[0];
+            res[p][1] = rp[1];
+        }
+    }
+}
+
+// Finishes the tile staged in LDS (stg, BM rows x STG_LD floats): bias,
+// LayerNorm over the row (the tile spans cout), modulate, SiLU, residual
+// (prefetched by load_residual), 16-byte stores.  Row statistics are summed
+// across the row's TPR lanes with shuffles when TPR is a power of two, else
+// through `part` (2*BM*TPR floats of LDS).
 template <int TPR, int BM, int STG_LD>
 __device__ __forceinline__ void finish_rows(const ConvArgs &a, const float *stg, float *part, int64_t m0,
-                                            int nb0, int tile_rows, int tid) {
-    constexpr int RPP = 256 / TPR;  // rows per pass
-    constexpr int PASSES = (BM + RPP - 1) / RPP;
+                                            int nb0, int tile_rows, int tid,
+                                            const uint4 (&res)[RowMap<TPR, BM>::PASSES][2]) {
+    using RM = RowMap<TPR, BM>;
+    constexpr int RPP = RM::RPP;
+    constexpr int PASSES = RM::PASSES;
     const int cg = tid % TPR, rsub = tid / TPR;
     const bool active = rsub < RPP;
     const int col0 = nb0 * 32 + cg * 8;  // global column of this thread's 8 values
+    const float inv_c = 1.0f / static_cast<float>(a.cout);
     float bias8[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) bias8[k] = a.bias ? a.bias[col0 + k] : 0.0f;
@@ -232,35 +269,41 @@ __device__ __forceinline__ void finish_rows(const ConvArgs &a, const float *stg,
         v[0] = x0.x + bias8[0]; v[1] = x0.y + bias8[1]; v[2] = x0.z + bias8[2]; v[3] = x0.w + bias8[3];
         v[4] = x1.x + bias8[4]; v[5] = x1.y + bias8[5]; v[6] = x1.z + bias8[6]; v[7] = x1.w + bias8[7];
     };
+    auto row_sum = [&](float x) __attribute__((always_inline)) {
+#pragma unroll
+        for (int d = TPR / 2; d >= 1; d >>= 1) x += __shfl_xor(x, d, TPR);
+        return x;
+    };
 
-    if (a.ln) {
-        // Row statistics (NT == cout): per-thread partials, then per-row sums.
-        float *psum = part, *psq = part + BM * TPR;
-        const float inv_c = 1.0f / static_cast<float>(a.cout);
+    if constexpr (!RM::POW2) {
+        if (a.ln) {
+            // Row statistics through LDS partials.
+            float *psum = part, *psq = part + BM * TPR;
 #pragma unroll
-        for (int p = 0; p < PASSES; ++p) {
-            const int rl = p * RPP + rsub;
-            if (!active || rl >= BM) continue;
-            float v[8];
-            tile_vals(rl, v);
-            psum[rl * TPR + cg] = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+            for (int p = 0; p < PASSES; ++p) {
+                const int rl = p * RPP + rsub;
+                if (!active || rl >= BM) continue;
+                float v[8];
+                tile_vals(rl, v);
+                psum[rl * TPR + cg] = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+            }
+            __syncthreads();
+#pragma unroll
+            for (int p = 0; p < PASSES; ++p) {
+                const int rl = p * RPP + rsub;
+                if (!active || rl >= BM) continue;
+                float m = 0.0f;
+                for (int g = 0; g < TPR; ++g) m += psum[rl * TPR + g];
+                m *= inv_c;
+                float v[8];
+                tile_vals(rl, v);
+                float q = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 8; ++k) q += (v[k] - m) * (v[k] - m);
+                psq[rl * TPR + cg] = q;
+            }
+            __syncthreads();
         }
-        __syncthreads();
-#pragma unroll
-        for (int p = 0; p < PASSES; ++p) {
-            const int rl = p * RPP + rsub;
-            if (!active || rl >= BM) continue;
-            float m = 0.0f;
-            for (int g = 0; g < TPR; ++g) m += psum[rl * TPR + g];
-            m *= inv_c;
-            float v[8];
-            tile_vals(rl, v);
-            float q = 0.0f;
-#pragma unroll
-            for (int k = 0; k < 8; ++k) q += (v[k] - m) * (v[k] - m);
-            psq[rl * TPR + cg] = q;
-        }
-        __syncthreads();
     }
 
     float lw[8], lb[8], ms[8], mh[8];
@@ -274,17 +317,30 @@ __device__ __forceinline__ void finish_rows(const ConvArgs &a, const float *stg,
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
         const int rl = p * RPP + rsub;
-        if (!active || rl >= tile_rows) continue;
+        if constexpr (!RM::POW2) {
+            if (!active || rl >= tile_rows) continue;
+        }
         float v[8];
-        tile_vals(rl, v);
+        tile_vals(rl < BM ? rl : BM - 1, v);
         if (a.ln) {
-            const float inv_c = 1.0f / static_cast<float>(a.cout);
-            float m = 0.0f, q = 0.0f;
-            for (int g = 0; g < TPR; ++g) {
-                m += part[rl * TPR + g];
-                q += part[BM * TPR + rl * TPR + g];
+            float m, q;
+            if constexpr (RM::POW2) {
+                // Two-pass mean / variance over the row's TPR lanes (every
+                // lane of the group takes part, whatever its row).
+                m = row_sum(((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]))) * inv_c;
+                float d2 = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 8; ++k) d2 += (v[k] - m) * (v[k] - m);
+                q = row_sum(d2);
+            } else {
+                m = 0.0f;
+                q = 0.0f;
+                for (int g = 0; g < TPR; ++g) {
+                    m += part[rl * TPR + g];
+                    q += part[BM * TPR + rl * TPR + g];
+                }
+                m *= inv_c;
             }
-            m *= inv_c;
             const float rstd = rsqrtf(q * inv_c + a.eps);
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
@@ -297,11 +353,11 @@ __device__ __forceinline__ void finish_rows(const ConvArgs &a, const float *stg,
 #pragma unroll
             for (int k = 0; k < 8; ++k) v[k] = silu(v[k]);
         }
+        if (rl >= tile_rows) continue;
         const int64_t off = (m0 + rl) * a.cout + col0;
         if (a.y_bf16) {
             if (a.residual) {
-                const uint4 r4 = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.residual) + off);
-                const uint32_t rw[4] = {r4.x, r4.y, r4.z, r4.w};
+                const uint32_t rw[4] = {res[p][0].x, res[p][0].y, res[p][0].z, res[p][0].w};
 #pragma unroll
                 for (int k = 0; k < 4; ++k) {
                     v[2 * k] += bf16_to_f32(static_cast<uint16_t>(rw[k] & 0xffffu));
@@ -317,10 +373,11 @@ __device__ __forceinline__ void finish_rows(const ConvArgs &a, const float *stg,
         } else {
             float4 *yp = reinterpret_cast<float4 *>(static_cast<float *>(a.y) + off);
             if (a.residual) {
-                const float4 *rp = reinterpret_cast<const float4 *>(static_cast<const float *>(a.residual) + off);
-                const float4 r0 = rp[0], r1 = rp[1];
-                v[0] += r0.x; v[1] += r0.y; v[2] += r0.z; v[3] += r0.w;
-                v[4] += r1.x; v[5] += r1.y; v[6] += r1.z; v[7] += r1.w;
+                const uint4 r0 = res[p][0], r1 = res[p][1];
+                v[0] += __builtin_bit_cast(float, r0.x); v[1] += __builtin_bit_cast(float, r0.y);
+                v[2] += __builtin_bit_cast(float, r0.z); v[3] += __builtin_bit_cast(float, r0.w);
+                v[4] += __builtin_bit_cast(float, r1.x); v[5] += __builtin_bit_cast(float, r1.y);
+                v[6] += __builtin_bit_cast(float, r1.z); v[7] += __builtin_bit_cast(float, r1.w);
             }
             yp[0] = make_float4(v[0], v[1], v[2], v[3]);
             yp[1] = make_float4(v[4], v[5], v[6], v[7]);
@@ -552,6 +609,8 @@ conv_mfma_kernel(ConvArgs a) {
             lds_barrier();
         }
     }
+    uint4 res[RowMap<SM::TPR, BM>::PASSES][2];
+    load_residual<SM::TPR, BM>(a, m0, nb0, tile_rows, tid, res);
     // Every wave is done with the weight buffers before the tile reuses them.
     __syncthreads();
 
@@ -569,7 +628,7 @@ conv_mfma_kernel(ConvArgs a) {
         }
     __syncthreads();
 
-    finish_rows<SM::TPR, BM, SM::STG_LD>(a, stg, part, m0, nb0, tile_rows, tid);
+    finish_rows<SM::TPR, BM, SM::STG_LD>(a, stg, part, m0, nb0, tile_rows, tid, res);
 }
 
 // ---------------------------------------------------------------------------
@@ -639,8 +698,15 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
     const int ksteps_total = a.cin / CPK;
     const int chunks = a.cin / KC;
     const int tile_rows = static_cast<int>(min(static_cast<int64_t>(BM), a.n_out - m0));
-    const uint4 *wg = static_cast<const uint4 *>(a.w);
     const int32_t xbytes = static_cast<int32_t>(a.x_bytes < INT32_MAX ? a.x_bytes : INT32_MAX);
+    constexpr int ES = static_cast<int>(sizeof(T));
+    // Packed weights through a buffer resource (the host keeps them < 2 GiB):
+    // per task a scalar byte offset, per column block an immediate.
+    const int64_t w_bytes = static_cast<int64_t>(kvol) * a.cin * a.cout * ES;
+    const auto w_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(a.w), static_cast<short>(0),
+                                                          static_cast<int32_t>(w_bytes), 0x00020000);
+    const auto x_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(a.x), static_cast<short>(0),
+                                                          xbytes, 0x00020000);
 
     // Tasks are the (present offset, Cin chunk) pairs in ascending order.  A
     // cursor walks them in scalar registers: the offsets not yet visited as a
@@ -658,24 +724,44 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
         c.kc = wrap ? (more ? 0 : c.kc) : c.kc + 1;
         c.rest = wrap && more ? (c.rest & (c.rest - 1u)) : c.rest;
     };
+    // Fragment (k-step ks, column block cb) of the packed weights sits at
+    // byte ((ks * nbtot + cb) * 64 + lane) * 16.  With ROT (NB = 4) wave w
+    // keeps column block (k + w) mod 4 in accumulator k, so the block it owns
+    // in the final reduction is always accumulator 0.
+    constexpr bool ROT = NB == 4;
     auto load_b = [&](const Cursor &c, uint4 (&bf)[KSW][NB]) __attribute__((always_inline)) {
-        const int64_t ks0 = static_cast<int64_t>(c.o) * ksteps_total + c.kc * KS;
+        const int ks0 = c.o * ksteps_total + c.kc * KS + wave;
 #pragma unroll
-        for (int i = 0; i < KSW; ++i)
+        for (int i = 0; i < KSW; ++i) {
+            const int32_t sbase = ((ks0 + 4 * i) * nbtot + nb0) * 1024;
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb)
-                bf[i][nb] = wg[((ks0 + wave + 4 * i) * nbtot + nb0 + nb) * 64 + lane];
+            for (int nb = 0; nb < NB; ++nb) {
+                // the column block goes into the scalar offset (rotated) or the immediate
+                const u32x4 v = ROT ? __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, lane * 16,
+                                                                            sbase + ((nb + wave) & 3) * 1024, 0)
+                                    : __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, lane * 16 + nb * 1024, sbase, 0);
+                bf[i][nb] = make_uint4(v.x, v.y, v.z, v.w);
+            }
+        }
     };
     // Row-major gather: piece u = tid + 256 q is row u / PPR, channels
-    // kc*KC + (u % PPR)*E .. +E.  The row indices come from the staged map.
+    // kc*KC + (u % PPR)*E .. +E.  The staged map holds, per (row, offset),
+    // the neighbour's byte offset in x (plain gathers; out of range when
+    // missing, which the buffer load answers with zeros) or its row index
+    // (transforming gathers; -1 when missing), at a fixed stride of 27.
     auto rows_of = [&](const Cursor &c, int32_t (&jn)[APT]) __attribute__((always_inline)) {
 #pragma unroll
-        for (int q = 0; q < APT; ++q) jn[q] = rows[((tid + q * 256) / PPR) * kvol + c.o];
+        for (int q = 0; q < APT; ++q) jn[q] = rows[((tid + q * 256) / PPR) * kMaxKvol + c.o];
     };
     auto gather = [&](const Cursor &c, int32_t j, int q) __attribute__((always_inline)) {
-        const int c0 = c.kc * KC + ((tid + q * 256) % PPR) * E;
-        if constexpr (XF == 0) return gather_plain<T>(a.x, xbytes, j, a.cin, c0);
-        else return load_fragment<T>(a, j, c0);
+        const int piece = (tid + q * 256) % PPR;
+        if constexpr (XF == 0) {
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
+                x_rsrc, static_cast<int32_t>(static_cast<uint32_t>(j) + piece * 16), c.kc * KC * ES, 0);
+            return make_uint4(v.x, v.y, v.z, v.w);
+        } else {
+            return load_fragment<T>(a, j, c.kc * KC + piece * E);
+        }
     };
     auto load_a = [&](const Cursor &c, uint4 (&ra)[APT]) __attribute__((always_inline)) {
         int32_t jn[APT];
@@ -704,40 +790,53 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
                 af[i][mb] = *reinterpret_cast<const uint4 *>(base + mb * 32 * SM::A_LD +
                                                              i * 4 * CPK * static_cast<int>(sizeof(T)));
     };
-    auto mfmas = [&](const uint4 (&af)[KSW][4], const uint4 (&bf)[KSW][NB]) __attribute__((always_inline)) {
+    // MFMAs number lo .. hi-1 of a task in (k-step, row block, column block)
+    // order; the bounds are compile-time, so the unrolled loop keeps only
+    // those.
+    auto mfma_range = [&](auto lo_c, auto hi_c, const uint4 (&af)[KSW][4], const uint4 (&bf)[KSW][NB])
+        __attribute__((always_inline)) {
+        constexpr int lo = decltype(lo_c)::value, hi = decltype(hi_c)::value;
 #pragma unroll
         for (int i = 0; i < KSW; ++i)
 #pragma unroll
             for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
-                for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = mfma_step<T>(af[i][mb], bf[i][nb], acc[mb][nb]);
+                for (int nb = 0; nb < NB; ++nb) {
+                    const int idx = (i * 4 + mb) * NB + nb;
+                    if (idx >= lo && idx < hi) acc[mb][nb] = mfma_step<T>(af[i][mb], bf[i][nb], acc[mb][nb]);
+                }
     };
 
-    // One task body: MFMAs of task t (A from LDS buffer rbuf, B in bc); store
-    // A(t+1) (in ra) to wbuf; issue the gathers and weight loads of task t+2
-    // (cursor nx) into ra and bc.  Instruction order: this task's fragment
-    // reads, the next gather's row-index reads, the first half of the MFMAs,
-    // then MFMAs alternating with (LDS store of a piece, gather into its
-    // registers), the weight loads last (they overwrite this task's B).
+    // One task body (task t, its A fragments already in afc, its weights in
+    // bc), split by one barrier:
+    //   first half   the first half of the MFMAs, alternating with the LDS
+    //                stores of A(t+1) (in ra) to wbuf and, into the freed
+    //                registers, the gathers of A(t+2) (cursor nx);
+    //   barrier      A(t+1) visible to every wave;
+    //   second half  the other MFMAs, alternating with the reads of A(t+1)'s
+    //                fragments into afn; then the weight loads of task t+2
+    //                into bc.
+    // The next body starts its MFMAs at once: its fragments are in registers.
     constexpr int MPS = sizeof(T) == 2 ? 1 : 4;  // MFMA instructions per fragment pair
-    constexpr int NMF = KSW * 4 * NB * MPS;
-    constexpr int M0 = NMF / 2;
-    constexpr int MI = (NMF - M0) / APT;
-    constexpr int MR = NMF - M0 - MI * APT;
-    auto body = [&](const char *rbuf, uint4 (&bc)[KSW][NB], char *wbuf, uint4 (&ra)[APT], Cursor &nx)
-        __attribute__((always_inline)) {
-        uint4 af[KSW][4];
-        read_frags(rbuf, af);
+    constexpr int NPAIR = KSW * 4 * NB;           // fragment pairs per task
+    constexpr int HALF = NPAIR / 2;
+    constexpr int NMF1 = HALF * MPS, NMF2 = (NPAIR - HALF) * MPS;
+    constexpr int M0 = NMF1 < 4 ? NMF1 : 4;       // MFMAs before the first LDS store
+    constexpr int MI = (NMF1 - M0) / APT;
+    constexpr int MR = NMF1 - M0 - MI * APT;
+    constexpr int NFR = KSW * 4;                  // fragment reads
+    constexpr int MJ = NMF2 / (NFR + 1);
+    constexpr int MK = NMF2 - MJ * NFR;
+    auto body = [&](const uint4 (&afc)[KSW][4], uint4 (&afn)[KSW][4], uint4 (&bc)[KSW][NB], char *wbuf,
+                    uint4 (&ra)[APT], Cursor &nx) __attribute__((always_inline)) {
         int32_t jn[APT];
         rows_of(nx, jn);
-        mfmas(af, bc);
+        mfma_range(std::integral_constant<int, 0>{}, std::integral_constant<int, HALF>{}, afc, bc);
 #pragma unroll
         for (int q = 0; q < APT; ++q) {
             *a_slot(wbuf, q) = ra[q];
             ra[q] = gather(nx, jn[q], q);
         }
-        load_b(nx, bc);
-        __builtin_amdgcn_sched_group_barrier(0x100, KSW * 4, 0);  // DS read: fragments
         __builtin_amdgcn_sched_group_barrier(0x100, APT, 0);      // DS read: row indices
         __builtin_amdgcn_sched_group_barrier(0x008, M0, 0);       // MFMA
 #pragma unroll
@@ -747,11 +846,25 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
             __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);    // VMEM read: gather
         }
         if constexpr (MR > 0) __builtin_amdgcn_sched_group_barrier(0x008, MR, 0);
+        lds_barrier();
+        mfma_range(std::integral_constant<int, HALF>{}, std::integral_constant<int, NPAIR>{}, afc, bc);
+        read_frags(wbuf, afn);
+        load_b(nx, bc);
+#pragma unroll
+        for (int k = 0; k < NFR; ++k) {
+            if constexpr (MJ > 0) __builtin_amdgcn_sched_group_barrier(0x008, MJ, 0);
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);    // DS read: next fragments
+        }
+        if constexpr (MK > 0) __builtin_amdgcn_sched_group_barrier(0x008, MK, 0);
         __builtin_amdgcn_sched_group_barrier(0x020, KSW * NB, 0); // VMEM read: weights
         advance(nx);
     };
 
-    // ---- stage this tile's neighbour rows (-1 = missing) and offset mask
+    // ---- stage this tile's neighbour rows and offset mask
+    auto staged = [&](bool valid, int32_t j) __attribute__((always_inline)) {
+        if constexpr (XF == 0) return valid ? j * a.cin * ES : static_cast<int32_t>(0x80000000u);
+        else return valid ? j : -1;
+    };
     if (tid == 0) *omask = 0;
     uint32_t my_mask = 0;
     if (a.kmap) {
@@ -780,8 +893,8 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
                 const int e = e0 + k;
                 if (e >= BM * kvol) continue;
                 const bool valid = e < count && jv[k] >= 0 && jv[k] < a.n_src;
-                rows[e] = valid ? jv[k] : -1;
-                const int o = kvol == 27 ? e % 27 : 0;
+                rows[kvol == kMaxKvol ? e : e * kMaxKvol] = staged(valid, jv[k]);
+                const int o = kvol == kMaxKvol ? e % kMaxKvol : 0;
                 if (valid) my_mask |= 1u << o;
             }
         }
@@ -789,7 +902,7 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
         for (int r = tid; r < BM; r += 256) {
             const int64_t j = m0 + r;
             const bool valid = r < tile_rows && j < a.n_src;
-            rows[r] = valid ? static_cast<int32_t>(j) : -1;
+            rows[r * kMaxKvol] = staged(valid, static_cast<int32_t>(j));
             if (valid) my_mask = 1u;
         }
     }
@@ -801,15 +914,16 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
     const uint32_t mask = __builtin_amdgcn_readfirstlane(*omask);
     const int ntasks = __popc(mask) * chunks;
 
-    // ---- main loop.  Entering task t: A(t) in LDS buffer t%2, A(t+1) on its
-    // way into ra, B(t) and B(t+1) in registers or on their way.
+    // ---- main loop.  Entering task t: A(t)'s fragments in registers, A(t+1)
+    // on its way into ra, B(t) and B(t+1) in registers or on their way.
     if (ntasks > 0) {
         char *buf0 = abuf, *buf1 = abuf + BM * SM::A_LD;
         uint4 b0[KSW][NB], b1[KSW][NB];
+        uint4 fx[KSW][4], fy[KSW][4];
         uint4 ra[APT];
         // An odd task count peels task 0 before the loop, so the loop always
-        // runs whole pairs and leaves straight into the reduction; task 0's
-        // weights then go to b1 and task 1's to b0.
+        // runs whole pairs; the peel's weights and fragments then live in the
+        // other register sets, and the two LDS buffers swap roles.
         const bool odd = ntasks & 1;
         Cursor nx{mask, -1, chunks - 1};
         advance(nx);  // task 0
@@ -825,63 +939,93 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
         advance(nx);  // task 2
         lds_barrier();
         if (odd) {
-            body(buf0, b1, buf1, ra, nx);
-            lds_barrier();
+            read_frags(buf0, fy);
+            body(fy, fx, b1, buf1, ra, nx);
             char *tmp = buf0;
             buf0 = buf1;
             buf1 = tmp;
+        } else {
+            read_frags(buf0, fx);
         }
         for (int t = odd ? 1 : 0; t < ntasks; t += 2) {
-            body(buf0, b0, buf1, ra, nx);
-            lds_barrier();
-            body(buf1, b1, buf0, ra, nx);
-            lds_barrier();
+            body(fx, fy, b0, buf1, ra, nx);
+            body(fy, fx, b1, buf0, ra, nx);
         }
+        lds_barrier();  // the last fragment reads finish before the tile reuses LDS
     }
 
     // ---- reduce the 4 partial tiles through LDS, 64 rows per phase ----
-    // Phase p: every wave writes its partial blocks 2p, 2p+1 as float4
-    // [nb][4][lane] into slot (h * 4 + writer) (16-byte lane stride,
-    // conflict-free); then the 2*NB (block, column-block) pairs of the phase
-    // are summed over the 4 writers, pair q by wave q % 4, into registers.
-    // Accumulators are only indexed by compile-time constants here.
+    // Phase p covers row blocks 2p, 2p+1; pair (h, c) = (block 2p+h, column
+    // block c) is summed by wave (h*NB + c) % 4 into registers, the other
+    // waves handing their partials over as float4 [4][lane] slots (16-byte
+    // lane stride, conflict-free).  With ROT the owner keeps its own partial
+    // (accumulator 0) and only three cross LDS.  Sums run in a fixed order,
+    // so results are deterministic.  Accumulators are only indexed by
+    // compile-time constants.
     constexpr int PPW = (2 * NB + 3) / 4;  // pairs per wave per phase
+    auto slot_of = [&](int h, int c, int writer) __attribute__((always_inline)) {
+        return red + ((h * NB + c) * 4 + writer) * (4 * 64);
+    };
     float fin[2][PPW][16];
 #pragma unroll
     for (int p = 0; p < 2; ++p) {
         if (p) __syncthreads();
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            float4 *slot = red + (h * 4 + wave) * (NB * 4 * 64);
+        for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int nb = 0; nb < NB; ++nb)
+            for (int k = ROT ? 1 : 0; k < NB; ++k) {
+                const int c = ROT ? ((k + wave) & 3) : k;
+                float4 *slot = slot_of(h, c, wave);
 #pragma unroll
                 for (int g = 0; g < 4; ++g)
-                    slot[(nb * 4 + g) * 64 + lane] =
-                        make_float4(acc[2 * p + h][nb][4 * g], acc[2 * p + h][nb][4 * g + 1],
-                                    acc[2 * p + h][nb][4 * g + 2], acc[2 * p + h][nb][4 * g + 3]);
-        }
+                    slot[g * 64 + lane] = make_float4(acc[2 * p + h][k][4 * g], acc[2 * p + h][k][4 * g + 1],
+                                                      acc[2 * p + h][k][4 * g + 2], acc[2 * p + h][k][4 * g + 3]);
+            }
         __syncthreads();
+        if constexpr (ROT) {
+            // Wave w owns (h, w) for h = 0, 1: its accumulator 0 plus the
+            // other three waves' slots.
 #pragma unroll
-        for (int i = 0; i < PPW; ++i) {
-            const int q = wave + 4 * i;
-            if (q >= 2 * NB) continue;
-            const int h = q / NB, nb = q - h * NB;
+            for (int h = 0; h < 2; ++h)
 #pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+                for (int g = 0; g < 4; ++g) {
+                    float4 sum = make_float4(acc[2 * p + h][0][4 * g], acc[2 * p + h][0][4 * g + 1],
+                                             acc[2 * p + h][0][4 * g + 2], acc[2 * p + h][0][4 * g + 3]);
 #pragma unroll
-                for (int src = 0; src < 4; ++src) {
-                    const float4 v = red[(h * 4 + src) * (NB * 4 * 64) + (nb * 4 + g) * 64 + lane];
-                    s.x += v.x;
-                    s.y += v.y;
-                    s.z += v.z;
-                    s.w += v.w;
+                    for (int s2 = 1; s2 < 4; ++s2) {
+                        const float4 v = slot_of(h, wave, (wave + s2) & 3)[g * 64 + lane];
+                        sum.x += v.x;
+                        sum.y += v.y;
+                        sum.z += v.z;
+                        sum.w += v.w;
+                    }
+                    fin[p][h][4 * g] = sum.x;
+                    fin[p][h][4 * g + 1] = sum.y;
+                    fin[p][h][4 * g + 2] = sum.z;
+                    fin[p][h][4 * g + 3] = sum.w;
                 }
-                fin[p][i][4 * g] = s.x;
-                fin[p][i][4 * g + 1] = s.y;
-                fin[p][i][4 * g + 2] = s.z;
-                fin[p][i][4 * g + 3] = s.w;
+        } else {
+#pragma unroll
+            for (int i = 0; i < PPW; ++i) {
+                const int q = wave + 4 * i;
+                if (q >= 2 * NB) continue;
+                const int h = q / NB, c = q - h * NB;
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                    for (int src = 0; src < 4; ++src) {
+                        const float4 v = slot_of(h, c, src)[g * 64 + lane];
+                        sum.x += v.x;
+                        sum.y += v.y;
+                        sum.z += v.z;
+                        sum.w += v.w;
+                    }
+                    fin[p][i][4 * g] = sum.x;
+                    fin[p][i][4 * g + 1] = sum.y;
+                    fin[p][i][4 * g + 2] = sum.z;
+                    fin[p][i][4 * g + 3] = sum.w;
+                }
             }
         }
     }
@@ -893,14 +1037,16 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
         for (int i = 0; i < PPW; ++i) {
             const int q = wave + 4 * i;
             if (q >= 2 * NB) continue;
-            const int h = q / NB, nb = q - h * NB;
-            const int col = nb * 32 + (lane & 31);
+            const int h = q / NB, c = q - h * NB;
+            const int col = c * 32 + (lane & 31);
             const int rb = (2 * p + h) * 32 + 4 * half;
 #pragma unroll
             for (int r = 0; r < 16; ++r) stg[(rb + 8 * (r >> 2) + (r & 3)) * SM::STG_LD + col] = fin[p][i][r];
         }
+    uint4 res[RowMap<SM::TPR, BM>::PASSES][2];
+    load_residual<SM::TPR, BM>(a, m0, nb0, tile_rows, tid, res);
     __syncthreads();
-    finish_rows<SM::TPR, BM, SM::STG_LD>(a, stg, part, m0, nb0, tile_rows, tid);
+    finish_rows<SM::TPR, BM, SM::STG_LD>(a, stg, part, m0, nb0, tile_rows, tid, res);
 }
 
 // Compiled tilings (tiling id -> MBW, NBW, WN, S); one task's weight chunk
