@@ -141,7 +141,9 @@ __device__ inline void store_from_f32<uint16_t>(uint16_t *p, float v) {
     *p = f32_to_bf16(v);
 }
 
-__device__ inline float silu(float v) { return v / (1.0f + __expf(-v)); }
+// x * sigmoid(x) with the hardware exponential and reciprocal (a few ulp; a
+// large negative x gives exp = inf, rcp = 0, result -0).
+__device__ inline float silu(float v) { return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v)); }
 
 inline int dtype_size(int32_t dt) { return dt == S3DX_BF16 ? 2 : 4; }
 inline void require_dtype(int32_t dt) {

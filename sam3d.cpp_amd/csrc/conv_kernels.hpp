@@ -269,9 +269,18 @@ __device__ __forceinline__ void finish_rows(const ConvArgs &a, const float *stg,
         v[0] = x0.x + bias8[0]; v[1] = x0.y + bias8[1]; v[2] = x0.z + bias8[2]; v[3] = x0.w + bias8[3];
         v[4] = x1.x + bias8[4]; v[5] = x1.y + bias8[5]; v[6] = x1.z + bias8[6]; v[7] = x1.w + bias8[7];
     };
+    // Sum over the row's TPR lanes, every lane receiving the total.  A
+    // 16-lane group is one DPP row: rotations by 8, 4, 2, 1 (VALU, no LDS).
     auto row_sum = [&](float x) __attribute__((always_inline)) {
+        if constexpr (TPR == 16) {
+            x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x128, 0xf, 0xf, false));
+            x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x124, 0xf, 0xf, false));
+            x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x122, 0xf, 0xf, false));
+            x += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x121, 0xf, 0xf, false));
+        } else {
 #pragma unroll
-        for (int d = TPR / 2; d >= 1; d >>= 1) x += __shfl_xor(x, d, TPR);
+            for (int d = TPR / 2; d >= 1; d >>= 1) x += __shfl_xor(x, d, TPR);
+        }
         return x;
     };
 
@@ -314,6 +323,35 @@ __device__ __forceinline__ void finish_rows(const ConvArgs &a, const float *stg,
         ms[k] = a.mod_scale ? a.mod_scale[col0 + k] : 0.0f;
         mh[k] = a.mod_shift ? a.mod_shift[col0 + k] : 0.0f;
     }
+    // Power-of-two groups: LayerNorm statistics of every pass first, all
+    // passes in lockstep so the cross-lane sums overlap (two-pass mean /
+    // variance; every lane of a group takes part, whatever its row).
+    float mean_p[PASSES], var_p[PASSES];
+    float vs[RM::POW2 ? PASSES : 1][8];  // the thread's tile values, read once
+    if constexpr (RM::POW2) {
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const int rl = p * RPP + rsub;
+            tile_vals(rl < BM ? rl : BM - 1, vs[p]);
+        }
+        if (a.ln) {
+#pragma unroll
+            for (int p = 0; p < PASSES; ++p)
+                mean_p[p] = ((vs[p][0] + vs[p][1]) + (vs[p][2] + vs[p][3])) +
+                            ((vs[p][4] + vs[p][5]) + (vs[p][6] + vs[p][7]));
+#pragma unroll
+            for (int p = 0; p < PASSES; ++p) mean_p[p] = row_sum(mean_p[p]) * inv_c;
+#pragma unroll
+            for (int p = 0; p < PASSES; ++p) {
+                float d2 = 0.0f;
+#pragma unroll
+                for (int k = 0; k < 8; ++k) d2 += (vs[p][k] - mean_p[p]) * (vs[p][k] - mean_p[p]);
+                var_p[p] = d2;
+            }
+#pragma unroll
+            for (int p = 0; p < PASSES; ++p) var_p[p] = row_sum(var_p[p]);
+        }
+    }
 #pragma unroll
     for (int p = 0; p < PASSES; ++p) {
         const int rl = p * RPP + rsub;
@@ -321,17 +359,17 @@ __device__ __forceinline__ void finish_rows(const ConvArgs &a, const float *stg,
             if (!active || rl >= tile_rows) continue;
         }
         float v[8];
-        tile_vals(rl < BM ? rl : BM - 1, v);
+        if constexpr (RM::POW2) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = vs[p][k];
+        } else {
+            tile_vals(rl, v);
+        }
         if (a.ln) {
             float m, q;
             if constexpr (RM::POW2) {
-                // Two-pass mean / variance over the row's TPR lanes (every
-                // lane of the group takes part, whatever its row).
-                m = row_sum(((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]))) * inv_c;
-                float d2 = 0.0f;
-#pragma unroll
-                for (int k = 0; k < 8; ++k) d2 += (v[k] - m) * (v[k] - m);
-                q = row_sum(d2);
+                m = mean_p[p];
+                q = var_p[p];
             } else {
                 m = 0.0f;
                 q = 0.0f;
