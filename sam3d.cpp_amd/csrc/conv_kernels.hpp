@@ -910,16 +910,24 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
         const int4 *src = reinterpret_cast<const int4 *>(a.kmap + m0 * kvol);
         constexpr int Q = (BM * kMaxKvol / 4 + 255) / 256;
         int4 v[Q];
+        if (tile_rows == BM) {
+            // Full tile (every tile but the last): BM*kvol is a multiple of
+            // 4, so clamped 16-byte loads cover it without branches.
+            const int last4 = BM * kvol / 4 - 1;
 #pragma unroll
-        for (int q = 0; q < Q; ++q) {
-            const int e = (tid + q * 256) * 4;
-            if (e + 3 < count) {
-                v[q] = src[tid + q * 256];
-            } else {
-                v[q] = make_int4(-1, -1, -1, -1);
-                if (e < count) v[q].x = a.kmap[m0 * kvol + e];
-                if (e + 1 < count) v[q].y = a.kmap[m0 * kvol + e + 1];
-                if (e + 2 < count) v[q].z = a.kmap[m0 * kvol + e + 2];
+            for (int q = 0; q < Q; ++q) v[q] = src[min(tid + q * 256, last4)];
+        } else {
+#pragma unroll
+            for (int q = 0; q < Q; ++q) {
+                const int e = (tid + q * 256) * 4;
+                if (e + 3 < count) {
+                    v[q] = src[tid + q * 256];
+                } else {
+                    v[q] = make_int4(-1, -1, -1, -1);
+                    if (e < count) v[q].x = a.kmap[m0 * kvol + e];
+                    if (e + 1 < count) v[q].y = a.kmap[m0 * kvol + e + 1];
+                    if (e + 2 < count) v[q].z = a.kmap[m0 * kvol + e + 2];
+                }
             }
         }
 #pragma unroll
@@ -944,11 +952,19 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
             if (valid) my_mask = 1u;
         }
     }
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) my_mask |= __shfl_xor(my_mask, d, 64);
-    __syncthreads();
+    // Wave OR: within each 16-lane DPP row, then across the four rows.
+    {
+        int m = static_cast<int>(my_mask);
+        m |= __builtin_amdgcn_update_dpp(0, m, 0x128, 0xf, 0xf, false);
+        m |= __builtin_amdgcn_update_dpp(0, m, 0x124, 0xf, 0xf, false);
+        m |= __builtin_amdgcn_update_dpp(0, m, 0x122, 0xf, 0xf, false);
+        m |= __builtin_amdgcn_update_dpp(0, m, 0x121, 0xf, 0xf, false);
+        my_mask = static_cast<uint32_t>(__builtin_amdgcn_readlane(m, 0) | __builtin_amdgcn_readlane(m, 16) |
+                                        __builtin_amdgcn_readlane(m, 32) | __builtin_amdgcn_readlane(m, 48));
+    }
+    lds_barrier();
     if (lane == 0 && my_mask) atomicOr(omask, my_mask);
-    __syncthreads();
+    lds_barrier();
     const uint32_t mask = __builtin_amdgcn_readfirstlane(*omask);
     const int ntasks = __popc(mask) * chunks;
 

@@ -217,3 +217,27 @@ def test_row_block_tilings(s3dx, O, W, monkeypatch, dtype, cin, cout, tiling):
     h = O.conv(rnd(s3dx, x, dtype), kmap, n, rnd(s3dx, w, dtype), 0, cout, b)
     ref = O.silu(O.layernorm(h, 1e-6)) + rnd(s3dx, res, dtype)
     assert rel_l2(got, ref) <= TOL[dtype] * (3 if dtype == 0 else 1)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [0, 1])
+def test_centre_column_not_identity(s3dx, O, W, dtype):
+    # The MFMA kernel fetches each tile's first task (the centre offset)
+    # assuming kmap[i][13] == i.  Maps that break it -- a permuted centre
+    # column, and later duplicates of a coordinate (all-sentinel rows) --
+    # must give the same results as the oracle.
+    rng = np.random.default_rng(21)
+    coords = W.shells_union(2)[:3000]
+    dup = np.concatenate([coords, coords[rng.integers(0, coords.shape[0], 200)]], 0)
+    for name, c in (("permuted", coords), ("duplicates", dup)):
+        n = c.shape[0]
+        kmap = O.kmap_subm3(c, n)
+        if name == "permuted":
+            kmap[:, 13] = np.roll(kmap[:, 13], 5)
+        x = W.normal_f32(22, 1, (n, 128))
+        w = W.conv_weight(22, 2, 128, 128)
+        b = W.normal_f32(22, 3, (128,))
+        print(f"centre test {name} dtype={dtype} n={n}", flush=True)
+        got = gpu_conv(s3dx, x, kmap, n, w, s3dx.WEIGHT_SLAT, b, dtype, 128)
+        ref = O.conv(rnd(s3dx, x, dtype), kmap, n, rnd(s3dx, w, dtype), 0, 128, b)
+        assert rel_l2(got, ref) <= TOL[dtype], name
