@@ -53,6 +53,8 @@ def parse():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     p.add_argument("--copy-calibration", action="store_true",
                    help="run only a 256 MiB copy kernel (HBM counter calibration)")
+    p.add_argument("--no-extras", action="store_true",
+                   help="skip the other configs (1, 3, 4, 5, coarsen, subdivide)")
     return p.parse_args()
 
 
@@ -85,6 +87,155 @@ class Block:
         self.conv2.run(self.h, self.n, kmap, self.n, self.y, self.dtype, self.x, s)
         if ev:
             ev[2].record(s)
+
+
+def _event_us(s3dx, stream, fn, reps=10, warm=2):
+    """Median device time of fn() on `stream`, HIP events around each call."""
+    for _ in range(warm):
+        fn()
+    ev = [(s3dx.Event(), s3dx.Event()) for _ in range(reps)]
+    for a, b in ev:
+        a.record(stream)
+        fn()
+        b.record(stream)
+    stream.synchronize()
+    return statistics.median(a.elapsed_ms(b) * 1e3 for a, b in ev)
+
+
+def _wall_us(fn, reps=5):
+    fn()
+    t = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        t.append(time.perf_counter() - t0)
+    return statistics.median(t) * 1e6
+
+
+def extras(s3dx, W, stream, seed):
+    """The other configs of the path, timed on the same GPU (not the headline)."""
+    out = {}
+    bf, f32 = s3dx.BF16, s3dx.F32
+
+    def conv_entry(name, conv, x, n_in, kmap, n_out, y, ydt, pairs, cin, cout, peak, residual=None):
+        us = _event_us(s3dx, stream, lambda: conv.run(x, n_in, kmap, n_out, y, ydt, residual, stream))
+        flops = 2.0 * cin * cout * pairs
+        out[name] = {"us": us, "tflops": flops / us / 1e6, "peak_tflops": peak,
+                     "frac": flops / us / 1e6 / peak, "rows": n_out, "pairs": pairs,
+                     "plan": conv.plan(n_in, n_out)}
+
+    # config 1: one FP32 64 -> 64 conv on the 20-radius shell (10,366 voxels)
+    c1 = W.shell_64()
+    n1 = c1.shape[0]
+    k1 = s3dx.kmap_subm3(s3dx.DeviceArray.from_host(c1, stream), n1, n1, stream=stream)
+    p1 = W.kmap_pairs(k1.download(stream), n1)
+    conv = s3dx.SparseConv(64, 64, 27, f32).set_weights(W.conv_weight(seed, 201, 64, 64), s3dx.WEIGHT_SLAT, None)
+    x = s3dx.DeviceArray.from_host(W.normal_f32(seed, 200, (n1, 64)), stream)
+    y = s3dx.DeviceArray((n1, 64), np.float32)
+    conv_entry("config1_fp32_conv_64", conv, x, n1, k1, n1, y, f32, p1, 64, 64, PEAK_FP32_TFLOPS)
+
+    # coarsen (SlatTables downsample tables) and config 3: 1024 -> 1024 BF16 on the coarse set
+    c2 = W.shells_union(seed)
+    n2 = c2.shape[0]
+    d2 = s3dx.DeviceArray.from_host(c2, stream)
+    res = {}
+
+    def do_coarsen():
+        res["c"] = s3dx.coarsen2(d2, n2, stream)
+    us = _wall_us(do_coarsen)
+    nc, cc = res["c"][0], res["c"][1]
+    out["coarsen2"] = {"us_wall": us, "fine": n2, "coarse": nc, "mvox_s": n2 / us,
+                       "note": "wall clock including its one host synchronization"}
+    k3 = s3dx.kmap_subm3(cc, nc, nc, stream=stream)
+    p3 = W.kmap_pairs(k3.download(stream)[:nc], nc)
+    conv = s3dx.SparseConv(1024, 1024, 27, bf).set_weights(W.conv_weight(seed, 301, 1024, 1024), s3dx.WEIGHT_SLAT, None)
+    x = s3dx.DeviceArray.from_host(W.f32_to_bf16_bits(W.normal_f32(seed, 300, (nc, 1024))), stream)
+    y = s3dx.DeviceArray((nc, 1024), np.uint16)
+    conv_entry("config3_bf16_conv_1024", conv, x, nc, k3, nc, y, bf, p3, 1024, 1024, PEAK_BF16_TFLOPS)
+
+    # subdivide (MeshSubdivideTables) and config 4: 192 -> 192 BF16 over the children,
+    # gathering parent rows (repeat x8) plus a per-slot offset
+    def do_subdivide():
+        res["s"] = s3dx.subdivide2(d2, n2, True, stream)
+    us = _wall_us(do_subdivide)
+    ch, k4 = res["s"]
+    n4 = 8 * n2
+    out["subdivide2"] = {"us_wall": us, "parents": n2, "children": n4, "mvox_s": n4 / us,
+                         "note": "wall clock including its one host synchronization"}
+    p4 = W.kmap_pairs(k4.download(stream), n4)
+    conv = (s3dx.SparseConv(192, 192, 27, bf).set_weights(W.conv_weight(seed, 401, 192, 192, layout="mesh"),
+                                                           s3dx.WEIGHT_MESH, None)
+            .set_gather_parent(True, W.normal_f32(seed, 402, (8, 192), 0.02)))
+    x = s3dx.DeviceArray.from_host(W.f32_to_bf16_bits(W.normal_f32(seed, 400, (n2, 192))), stream)
+    y = s3dx.DeviceArray((n4, 192), np.uint16)
+    conv_entry("config4_bf16_conv_192_children", conv, x, n2, k4, n4, y, bf, p4, 192, 192, PEAK_BF16_TFLOPS)
+
+    # config 5: 768-channel parents -> upsample block (768 -> 192) -> upsample
+    # block (192 -> 96) -> linear 96 -> 101 (FP32), the mesh decoder's sparse stack
+    out["config5_stack"] = mesh_stack(s3dx, W, stream, seed, d2, n2, ch, k4)
+    return out
+
+
+def mesh_stack(s3dx, W, stream, seed, d0, p0, ch0, k0):
+    bf, f32 = s3dx.BF16, s3dx.F32
+    stages, flops = {}, {}
+
+    def block(level, xp, p, kmap, cin, cout):
+        n = 8 * p
+        g1 = s3dx.DeviceArray.from_host(W.normal_f32(seed, 510 + level, (cin,), 0.2) + 1.0, stream)
+        b1 = s3dx.DeviceArray.from_host(W.normal_f32(seed, 520 + level, (cin,), 0.2), stream)
+        g2 = s3dx.DeviceArray.from_host(W.normal_f32(seed, 530 + level, (cout,), 0.2) + 1.0, stream)
+        b2 = s3dx.DeviceArray.from_host(W.normal_f32(seed, 540 + level, (cout,), 0.2), stream)
+        conv1 = (s3dx.SparseConv(cin, cout, 27, bf)
+                 .set_weights(W.conv_weight(seed, 550 + level, cin, cout, layout="mesh"), s3dx.WEIGHT_MESH, None)
+                 .set_gather_parent(True))
+        skip = (s3dx.SparseConv(cin, cout, 1, bf)
+                .set_weights(W.conv_weight(seed, 560 + level, cin, cout, kvol=1, layout="mesh"), s3dx.WEIGHT_MESH, None)
+                .set_gather_parent(True))
+        conv2 = s3dx.SparseConv(cout, cout, 27, bf).set_weights(
+            W.conv_weight(seed, 570 + level, cout, cout, layout="mesh"), s3dx.WEIGHT_MESH, None)
+        y1 = s3dx.DeviceArray((n, cout), np.uint16)
+        ys = s3dx.DeviceArray((n, cout), np.uint16)
+        y2 = s3dx.DeviceArray((n, cout), np.uint16)
+        pairs = W.kmap_pairs(kmap.download(stream), n)
+        flops[level] = 2.0 * pairs * (cin * cout + cout * cout) + 2.0 * n * cin * cout
+        gn1 = s3dx.groupnorm_stats(xp, bf, p, cin, 32, 1e-5, g1, b1, stream)
+        gn2 = s3dx.groupnorm_stats(y1, bf, n, cout, 32, 1e-5, g2, b2, stream)
+        conv1.set_input_affine_silu(gn1[0], gn1[1])
+        conv2.set_input_affine_silu(gn2[0], gn2[1])
+
+        def run():
+            s3dx.groupnorm_stats(xp, bf, p, cin, 32, 1e-5, g1, b1, stream, out=gn1)
+            conv1.run(xp, p, kmap, n, y1, bf, None, stream)
+            skip.run(xp, p, None, n, ys, bf, None, stream)
+            s3dx.groupnorm_stats(y1, bf, n, cout, 32, 1e-5, g2, b2, stream, out=gn2)
+            conv2.run(y1, n, kmap, n, y2, bf, ys, stream)
+        run.keep = (g1, b1, g2, b2, gn1, gn2)
+        return run, y2, n
+
+    x0 = s3dx.DeviceArray.from_host(W.f32_to_bf16_bits(W.normal_f32(seed, 500, (p0, 768))), stream)
+    run0, y0, n0 = block(0, x0, p0, k0, 768, 192)
+    run0()
+    ch1, k1 = s3dx.subdivide2(ch0, n0, True, stream)
+    run1, y1, n1 = block(1, y0, n0, k1, 192, 96)
+    head = s3dx.SparseConv(96, 101, 1, f32).set_weights(W.conv_weight(seed, 590, 96, 101, kvol=1), s3dx.WEIGHT_SLAT, None)
+    y1f = s3dx.DeviceArray((n1, 96), np.float32)
+    out = s3dx.DeviceArray((n1, 101), np.float32)
+
+    def run_head():
+        s3dx.convert(y1, bf, n1 * 96, y1f, f32, stream)
+        head.run(y1f, n1, None, n1, out, f32, None, stream)
+
+    stages["level0_block_us"] = _event_us(s3dx, stream, run0, reps=5)
+    stages["level1_block_us"] = _event_us(s3dx, stream, run1, reps=5)
+    stages["head_us"] = _event_us(s3dx, stream, run_head, reps=5)
+    total = stages["level0_block_us"] + stages["level1_block_us"] + stages["head_us"]
+    fl = flops[0] + flops[1] + 2.0 * n1 * 96 * 101
+    return {**stages, "total_us": total, "parents": p0, "level0_children": n0, "level1_children": n1,
+            "tflops": fl / total / 1e6, "dtype": "bf16 blocks, fp32 head",
+            "note": "per block: GN32 stats, conv (GN affine+SiLU and the x8 repeat fused into its gather), "
+                    "1x1 skip, GN32 stats, conv (GN affine+SiLU fused) + skip as residual; the level-1 "
+                    "subdivide is outside the timed stages"}
 
 
 def copy_calibration(s3dx):
@@ -264,6 +415,8 @@ def main():
         },
         "device": s3dx.device_name(),
     }
+    if not args.no_extras:
+        out["extras"] = extras(s3dx, W, stream, args.seed)
     if not args.no_cpu:
         cb = cpu_baseline(f32, kmap_host, n, pairs, coords, W)
         out["cpu_baseline"] = cb

@@ -389,12 +389,17 @@ def layernorm_rows(x, x_dtype, n, c, eps, w=None, b=None, mod_scale=None, mod_sh
          _i32(yd), _sptr(stream))
 
 
-def groupnorm_stats(x, x_dtype, n, c, groups, eps, gamma=None, beta=None, stream=None):
-    b = _u64(0)
-    call("s3dx_groupnorm_workspace_size", _i64(n), _i32(c), _i32(groups), C.byref(b))
-    ws = DeviceArray(int(b.value), np.uint8)
-    scale = DeviceArray((c,), np.float32)
-    shift = DeviceArray((c,), np.float32)
+def groupnorm_stats(x, x_dtype, n, c, groups, eps, gamma=None, beta=None, stream=None, out=None):
+    """Per-channel GroupNorm scale/shift (s3dx_groupnorm_stats); `out` = a previous
+    call's (scale, shift, workspace) to reuse (no allocation)."""
+    if out is None:
+        b = _u64(0)
+        call("s3dx_groupnorm_workspace_size", _i64(n), _i32(c), _i32(groups), C.byref(b))
+        ws = DeviceArray(int(b.value), np.uint8)
+        scale = DeviceArray((c,), np.float32)
+        shift = DeviceArray((c,), np.float32)
+    else:
+        scale, shift, ws = out
     call("s3dx_groupnorm_stats", _dptr(x), _i32(x_dtype), _i64(n), _i32(c), _i32(groups), _f32(eps),
          _dptr(gamma), _dptr(beta), _dptr(scale), _dptr(shift), _dptr(ws), _u64(ws.nbytes), _sptr(stream))
     return scale, shift, ws
