@@ -233,9 +233,9 @@ def mesh_stack(s3dx, W, stream, seed, d0, p0, ch0, k0):
     fl = flops[0] + flops[1] + 2.0 * n1 * 96 * 101
     return {**stages, "total_us": total, "parents": p0, "level0_children": n0, "level1_children": n1,
             "tflops": fl / total / 1e6, "dtype": "bf16 blocks, fp32 head",
-            "note": "per block: GN32 stats, conv (GN affine+SiLU and the x8 repeat fused into its gather), "
-                    "1x1 skip, GN32 stats, conv (GN affine+SiLU fused) + skip as residual; the level-1 "
-                    "subdivide is outside the timed stages"}
+            "note": "per block: GN32 stats, conv (GN affine+SiLU pass over the parents, gather of "
+                    "parent row j>>3), 1x1 skip, GN32 stats, conv (GN affine+SiLU pass) + skip as "
+                    "residual; the level-1 subdivide is outside the timed stages"}
 
 
 def copy_calibration(s3dx):

@@ -153,11 +153,16 @@ S3DX_API s3dx_status s3dx_subdivide2(const int32_t *parent_coords, int64_t paren
  * Per output row i:  v = bias + sum_o W_o . in(kmap[i][o])
  *   in(j)   = x[j]                               (default)
  *           = x[j >> 3] + slot_offset[j & 7]     (gather_parent: repeat_children
- *                                                 mesh_decoder_graph.cpp:32-38
- *                                                 fused into the gather)
+ *                                                 mesh_decoder_graph.cpp:32-38)
  *           then silu(in*pre_scale + pre_shift)  (input affine+SiLU: GroupNorm
- *                                                 apply + ggml_silu, fused; missing
+ *                                                 apply + ggml_silu; missing
  *                                                 rows stay zero)
+ * The parent repeat alone costs nothing (the gather reads row j >> 3).  Slot
+ * offsets and the affine + SiLU run once per source element, in a row pass
+ * before the gather, into a buffer the layer object owns and grows on demand
+ * (rows: 8 * n_in with slot offsets, else n_in), rounded to the conv's dtype
+ * as a stored tensor would be.  Runs of one such layer object on different
+ * streams must not overlap: they share that buffer.
  *   v -> LayerNorm over Cout (eps, optional affine), optional modulate
  *        v*scale + v + shift (slat_flow_graph.cpp:55-59) -> optional SiLU
  *        -> optional + residual[i] -> y[i]
@@ -175,12 +180,12 @@ S3DX_API void s3dx_conv_free(s3dx_conv *conv);
 S3DX_API s3dx_status s3dx_conv_set_weights(s3dx_conv *conv, const float *host_weight,
                                            int32_t layout, const float *host_bias,
                                            char *error, uint64_t error_capacity);
-/* Fused repeat_children; host slot_offset [8][cin] float32 may be NULL. */
+/* repeat_children of the input; host slot_offset [8][cin] float32 may be NULL. */
 S3DX_API s3dx_status s3dx_conv_set_gather_parent(s3dx_conv *conv, int32_t enable,
                                                  const float *host_slot_offset, char *error,
                                                  uint64_t error_capacity);
-/* Fused input affine + SiLU; DEVICE scale/shift [cin] float32, read at run
- * time (s3dx_groupnorm_stats writes them).  NULL,NULL disables. */
+/* Input affine + SiLU; DEVICE scale/shift [cin] float32, read at run time
+ * (s3dx_groupnorm_stats writes them).  NULL,NULL disables. */
 S3DX_API s3dx_status s3dx_conv_set_input_affine_silu(s3dx_conv *conv, const float *scale,
                                                      const float *shift, char *error,
                                                      uint64_t error_capacity);

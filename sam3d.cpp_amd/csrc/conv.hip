@@ -27,6 +27,7 @@
 //                  weight packed in the same permuted order.
 #include "conv_kernels.hpp"
 
+#include <algorithm>
 #include <cstdio>
 
 #include <cstdlib>
@@ -45,12 +46,73 @@ constexpr int kGM = 64, kGN = 64, kGK = 16;
 
 template <class T>
 __device__ __forceinline__ float load_input(const ConvArgs &a, int32_t j, int32_t c) {
-    const int64_t src = a.gather_parent ? (j >> 3) : j;
-    float v = load_as_f32<T>(static_cast<const T *>(a.x) + src * a.cin + c);
-    if (a.gather_parent && a.slot_offset) v += a.slot_offset[(j & 7) * a.cin + c];
-    if (a.pre_scale) v = silu(v * a.pre_scale[c] + a.pre_shift[c]);
-    if constexpr (sizeof(T) == 2) v = bf16_to_f32(f32_to_bf16(v));
+    return load_as_f32<T>(static_cast<const T *>(a.x) + static_cast<int64_t>(j) * a.cin + c);
+}
+
+// ---------------------------------------------------------------------------
+// Input transforms of the mesh upsample block (mesh_decoder_graph.cpp:16-38,
+// 109-134), applied once per source element before the conv gathers it 27
+// times: out[r] = SiLU((x[src(r)] + slot_offset[r & 7]) * scale + shift),
+// src(r) = r >> 3 when the rows are the parents' children (slot offsets
+// set), else r.  Each step is optional; rounded once to T, as storing the
+// transformed tensor would round it.
+// ---------------------------------------------------------------------------
+struct XformArgs {
+    const void *x;
+    void *out;
+    int64_t rows;  // output rows
+    int32_t cin;
+    int32_t children;  // output row r reads x row r >> 3 and adds slot_offset[r & 7]
+    const float *slot_offset;
+    const float *scale, *shift;
+};
+
+template <class T>
+__device__ __forceinline__ float xform_one(const XformArgs &a, float v, int64_t r, int32_t c) {
+    if (a.children) v += a.slot_offset[(r & 7) * a.cin + c];
+    if (a.scale) v = silu(v * a.scale[c] + a.shift[c]);
     return v;
+}
+
+// 16-byte pieces (cin a multiple of the piece's element count).
+template <class T>
+__global__ void __launch_bounds__(256) xform_rows_kernel(XformArgs a) {
+    constexpr int E = 16 / sizeof(T);
+    const int32_t ppr = a.cin / E;
+    const int64_t total = a.rows * ppr;
+    for (int64_t u = blockIdx.x * 256ll + threadIdx.x; u < total; u += gridDim.x * 256ll) {
+        const int64_t r = u / ppr;
+        const int32_t c0 = static_cast<int32_t>(u - r * ppr) * E;
+        const int64_t src = a.children ? (r >> 3) : r;
+        const uint4 raw = *reinterpret_cast<const uint4 *>(static_cast<const T *>(a.x) + src * a.cin + c0);
+        const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+        uint32_t o4[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            if constexpr (E == 8) {
+                const float lo = xform_one<T>(a, bf16_to_f32(static_cast<uint16_t>(w4[k] & 0xffffu)), r, c0 + 2 * k);
+                const float hi = xform_one<T>(a, bf16_to_f32(static_cast<uint16_t>(w4[k] >> 16)), r, c0 + 2 * k + 1);
+                o4[k] = static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+            } else {
+                o4[k] = __builtin_bit_cast(uint32_t, xform_one<T>(a, __builtin_bit_cast(float, w4[k]), r, c0 + k));
+            }
+        }
+        *reinterpret_cast<uint4 *>(static_cast<T *>(a.out) + r * a.cin + c0) = make_uint4(o4[0], o4[1], o4[2], o4[3]);
+    }
+}
+
+// Any cin: one element per thread.
+template <class T>
+__global__ void __launch_bounds__(256) xform_elems_kernel(XformArgs a) {
+    const int64_t total = a.rows * a.cin;
+    for (int64_t u = blockIdx.x * 256ll + threadIdx.x; u < total; u += gridDim.x * 256ll) {
+        const int64_t r = u / a.cin;
+        const int32_t c = static_cast<int32_t>(u - r * a.cin);
+        const int64_t src = a.children ? (r >> 3) : r;
+        const float v = xform_one<T>(a, load_as_f32<T>(static_cast<const T *>(a.x) + src * a.cin + c), r, c);
+        if constexpr (sizeof(T) == 2) static_cast<uint16_t *>(a.out)[u] = f32_to_bf16(v);
+        else static_cast<float *>(a.out)[u] = v;
+    }
 }
 
 template <class T>
@@ -73,7 +135,7 @@ __global__ void __launch_bounds__(256) conv_generic_kernel(ConvArgs a) {
         int64_t j = -1;
         if (row < a.n_out) j = a.kmap ? a.kmap[row * kvol + o] : row;
         const bool valid = j >= 0 && j < a.n_src;
-        rows[idx] = valid ? static_cast<int32_t>(j) : -1;
+        rows[idx] = valid ? static_cast<int32_t>(j >> a.row_shift) : -1;
         if (valid) my_mask |= 1u << o;
     }
     if (my_mask) atomicOr(&omask, my_mask);
@@ -172,11 +234,17 @@ struct s3dx_conv {
     float eps = 1e-6f;
     float *ln_w = nullptr, *ln_b = nullptr, *mod_scale = nullptr, *mod_shift = nullptr;
     bool weights_set = false;
+    // Transformed input rows (slot offsets / affine + SiLU applied), grown on
+    // demand by s3dx_conv_run; one buffer per layer object.
+    mutable void *xin = nullptr;
+    mutable int64_t xin_bytes = 0;
+
+    bool transforms() const { return slot_offset != nullptr || pre_scale != nullptr; }
 
     ~s3dx_conv() {
         for (void *p : {w, static_cast<void *>(bias), static_cast<void *>(slot_offset),
                         static_cast<void *>(ln_w), static_cast<void *>(ln_b),
-                        static_cast<void *>(mod_scale), static_cast<void *>(mod_shift)})
+                        static_cast<void *>(mod_scale), static_cast<void *>(mod_shift), xin})
             if (p) (void)hipFree(p);
     }
 };
@@ -227,12 +295,32 @@ const Tiling *choose_tiling(int64_t n_out, int nb, int ntiles, bool bf, int kc, 
 // Kernel choice of one launch, shared by s3dx_conv_run and s3dx_conv_plan.
 struct LaunchPlan {
     bool mfma = false;      // MFMA kernel (else the generic VALU kernel)
-    bool xf = false;        // gathers with input transforms / 64-bit offsets
+    bool xf = false;        // 64-bit addressed gathers (source above 2 GiB)
     bool fused_ln = false;  // LayerNorm in the MFMA epilogue
     const Tiling *tl = nullptr;
     KernelFn fn = nullptr;
     dim3 grid;
 };
+
+// What the conv gathers from: the caller's rows, or the transformed rows the
+// pre-pass writes (children when slot offsets are set), and the shift that
+// turns a kmap entry into a row of it.
+struct Source {
+    int64_t rows = 0;   // rows of the gathered tensor
+    int64_t n_src = 0;  // bound on kmap entries
+    int32_t shift = 0;
+    bool children = false, pre = false;
+};
+
+Source source_of(const s3dx_conv *conv, int64_t n_in) {
+    Source src;
+    src.children = conv->gather_parent && conv->slot_offset != nullptr;
+    src.pre = conv->transforms();
+    src.rows = src.children ? 8 * n_in : n_in;
+    src.shift = conv->gather_parent && !src.children ? 3 : 0;
+    src.n_src = conv->gather_parent ? 8 * n_in : n_in;
+    return src;
+}
 
 LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bool aligned16) {
     LaunchPlan p;
@@ -240,9 +328,9 @@ LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bo
     p.mfma = conv->mfma && aligned16;
     if (p.mfma) {
         p.fused_ln = conv->ln && conv->nb * 32 == conv->cout;
-        // Buffer-resource gathers address at most 2 GiB; larger inputs and
-        // the input transforms take the XF=1 variant.
-        p.xf = conv->gather_parent || conv->pre_scale != nullptr || x_bytes >= (int64_t(1) << 31);
+        // Buffer-resource gathers address at most 2 GiB; larger inputs take
+        // the XF=1 (64-bit addressed) variant.
+        p.xf = x_bytes >= (int64_t(1) << 31);
         const int ntiles = conv->cout / (32 * conv->nb);
         const int64_t w_bytes = static_cast<int64_t>(conv->kvol) * conv->cin * conv->cout * (bf ? 2 : 4);
         p.tl = choose_tiling(n_out, conv->nb, ntiles, bf, conv->kc, p.xf, w_bytes < (int64_t(1) << 31));
@@ -268,6 +356,22 @@ float *upload_f32(const float *host, size_t count) {
         hip_check(e, "hipMemcpy");
     }
     return static_cast<float *>(d);
+}
+
+// The layer's transformed-input buffer, at least `bytes` long.  Growing it
+// waits for the stream's earlier work, which may still read the old one.
+void *transform_buffer(const s3dx_conv *conv, int64_t bytes, hipStream_t s) {
+    if (bytes > conv->xin_bytes) {
+        if (conv->xin) {
+            hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
+            hip_check(hipFree(conv->xin), "hipFree");
+            conv->xin = nullptr;
+            conv->xin_bytes = 0;
+        }
+        hip_check(hipMalloc(&conv->xin, static_cast<size_t>(bytes)), "hipMalloc");
+        conv->xin_bytes = bytes;
+    }
+    return conv->xin;
 }
 
 void replace(float *&slot, float *fresh) {
@@ -452,7 +556,8 @@ S3DX_API s3dx_status s3dx_conv_plan(const s3dx_conv *conv, int64_t n_in, int64_t
         require(conv != nullptr, "conv is NULL");
         require(plan != nullptr && plan_capacity > 0, "plan buffer is empty");
         require(n_in > 0 && n_out > 0, "row counts must be positive");
-        const int64_t x_bytes = n_in * conv->cin * static_cast<int64_t>(dtype_size(conv->dtype));
+        const Source src = source_of(conv, n_in);
+        const int64_t x_bytes = src.rows * conv->cin * static_cast<int64_t>(dtype_size(conv->dtype));
         const LaunchPlan p = plan_launch(conv, x_bytes, n_out, true);
         char text[256];
         if (p.mfma)
@@ -463,7 +568,8 @@ S3DX_API s3dx_status s3dx_conv_plan(const s3dx_conv *conv, int64_t n_in, int64_t
         else
             std::snprintf(text, sizeof(text), "generic rows=%d cols=%d ln=%s grid=%ux%u", kGM, kGN,
                           conv->ln ? "separate" : "none", p.grid.x, p.grid.y);
-        std::snprintf(plan, plan_capacity, "%s", text);
+        std::snprintf(plan, plan_capacity, "%s%s%s", src.pre ? (src.children ? "pre=children " : "pre=rows ") : "",
+                      src.shift ? "parent-rows " : "", text);
     });
 }
 
@@ -480,13 +586,39 @@ S3DX_API s3dx_status s3dx_conv_run(const s3dx_conv *conv, const void *x, int64_t
         require(n_out <= INT32_MAX, "n_out exceeds INT32_MAX");
         require_dtype(y_dtype);
         require(aligned(x, 16) && aligned(y, 4) && aligned(residual, 4), "misaligned buffer");
-        const int64_t n_src = conv->gather_parent ? n_in * 8 : n_in;
-        require(n_src <= INT32_MAX, "input rows exceed INT32_MAX");
+        const Source src = source_of(conv, n_in);
+        require(src.n_src <= INT32_MAX, "input rows exceed INT32_MAX");
         const hipStream_t s = as_stream(stream);
+        const bool bf = conv->dtype == S3DX_BF16;
+        const int64_t x_bytes = src.rows * conv->cin * static_cast<int64_t>(dtype_size(conv->dtype));
+        if (src.pre) {
+            XformArgs xa{};
+            xa.x = x;
+            xa.out = transform_buffer(conv, x_bytes, s);
+            xa.rows = src.rows;
+            xa.cin = conv->cin;
+            xa.children = src.children;
+            xa.slot_offset = conv->slot_offset;
+            xa.scale = conv->pre_scale;
+            xa.shift = conv->pre_shift;
+            const bool vec = conv->cin % (bf ? 8 : 4) == 0;
+            const int64_t items = src.rows * (vec ? conv->cin / (bf ? 8 : 4) : conv->cin);
+            const dim3 grid(static_cast<unsigned>(std::min<int64_t>((items + 255) / 256, 16384)));
+            if (vec) {
+                if (bf) hipLaunchKernelGGL(xform_rows_kernel<uint16_t>, grid, dim3(256), 0, s, xa);
+                else hipLaunchKernelGGL(xform_rows_kernel<float>, grid, dim3(256), 0, s, xa);
+            } else {
+                if (bf) hipLaunchKernelGGL(xform_elems_kernel<uint16_t>, grid, dim3(256), 0, s, xa);
+                else hipLaunchKernelGGL(xform_elems_kernel<float>, grid, dim3(256), 0, s, xa);
+            }
+            launch_check("conv_xform");
+            x = xa.out;
+        }
         ConvArgs a{};
         a.x = x;
-        a.x_bytes = n_in * conv->cin * static_cast<int64_t>(dtype_size(conv->dtype));
-        a.n_src = n_src;
+        a.x_bytes = x_bytes;
+        a.n_src = src.n_src;
+        a.row_shift = src.shift;
         a.cin = conv->cin;
         a.kmap = kmap;
         a.n_out = n_out;
@@ -497,17 +629,12 @@ S3DX_API s3dx_status s3dx_conv_run(const s3dx_conv *conv, const void *x, int64_t
         a.residual = residual;
         a.y = y;
         a.y_bf16 = y_dtype == S3DX_BF16;
-        a.gather_parent = conv->gather_parent;
-        a.slot_offset = conv->slot_offset;
-        a.pre_scale = conv->pre_scale;
-        a.pre_shift = conv->pre_shift;
         a.silu = conv->silu;
         a.eps = conv->eps;
         a.ln_w = conv->ln_w;
         a.ln_b = conv->ln_b;
         a.mod_scale = conv->mod_scale;
         a.mod_shift = conv->mod_shift;
-        const bool bf = conv->dtype == S3DX_BF16;
         // The MFMA kernel reads the map and writes rows with 16-byte accesses.
         const LaunchPlan plan = plan_launch(conv, a.x_bytes, n_out,
                                             aligned(kmap, 16) && aligned(y, 16) && aligned(residual, 16));

@@ -23,10 +23,7 @@ struct ConvArgs {
     const void *residual;
     void *y;
     int32_t y_bf16;
-    int32_t gather_parent;
-    const float *slot_offset;
-    const float *pre_scale;
-    const float *pre_shift;
+    int32_t row_shift;  // kmap entry j reads source row j >> row_shift (3: parent of child j)
     int32_t ln;
     float eps;
     const float *ln_w;
@@ -53,7 +50,7 @@ inline constexpr Tiling kTilings[] = {
     {10, 1, 4, 1, 0}, {11, 4, 4, 1, 1}, {12, 4, 2, 1, 1}, {13, 4, 3, 1, 1}, {14, 4, 1, 1, 1},
 };
 
-// MFMA kernel for tiling `id`, kc channels per task, xf input transforms;
+// MFMA kernel for tiling `id`, kc channels per task, xf 64-bit gathers;
 // nullptr if that combination is not compiled.
 KernelFn pick_mfma_bf16(int id, int kc, bool xf);
 KernelFn pick_mfma_f32(int id, int kc, bool xf);
@@ -84,52 +81,13 @@ struct Frag<float> {
     static constexpr int E = 4;
 };
 
-// Applies the optional input transforms to one 16-byte fragment of row j,
-// channels c0 .. c0+E.  Returns the fragment in T.
+// One 16-byte fragment of source row j (already shifted), channels c0 ..
+// c0+E, with 64-bit addressing; a zero fragment when j < 0.
 template <class T>
 __device__ __forceinline__ uint4 load_fragment(const ConvArgs &a, int32_t j, int32_t c0) {
-    constexpr int E = Frag<T>::E;
     if (j < 0) return make_uint4(0, 0, 0, 0);
-    const int64_t src = a.gather_parent ? (j >> 3) : j;
-    const T *xp = static_cast<const T *>(a.x) + src * a.cin + c0;
-    uint4 raw = *reinterpret_cast<const uint4 *>(xp);
-    const bool slot = a.gather_parent && a.slot_offset;
-    const bool affine = a.pre_scale != nullptr;
-    if (!slot && !affine) return raw;
-    float v[E];
-    if constexpr (E == 8) {
-        const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            v[2 * e] = bf16_to_f32(static_cast<uint16_t>(w4[e] & 0xffffu));
-            v[2 * e + 1] = bf16_to_f32(static_cast<uint16_t>(w4[e] >> 16));
-        }
-    } else {
-        v[0] = __builtin_bit_cast(float, raw.x);
-        v[1] = __builtin_bit_cast(float, raw.y);
-        v[2] = __builtin_bit_cast(float, raw.z);
-        v[3] = __builtin_bit_cast(float, raw.w);
-    }
-    if (slot) {
-        const float *so = a.slot_offset + (j & 7) * a.cin + c0;
-#pragma unroll
-        for (int e = 0; e < E; ++e) v[e] += so[e];
-    }
-    if (affine) {
-#pragma unroll
-        for (int e = 0; e < E; ++e) v[e] = silu(v[e] * a.pre_scale[c0 + e] + a.pre_shift[c0 + e]);
-    }
-    if constexpr (E == 8) {
-        uint32_t w4[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-            w4[e] = static_cast<uint32_t>(f32_to_bf16(v[2 * e])) |
-                    (static_cast<uint32_t>(f32_to_bf16(v[2 * e + 1])) << 16);
-        return make_uint4(w4[0], w4[1], w4[2], w4[3]);
-    } else {
-        return make_uint4(__builtin_bit_cast(uint32_t, v[0]), __builtin_bit_cast(uint32_t, v[1]),
-                          __builtin_bit_cast(uint32_t, v[2]), __builtin_bit_cast(uint32_t, v[3]));
-    }
+    const T *xp = static_cast<const T *>(a.x) + static_cast<int64_t>(j) * a.cin + c0;
+    return *reinterpret_cast<const uint4 *>(xp);
 }
 
 template <class T>
@@ -443,8 +401,8 @@ struct ConvSmem {
     static constexpr int OCC = (TOTAL <= 80 * 1024 && MBW == 1) ? 2 : 1;
 };
 
-// T: uint16_t (bf16) or float.  XF: 0 = plain gathers, 1 = gathers with the
-// parent-repeat / slot-offset / affine+SiLU input transforms.
+// T: uint16_t (bf16) or float.  XF: 0 = buffer-resource gathers (inputs
+// below 2 GiB), 1 = 64-bit addressed gathers.
 //
 // Workgroup = 4 waves arranged WM x WN (WM = 4 / WN).  A wave owns MBW 32-row
 // blocks x NBW 32-column blocks of the output (BM = WM*MBW*32 rows and
@@ -522,7 +480,7 @@ conv_mfma_kernel(ConvArgs a) {
                 const int e = e0 + k;
                 if (e >= BM * kvol) continue;
                 const bool valid = e < count && jv[k] >= 0 && jv[k] < a.n_src;
-                rows[e] = valid ? jv[k] : -1;
+                rows[e] = valid ? jv[k] >> a.row_shift : -1;
                 const int o = kvol == 27 ? e % 27 : 0;
                 if (valid) my_mask |= 1u << o;
             }
@@ -531,7 +489,7 @@ conv_mfma_kernel(ConvArgs a) {
         for (int r = tid; r < BM; r += 256) {
             const int64_t j = m0 + r;
             const bool valid = r < tile_rows && j < a.n_src;
-            rows[r] = valid ? static_cast<int32_t>(j) : -1;
+            rows[r] = valid ? static_cast<int32_t>(j >> a.row_shift) : -1;
             if (valid) my_mask = 1u;
         }
     }
@@ -786,7 +744,7 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
     // kc*KC + (u % PPR)*E .. +E.  The staged map holds, per (row, offset),
     // the neighbour's byte offset in x (plain gathers; out of range when
     // missing, which the buffer load answers with zeros) or its row index
-    // (transforming gathers; -1 when missing), at a fixed stride of 27.
+    // (64-bit gathers; -1 when missing), at a fixed stride of 27.
     auto rows_of = [&](const Cursor &c, int32_t (&jn)[APT]) __attribute__((always_inline)) {
 #pragma unroll
         for (int q = 0; q < APT; ++q) jn[q] = rows[((tid + q * 256) / PPR) * kMaxKvol + c.o];
@@ -900,6 +858,7 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
 
     // ---- stage this tile's neighbour rows and offset mask
     auto staged = [&](bool valid, int32_t j) __attribute__((always_inline)) {
+        j >>= a.row_shift;
         if constexpr (XF == 0) return valid ? j * a.cin * ES : static_cast<int32_t>(0x80000000u);
         else return valid ? j : -1;
     };

@@ -115,6 +115,9 @@ def test_conv_plan_names_the_launched_kernel(s3dx, monkeypatch):
     assert s3dx.SparseConv(96, 96, 27, s3dx.BF16).plan(n, n).startswith("mfma tiling=2 ")
     # Cout not a multiple of 32: the generic kernel.
     assert s3dx.SparseConv(16, 40, 27, s3dx.F32).plan(100, 100) == "generic rows=64 cols=64 ln=none grid=2x1"
+    # The parent repeat alone is a shift of the staged rows, no pre-pass.
+    skip = s3dx.SparseConv(192, 192, 1, s3dx.BF16).set_gather_parent(True)
+    assert skip.plan(n, 8 * n).startswith("parent-rows mfma tiling=")
     monkeypatch.setenv("S3DX_CONV_TILING", "10")
     assert c128.plan(n, n).startswith("mfma tiling=10 rows=128 cols=128")
     with pytest.raises(s3dx.S3dxError):

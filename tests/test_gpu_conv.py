@@ -102,15 +102,18 @@ def test_mesh_layout_minus_one_sentinel(s3dx, O, W, dtype):
 
 
 @pytest.mark.parametrize("dtype", [0, 1])
-@pytest.mark.parametrize("cin,cout", [(64, 64), (24, 40)])
-def test_gather_parent_slot_offset_and_input_affine(s3dx, O, W, dtype, cin, cout):
+@pytest.mark.parametrize("cin,cout", [(64, 64), (24, 40), (20, 64)])
+@pytest.mark.parametrize("slot_on,affine_on", [(True, True), (True, False), (False, True)])
+def test_gather_parent_slot_offset_and_input_affine(s3dx, O, W, dtype, cin, cout, slot_on, affine_on):
     # conv over subdivided children whose features are silu(GN-affine(parent))
-    # repeated x8 plus a per-slot offset, without materialising the repeat.
+    # repeated x8, plus a per-slot offset when set.  cin 20 takes the
+    # per-element transform pass; without slot offsets the parent rows are
+    # transformed and the gather reads row j >> 3.
     parents = W.shell_64(res=24, centre=(12.0, 12.0, 12.0), radius=7.0)
     p = parents.shape[0]
     child, kmap = O.subdivide2(parents)
     n = 8 * p
-    print(f"gather-parent dtype={dtype} p={p} cin={cin}", flush=True)
+    print(f"gather-parent dtype={dtype} p={p} cin={cin} slot={slot_on} affine={affine_on}", flush=True)
     xp = W.normal_f32(6, 1, (p, cin))
     slot = W.normal_f32(6, 2, (8, cin), 0.02)
     scale = W.normal_f32(6, 3, (cin,), 0.5) + 1.0
@@ -120,15 +123,43 @@ def test_gather_parent_slot_offset_and_input_affine(s3dx, O, W, dtype, cin, cout
     ds, dh = s3dx.DeviceArray.from_host(scale), s3dx.DeviceArray.from_host(shift)
 
     def setup(conv):
-        conv.set_gather_parent(True, slot)
-        conv.set_input_affine_silu(ds, dh)
+        conv.set_gather_parent(True, slot if slot_on else None)
+        if affine_on:
+            conv.set_input_affine_silu(ds, dh)
+        plan = conv.plan(p, n)
+        assert plan.startswith("pre=children " if slot_on else "pre=rows parent-rows "), plan
 
     got = gpu_conv(s3dx, xp, kmap, p, w, s3dx.WEIGHT_MESH, b, dtype, cout, n_out=n, setup=setup)
     xr = rnd(s3dx, xp, dtype)
-    xc = O.repeat_children(xr) + np.tile(slot, (p, 1))
-    act = O.silu(xc * scale + shift)
+    xc = O.repeat_children(xr) + (np.tile(slot, (p, 1)) if slot_on else 0.0)
+    act = O.silu(xc * scale + shift) if affine_on else xc
     ref = O.conv(rnd(s3dx, act, dtype), kmap, n, rnd(s3dx, w, dtype), 1, cout, b)
     assert rel_l2(got, ref) <= TOL[dtype] * (2 if dtype == 0 else 1)
+
+
+def test_transform_buffer_regrows(s3dx, O, W):
+    # One layer object run on a small, a larger, then the small parent set:
+    # the transformed-input buffer grows once and stays valid.
+    dtype, cin, cout = 1, 64, 64
+    slot = W.normal_f32(8, 2, (8, cin), 0.02)
+    w = W.conv_weight(8, 5, cin, cout, layout="mesh")
+    conv = (s3dx.SparseConv(cin, cout, 27, dtype).set_weights(w, s3dx.WEIGHT_MESH, None)
+            .set_gather_parent(True, slot))
+    for radius in (4.0, 7.0, 4.0):
+        parents = W.shell_64(res=24, centre=(12.0, 12.0, 12.0), radius=radius)
+        p = parents.shape[0]
+        _, kmap = O.subdivide2(parents)
+        n = 8 * p
+        print(f"regrow p={p}", flush=True)
+        xp = W.normal_f32(8, int(radius), (p, cin))
+        y = s3dx.DeviceArray((n, cout), np.uint16)
+        conv.run(s3dx.DeviceArray.from_host(W.f32_to_bf16_bits(xp)), p,
+                 s3dx.DeviceArray.from_host(kmap), n, y, dtype)
+        h = y.download()
+        got = W.bf16_bits_to_f32(h).reshape(h.shape)
+        xc = O.repeat_children(rnd(s3dx, xp, dtype)) + np.tile(slot, (p, 1))
+        ref = O.conv(rnd(s3dx, xc, dtype), kmap, n, rnd(s3dx, w, dtype), 1, cout, None)
+        assert rel_l2(got, ref) <= TOL[dtype]
 
 
 @pytest.mark.parametrize("dtype", [0, 1])
