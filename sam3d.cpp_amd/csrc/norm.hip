@@ -63,89 +63,158 @@ add_kernel(const void *a, const void *b, int64_t count, void *y) {
         st<T>(y, i, ld<T>(a, i) + ld<T>(b, i));
 }
 
-// GroupNorm statistics, pass 1 (centre == nullptr: plain sums) or pass 2
-// (sums of squared deviations from the group mean).  Block (64 x 4): x over
-// channels, y over rows; writes per-block per-channel partials.
-constexpr int kStatBlocks = 512;
-constexpr int kMaxChanPerThread = 16;  // c <= 1024
+// GroupNorm statistics in one pass over x.  Each channel's values are
+// shifted by its row-0 value K (the shifted-data variance method), so
+// sum (x - K) and sum (x - K)^2 stay well conditioned when |mean| >> std.
+// Block b owns a contiguous run of rows; a thread owns VE*MP channels of one
+// row slot (pieces of VE channels, 16-byte loads when VE > 1) and walks the
+// run `rstep` rows at a time.  Writes per-block per-channel partial sums
+// partials[b][0][ch] and partials[b][1][ch]; gn_finalize_kernel combines
+// them per group in double, in a fixed order.
+constexpr int kStatBlocks = 1024;
+constexpr int kMaxGnChannels = 1024;
 
-template <class T>
+template <class T, int VE>
+__device__ __forceinline__ void load_piece(const void *x, int64_t off, float (&v)[VE]) {
+    if constexpr (VE == 1) {
+        v[0] = ld<T>(x, off);
+    } else {
+        const uint4 raw = *reinterpret_cast<const uint4 *>(static_cast<const T *>(x) + off);
+        const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
+        if constexpr (sizeof(T) == 2) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                v[2 * k] = bf16_to_f32(static_cast<uint16_t>(w4[k] & 0xffffu));
+                v[2 * k + 1] = bf16_to_f32(static_cast<uint16_t>(w4[k] >> 16));
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) v[k] = __builtin_bit_cast(float, w4[k]);
+        }
+    }
+}
+
+template <class T, int VE, int MP>
 __global__ void __launch_bounds__(256)
-gn_partial_kernel(const void *x, int64_t n, int32_t c, int32_t cg, const double *group_mean,
-                  float *partials) {
-    __shared__ float red[4][1024];
-    const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+gn_sums_kernel(const void *x, int64_t n, int32_t c, float *partials) {
+    __shared__ float red[2][2048];
+    const int ppr = c / VE;                 // pieces per row
+    const int tpr = ppr < 256 ? ppr : 256;  // threads per row slot
+    const int rstep = 256 / tpr;
+    const int tid = threadIdx.x;
+    const int roff = tid / tpr, p0 = tid - roff * tpr;
+    const bool active = roff < rstep;
     const int64_t rows_per = (n + gridDim.x - 1) / gridDim.x;
     const int64_t r0 = static_cast<int64_t>(blockIdx.x) * rows_per;
     const int64_t r1 = min(n, r0 + rows_per);
-    float acc[kMaxChanPerThread];
-    float centre[kMaxChanPerThread];
+    float k[MP][VE], s[MP][VE], q[MP][VE];
 #pragma unroll
-    for (int q = 0; q < kMaxChanPerThread; ++q) {
-        acc[q] = 0.0f;
-        const int ch = tx + q * 64;
-        centre[q] = (group_mean && ch < c) ? static_cast<float>(group_mean[ch / cg]) : 0.0f;
+    for (int i = 0; i < MP; ++i) {
+        const int p = p0 + i * tpr;
+        if (active && p < ppr) load_piece<T, VE>(x, static_cast<int64_t>(p) * VE, k[i]);
+#pragma unroll
+        for (int e = 0; e < VE; ++e) {
+            s[i][e] = 0.0f;
+            q[i][e] = 0.0f;
+        }
     }
-    for (int64_t r = r0 + ty; r < r1; r += 4) {
+    if (active) {
+#pragma unroll 4
+        for (int64_t r = r0 + roff; r < r1; r += rstep) {
 #pragma unroll
-        for (int q = 0; q < kMaxChanPerThread; ++q) {
-            const int ch = tx + q * 64;
-            if (ch < c) {
-                const float v = ld<T>(x, r * c + ch);
-                if (group_mean) {
-                    const float d = v - centre[q];
-                    acc[q] += d * d;
-                } else {
-                    acc[q] += v;
+            for (int i = 0; i < MP; ++i) {
+                const int p = p0 + i * tpr;
+                if (MP > 1 && p >= ppr) continue;
+                float v[VE];
+                load_piece<T, VE>(x, r * c + static_cast<int64_t>(p) * VE, v);
+#pragma unroll
+                for (int e = 0; e < VE; ++e) {
+                    const float d = v[e] - k[i][e];
+                    s[i][e] += d;
+                    q[i][e] += d * d;
                 }
             }
         }
-    }
 #pragma unroll
-    for (int q = 0; q < kMaxChanPerThread; ++q) {
-        const int ch = tx + q * 64;
-        if (ch < c) red[ty][ch] = acc[q];
+        for (int i = 0; i < MP; ++i) {
+            const int p = p0 + i * tpr;
+            if (MP > 1 && p >= ppr) continue;
+#pragma unroll
+            for (int e = 0; e < VE; ++e) {
+                red[0][roff * c + p * VE + e] = s[i][e];
+                red[1][roff * c + p * VE + e] = q[i][e];
+            }
+        }
     }
     __syncthreads();
-    for (int ch = threadIdx.x; ch < c; ch += 256)
-        partials[static_cast<int64_t>(blockIdx.x) * c + ch] =
-            (red[0][ch] + red[1][ch]) + (red[2][ch] + red[3][ch]);
+    for (int ch = tid; ch < c; ch += 256) {
+        float ts = 0.0f, tq = 0.0f;
+        for (int j = 0; j < rstep; ++j) {
+            ts += red[0][j * c + ch];
+            tq += red[1][j * c + ch];
+        }
+        float *out = partials + static_cast<int64_t>(blockIdx.x) * 2 * c;
+        out[ch] = ts;
+        out[c + ch] = tq;
+    }
 }
 
-// Reduce partials over blocks per group (double), in a fixed order.
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) v += __shfl_xor(v, d, 64);
+    return v;
+}
+
+// One block per group: per-channel totals over the blocks (a wave per
+// channel), then the group mean and centred variance from the shifted sums
+//   sum_r (x - m)^2 = sum_r (x - K)^2 - 2 (m - K) sum_r (x - K) + n (m - K)^2,
+// then scale = gamma * rstd, shift = beta - m * gamma * rstd per channel.
+template <class T>
 __global__ void __launch_bounds__(256)
-gn_reduce_kernel(const float *partials, int nblocks, int32_t c, int32_t cg, int32_t groups,
-                 double denom, double *group_out) {
-    // one block per group
+gn_finalize_kernel(const void *x, const float *partials, int nblocks, int64_t n, int32_t c,
+                   int32_t cg, float eps, const float *gamma, const float *beta, float *scale,
+                   float *shift) {
+    __shared__ double t1[kMaxGnChannels], t2[kMaxGnChannels];
+    __shared__ double stats[2];
     const int g = blockIdx.x;
-    if (g >= groups) return;
-    __shared__ double red[256];
-    double s = 0.0;
-    const int items = nblocks * cg;
-    for (int i = threadIdx.x; i < items; i += 256) {
-        const int blk = i / cg, ch = g * cg + (i - (i / cg) * cg);
-        s += static_cast<double>(partials[static_cast<int64_t>(blk) * c + ch]);
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    for (int cl = wave; cl < cg; cl += 4) {
+        const int ch = g * cg + cl;
+        double a = 0.0, b = 0.0;
+        for (int blk = lane; blk < nblocks; blk += 64) {
+            a += static_cast<double>(partials[static_cast<int64_t>(blk) * 2 * c + ch]);
+            b += static_cast<double>(partials[static_cast<int64_t>(blk) * 2 * c + c + ch]);
+        }
+        a = wave_sum_f64(a);
+        b = wave_sum_f64(b);
+        if (lane == 0) {
+            t1[cl] = a;
+            t2[cl] = b;
+        }
     }
-    red[threadIdx.x] = s;
     __syncthreads();
-    for (int d = 128; d > 0; d >>= 1) {
-        if (threadIdx.x < d) red[threadIdx.x] += red[threadIdx.x + d];
-        __syncthreads();
+    if (threadIdx.x == 0) {
+        const double dn = static_cast<double>(n);
+        double sum = 0.0;
+        for (int cl = 0; cl < cg; ++cl) sum += static_cast<double>(ld<T>(x, g * cg + cl)) * dn + t1[cl];
+        const double m = sum / (dn * cg);
+        double ss = 0.0;
+        for (int cl = 0; cl < cg; ++cl) {
+            const double dk = m - static_cast<double>(ld<T>(x, g * cg + cl));
+            ss += t2[cl] - 2.0 * dk * t1[cl] + dn * dk * dk;
+        }
+        const double var = ss / (dn * cg);
+        stats[0] = m;
+        stats[1] = 1.0 / sqrt((var > 0.0 ? var : 0.0) + static_cast<double>(eps));
     }
-    if (threadIdx.x == 0) group_out[g] = red[0] / denom;
-}
-
-__global__ void gn_finalize_kernel(const double *mean, const double *var, int32_t c, int32_t cg,
-                                   float eps, const float *gamma, const float *beta, float *scale,
-                                   float *shift) {
-    const int ch = blockIdx.x * blockDim.x + threadIdx.x;
-    if (ch >= c) return;
-    const int g = ch / cg;
-    const double rstd = 1.0 / sqrt(var[g] + static_cast<double>(eps));
-    const double ga = gamma ? gamma[ch] : 1.0;
-    const double be = beta ? beta[ch] : 0.0;
-    scale[ch] = static_cast<float>(ga * rstd);
-    shift[ch] = static_cast<float>(be - mean[g] * ga * rstd);
+    __syncthreads();
+    for (int cl = threadIdx.x; cl < cg; cl += 256) {
+        const int ch = g * cg + cl;
+        const double ga = gamma ? gamma[ch] : 1.0;
+        const double be = beta ? beta[ch] : 0.0;
+        scale[ch] = static_cast<float>(ga * stats[1]);
+        shift[ch] = static_cast<float>(be - stats[0] * ga * stats[1]);
+    }
 }
 
 template <class TI, class TO>
@@ -220,20 +289,12 @@ unsigned grid_for(int64_t count) {
     } while (0)
 
 struct GnLayout {
-    float *partials;
-    double *mean, *var;
+    float *partials;  // [kStatBlocks][2][c]
 };
 template <class W>
-void gn_layout(W &w, int32_t c, int32_t groups, GnLayout *l) {
-    if constexpr (std::is_same_v<W, Carver>) {
-        l->partials = w.template take<float>(static_cast<uint64_t>(kStatBlocks) * c);
-        l->mean = w.template take<double>(groups);
-        l->var = w.template take<double>(groups);
-    } else {
-        w.template take<float>(static_cast<uint64_t>(kStatBlocks) * c);
-        w.template take<double>(groups);
-        w.template take<double>(groups);
-    }
+void gn_layout(W &w, int32_t c, GnLayout *l) {
+    if constexpr (std::is_same_v<W, Carver>) l->partials = w.template take<float>(static_cast<uint64_t>(kStatBlocks) * 2 * c);
+    else w.template take<float>(static_cast<uint64_t>(kStatBlocks) * 2 * c);
 }
 
 }  // namespace
@@ -286,9 +347,9 @@ S3DX_API s3dx_status s3dx_groupnorm_workspace_size(int64_t n, int32_t c, int32_t
     return boundary(error, error_capacity, [&] {
         require(bytes != nullptr, "bytes is NULL");
         require(n > 0 && c > 0 && groups > 0 && c % groups == 0, "invalid GroupNorm shape");
-        require(c <= 64 * kMaxChanPerThread, "GroupNorm supports at most 1024 channels");
+        require(c <= kMaxGnChannels, "GroupNorm supports at most 1024 channels");
         Sizer s;
-        gn_layout(s, c, groups, nullptr);
+        gn_layout(s, c, nullptr);
         *bytes = s.used;
     });
 }
@@ -302,29 +363,28 @@ S3DX_API s3dx_status s3dx_groupnorm_stats(const void *x, int32_t x_dtype, int64_
     return boundary(error, error_capacity, [&] {
         require(x && scale && shift && workspace, "NULL argument");
         require(n > 0 && c > 0 && groups > 0 && c % groups == 0, "invalid GroupNorm shape");
-        require(c <= 64 * kMaxChanPerThread, "GroupNorm supports at most 1024 channels");
+        require(c <= kMaxGnChannels, "GroupNorm supports at most 1024 channels");
         require_dtype(x_dtype);
         const hipStream_t s = as_stream(stream);
         Carver w(workspace, workspace_bytes);
         GnLayout l;
-        gn_layout(w, c, groups, &l);
+        gn_layout(w, c, &l);
         const int cg = c / groups;
-        const double denom = static_cast<double>(n) * cg;
         const bool bf = x_dtype == S3DX_BF16;
-        // pass 1: means
-        if (bf) gn_partial_kernel<uint16_t><<<kStatBlocks, 256, 0, s>>>(x, n, c, cg, nullptr, l.partials);
-        else gn_partial_kernel<float><<<kStatBlocks, 256, 0, s>>>(x, n, c, cg, nullptr, l.partials);
-        launch_check("gn_partial");
-        gn_reduce_kernel<<<groups, 256, 0, s>>>(l.partials, kStatBlocks, c, cg, groups, denom, l.mean);
-        launch_check("gn_reduce");
-        // pass 2: centred variance
-        if (bf) gn_partial_kernel<uint16_t><<<kStatBlocks, 256, 0, s>>>(x, n, c, cg, l.mean, l.partials);
-        else gn_partial_kernel<float><<<kStatBlocks, 256, 0, s>>>(x, n, c, cg, l.mean, l.partials);
-        launch_check("gn_partial");
-        gn_reduce_kernel<<<groups, 256, 0, s>>>(l.partials, kStatBlocks, c, cg, groups, denom, l.var);
-        launch_check("gn_reduce");
-        gn_finalize_kernel<<<(c + 255) / 256, 256, 0, s>>>(l.mean, l.var, c, cg, eps, gamma, beta,
-                                                           scale, shift);
+        // 16-byte pieces when rows are whole pieces and x is 16-byte aligned.
+        const bool vec = c % (bf ? 8 : 4) == 0 && (reinterpret_cast<uintptr_t>(x) & 15) == 0;
+        if (bf) {
+            if (vec) gn_sums_kernel<uint16_t, 8, 1><<<kStatBlocks, 256, 0, s>>>(x, n, c, l.partials);
+            else gn_sums_kernel<uint16_t, 1, 4><<<kStatBlocks, 256, 0, s>>>(x, n, c, l.partials);
+        } else {
+            if (vec) gn_sums_kernel<float, 4, 1><<<kStatBlocks, 256, 0, s>>>(x, n, c, l.partials);
+            else gn_sums_kernel<float, 1, 4><<<kStatBlocks, 256, 0, s>>>(x, n, c, l.partials);
+        }
+        launch_check("gn_sums");
+        if (bf) gn_finalize_kernel<uint16_t><<<groups, 256, 0, s>>>(x, l.partials, kStatBlocks, n, c, cg, eps,
+                                                                     gamma, beta, scale, shift);
+        else gn_finalize_kernel<float><<<groups, 256, 0, s>>>(x, l.partials, kStatBlocks, n, c, cg, eps, gamma,
+                                                               beta, scale, shift);
         launch_check("gn_finalize");
     });
 }

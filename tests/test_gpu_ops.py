@@ -30,15 +30,34 @@ def test_layernorm_rows(s3dx, O, W, c):
     assert rel_l2(got, O.layernorm(W.round_bf16(x), 1e-6)) <= 1e-2
 
 
-@pytest.mark.parametrize("n,c", [(5000, 96), (40000, 192), (3000, 768)])
-def test_groupnorm_stats_and_affine(s3dx, O, W, n, c):
-    x = W.normal_f32(12, 1, (n, c), 1.5) + W.normal_f32(12, 2, (c,), 2.0)
+@pytest.mark.parametrize("n,c,groups,mean,std", [
+    (5000, 96, 32, 2.0, 1.5), (40000, 192, 32, 2.0, 1.5), (3000, 768, 32, 2.0, 1.5),
+    (20000, 96, 32, 300.0, 0.05),  # |mean| >> std: the shifted sums keep the variance
+    (700, 36, 4, 1.0, 1.0),        # rows not whole 16-byte pieces: per-element loads
+    (3, 64, 32, 0.0, 1.0),         # fewer rows than blocks
+])
+def test_groupnorm_stats_and_affine(s3dx, O, W, n, c, groups, mean, std):
+    x = W.normal_f32(12, 1, (n, c), std) + W.normal_f32(12, 2, (c,), 2.0) + np.float32(mean)
+    x = x.astype(np.float32)
     g, b = W.normal_f32(12, 3, (c,)), W.normal_f32(12, 4, (c,))
     dx = dev(s3dx, x)
-    scale, shift, _ = s3dx.groupnorm_stats(dx, s3dx.F32, n, c, 32, 1e-5, dev(s3dx, g), dev(s3dx, b))
+    scale, shift, _ = s3dx.groupnorm_stats(dx, s3dx.F32, n, c, groups, 1e-5, dev(s3dx, g), dev(s3dx, b))
     y = s3dx.DeviceArray((n, c), np.float32)
     s3dx.affine_rows(dx, s3dx.F32, n, c, scale, shift, True, y, s3dx.F32)
-    ref = O.silu(O.groupnorm(x, 32, 1e-5, g, b))
+    ref = O.silu(O.groupnorm(x, groups, 1e-5, g, b))
+    assert rel_l2(y.download(), ref) <= 1e-5
+
+
+@pytest.mark.parametrize("n,c", [(30000, 768), (100000, 96), (999, 40)])
+def test_groupnorm_stats_bf16_input(s3dx, O, W, n, c):
+    # bf16 rows: statistics of the stored (rounded) values, in float.
+    x = W.round_bf16(W.normal_f32(14, 1, (n, c), 1.5) + W.normal_f32(14, 2, (c,), 2.0))
+    g, b = W.normal_f32(14, 3, (c,)), W.normal_f32(14, 4, (c,))
+    dx = dev(s3dx, W.f32_to_bf16_bits(x))
+    scale, shift, _ = s3dx.groupnorm_stats(dx, s3dx.BF16, n, c, 8, 1e-5, dev(s3dx, g), dev(s3dx, b))
+    y = s3dx.DeviceArray((n, c), np.float32)
+    s3dx.affine_rows(dx, s3dx.BF16, n, c, scale, shift, False, y, s3dx.F32)
+    ref = O.groupnorm(x, 8, 1e-5, g, b)
     assert rel_l2(y.download(), ref) <= 1e-5
 
 
