@@ -189,16 +189,18 @@ def mesh_stack(s3dx, W, stream, seed, d0, p0, ch0, k0):
         conv1 = (s3dx.SparseConv(cin, cout, 27, bf)
                  .set_weights(W.conv_weight(seed, 550 + level, cin, cout, layout="mesh"), s3dx.WEIGHT_MESH, None)
                  .set_gather_parent(True))
-        skip = (s3dx.SparseConv(cin, cout, 1, bf)
-                .set_weights(W.conv_weight(seed, 560 + level, cin, cout, kvol=1, layout="mesh"), s3dx.WEIGHT_MESH, None)
-                .set_gather_parent(True))
-        conv2 = s3dx.SparseConv(cout, cout, 27, bf).set_weights(
+        # 1x1 skip of repeat_children(x) == repeat_children(1x1 skip of x): run
+        # it on the parents; conv2 adds residual row i >> 3.
+        skip = s3dx.SparseConv(cin, cout, 1, bf).set_weights(
+            W.conv_weight(seed, 560 + level, cin, cout, kvol=1, layout="mesh"), s3dx.WEIGHT_MESH, None)
+        conv2 = (s3dx.SparseConv(cout, cout, 27, bf).set_weights(
             W.conv_weight(seed, 570 + level, cout, cout, layout="mesh"), s3dx.WEIGHT_MESH, None)
+            .set_residual_parent(True))
         y1 = s3dx.DeviceArray((n, cout), np.uint16)
-        ys = s3dx.DeviceArray((n, cout), np.uint16)
+        ys = s3dx.DeviceArray((p, cout), np.uint16)
         y2 = s3dx.DeviceArray((n, cout), np.uint16)
         pairs = W.kmap_pairs(kmap.download(stream), n)
-        flops[level] = 2.0 * pairs * (cin * cout + cout * cout) + 2.0 * n * cin * cout
+        flops[level] = 2.0 * pairs * (cin * cout + cout * cout) + 2.0 * p * cin * cout
         gn1 = s3dx.groupnorm_stats(xp, bf, p, cin, 32, 1e-5, g1, b1, stream)
         gn2 = s3dx.groupnorm_stats(y1, bf, n, cout, 32, 1e-5, g2, b2, stream)
         conv1.set_input_affine_silu(gn1[0], gn1[1])
@@ -207,7 +209,7 @@ def mesh_stack(s3dx, W, stream, seed, d0, p0, ch0, k0):
         def run():
             s3dx.groupnorm_stats(xp, bf, p, cin, 32, 1e-5, g1, b1, stream, out=gn1)
             conv1.run(xp, p, kmap, n, y1, bf, None, stream)
-            skip.run(xp, p, None, n, ys, bf, None, stream)
+            skip.run(xp, p, None, p, ys, bf, None, stream)
             s3dx.groupnorm_stats(y1, bf, n, cout, 32, 1e-5, g2, b2, stream, out=gn2)
             conv2.run(y1, n, kmap, n, y2, bf, ys, stream)
         run.keep = (g1, b1, g2, b2, gn1, gn2)
@@ -234,8 +236,9 @@ def mesh_stack(s3dx, W, stream, seed, d0, p0, ch0, k0):
     return {**stages, "total_us": total, "parents": p0, "level0_children": n0, "level1_children": n1,
             "tflops": fl / total / 1e6, "dtype": "bf16 blocks, fp32 head",
             "note": "per block: GN32 stats, conv (GN affine+SiLU pass over the parents, gather of "
-                    "parent row j>>3), 1x1 skip, GN32 stats, conv (GN affine+SiLU pass) + skip as "
-                    "residual; the level-1 subdivide is outside the timed stages"}
+                    "parent row j>>3), 1x1 skip over the parents, GN32 stats, conv (GN affine+SiLU "
+                    "pass) + skip row i>>3 as residual; flops count the skip once per parent; the "
+                    "level-1 subdivide is outside the timed stages"}
 
 
 def copy_calibration(s3dx):

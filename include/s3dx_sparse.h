@@ -198,6 +198,14 @@ S3DX_API s3dx_status s3dx_conv_set_layernorm(s3dx_conv *conv, int32_t enable, fl
                                              uint64_t error_capacity);
 S3DX_API s3dx_status s3dx_conv_set_silu(s3dx_conv *conv, int32_t enable, char *error,
                                         uint64_t error_capacity);
+/* Residual at parent resolution (enable 0/1): the residual passed to
+ * s3dx_conv_run holds ceil(n_out / 8) rows and output row i adds residual row
+ * i >> 3, i.e. repeat_children of a per-parent tensor.  The mesh block's skip
+ * (mesh_decoder_graph.cpp:125-131) is a 1x1 conv of repeat_children(x), which
+ * equals repeat_children of the 1x1 conv of x: run the skip on the parents
+ * and let the block's second conv add it this way. */
+S3DX_API s3dx_status s3dx_conv_set_residual_parent(s3dx_conv *conv, int32_t enable, char *error,
+                                                   uint64_t error_capacity);
 /* Runs the layer.  x [n_in or n_in parents][cin] in the conv's dtype; kmap
  * [n_out][kvol] (NULL only for kvol 1); residual [n_out][cout] in y_dtype or
  * NULL; y [n_out][cout] in y_dtype.  Asynchronous on `stream`. */

@@ -195,11 +195,12 @@ __global__ void __launch_bounds__(256) conv_generic_kernel(ConvArgs a) {
             float t = acc[i][jj] + (a.bias ? a.bias[col] : 0.0f);
             if (a.silu) t = silu(t);
             const int64_t off = row * a.cout + col;
+            const int64_t roff = (row >> a.residual_shift) * a.cout + col;
             if (a.y_bf16) {
-                if (a.residual) t += bf16_to_f32(static_cast<const uint16_t *>(a.residual)[off]);
+                if (a.residual) t += bf16_to_f32(static_cast<const uint16_t *>(a.residual)[roff]);
                 static_cast<uint16_t *>(a.y)[off] = f32_to_bf16(t);
             } else {
-                if (a.residual) t += static_cast<const float *>(a.residual)[off];
+                if (a.residual) t += static_cast<const float *>(a.residual)[roff];
                 static_cast<float *>(a.y)[off] = t;
             }
         }
@@ -213,8 +214,8 @@ void layernorm_rows_launch(const void *x, int32_t x_dtype, int64_t n, int32_t c,
                            const float *w, const float *b, const float *mod_scale,
                            const float *mod_shift, int32_t silu, void *y, int32_t y_dtype,
                            hipStream_t stream);
-void add_rows_launch(const void *a, const void *b, int32_t dtype, int64_t count, void *y,
-                     hipStream_t stream);
+void add_rows_launch(const void *a, const void *b, int32_t dtype, int64_t n, int32_t c,
+                     int32_t b_shift, void *y, hipStream_t stream);
 
 }  // namespace s3dx
 
@@ -231,6 +232,7 @@ struct s3dx_conv {
     bool gather_parent = false;
     const float *pre_scale = nullptr, *pre_shift = nullptr;  // caller-owned device
     bool ln = false, silu = false;
+    bool residual_parent = false;  // residual has one row per 8 output rows
     float eps = 1e-6f;
     float *ln_w = nullptr, *ln_b = nullptr, *mod_scale = nullptr, *mod_shift = nullptr;
     bool weights_set = false;
@@ -550,6 +552,14 @@ S3DX_API s3dx_status s3dx_conv_set_silu(s3dx_conv *conv, int32_t enable, char *e
     });
 }
 
+S3DX_API s3dx_status s3dx_conv_set_residual_parent(s3dx_conv *conv, int32_t enable, char *error,
+                                                   uint64_t error_capacity) {
+    return boundary(error, error_capacity, [&] {
+        require(conv != nullptr, "conv is NULL");
+        conv->residual_parent = enable != 0;
+    });
+}
+
 S3DX_API s3dx_status s3dx_conv_plan(const s3dx_conv *conv, int64_t n_in, int64_t n_out, char *plan,
                                     uint64_t plan_capacity, char *error, uint64_t error_capacity) {
     return boundary(error, error_capacity, [&] {
@@ -627,6 +637,7 @@ S3DX_API s3dx_status s3dx_conv_run(const s3dx_conv *conv, const void *x, int64_t
         a.bias = conv->bias;
         a.cout = conv->cout;
         a.residual = residual;
+        a.residual_shift = conv->residual_parent ? 3 : 0;
         a.y = y;
         a.y_bf16 = y_dtype == S3DX_BF16;
         a.silu = conv->silu;
@@ -659,7 +670,8 @@ S3DX_API s3dx_status s3dx_conv_run(const s3dx_conv *conv, const void *x, int64_t
         if (conv->ln && !a.ln) {
             layernorm_rows_launch(y, y_dtype, n_out, conv->cout, conv->eps, conv->ln_w, conv->ln_b,
                                   conv->mod_scale, conv->mod_shift, conv->silu ? 1 : 0, y, y_dtype, s);
-            if (residual) add_rows_launch(y, residual, y_dtype, n_out * conv->cout, y, s);
+            if (residual)
+                add_rows_launch(y, residual, y_dtype, n_out, conv->cout, conv->residual_parent ? 3 : 0, y, s);
         }
     });
 }

@@ -21,6 +21,7 @@ struct ConvArgs {
     const float *bias;
     int32_t cout;
     const void *residual;
+    int32_t residual_shift;  // output row i adds residual row i >> residual_shift
     void *y;
     int32_t y_bf16;
     int32_t row_shift;  // kmap entry j reads source row j >> row_shift (3: parent of child j)
@@ -190,7 +191,7 @@ __device__ __forceinline__ void load_residual(const ConvArgs &a, int64_t m0, int
         res[p][0] = res[p][1] = make_uint4(0, 0, 0, 0);
         const int rl = p * RM::RPP + rsub;
         if (!a.residual || rsub >= RM::RPP || rl >= tile_rows) continue;
-        const int64_t off = (m0 + rl) * a.cout + col0;
+        const int64_t off = ((m0 + rl) >> a.residual_shift) * a.cout + col0;
         if (a.y_bf16) {
             res[p][0] = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.residual) + off);
         } else {

@@ -54,13 +54,17 @@ layernorm_kernel(const void *x, int64_t n, int32_t c, float eps, const float *w,
     }
 }
 
+// y[r][ch] = a[r][ch] + b[r >> b_shift][ch].
 template <class T>
 __global__ void __launch_bounds__(256)
-add_kernel(const void *a, const void *b, int64_t count, void *y) {
+add_kernel(const void *a, const void *b, int64_t n, int32_t c, int32_t b_shift, void *y) {
+    const int64_t count = n * c;
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
     for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count;
-         i += stride)
-        st<T>(y, i, ld<T>(a, i) + ld<T>(b, i));
+         i += stride) {
+        const int64_t r = i / c;
+        st<T>(y, i, ld<T>(a, i) + ld<T>(b, (r >> b_shift) * c + (i - r * c)));
+    }
 }
 
 // GroupNorm statistics in one pass over x.  Each channel's values are
@@ -309,10 +313,11 @@ void layernorm_rows_launch(const void *x, int32_t x_dtype, int64_t n, int32_t c,
     launch_check("layernorm");
 }
 
-void add_rows_launch(const void *a, const void *b, int32_t dtype, int64_t count, void *y,
-                     hipStream_t stream) {
-    if (dtype == S3DX_BF16) add_kernel<uint16_t><<<grid_for(count), 256, 0, stream>>>(a, b, count, y);
-    else add_kernel<float><<<grid_for(count), 256, 0, stream>>>(a, b, count, y);
+void add_rows_launch(const void *a, const void *b, int32_t dtype, int64_t n, int32_t c,
+                     int32_t b_shift, void *y, hipStream_t stream) {
+    const int64_t count = n * c;
+    if (dtype == S3DX_BF16) add_kernel<uint16_t><<<grid_for(count), 256, 0, stream>>>(a, b, n, c, b_shift, y);
+    else add_kernel<float><<<grid_for(count), 256, 0, stream>>>(a, b, n, c, b_shift, y);
     launch_check("add");
 }
 

@@ -59,14 +59,15 @@ def _gn_dev(s3dx, x_dev, dtype, n, c, gamma, beta):
     return scale, shift, (g, bt, ws)
 
 
+@pytest.mark.parametrize("parent_skip", [False, True])
 @pytest.mark.parametrize("level,cin,cout,radius", [(0, 768, 192, 2.0), (1, 192, 96, 4.0)])
-def test_mesh_upsample_block(s3dx, O, W, level, cin, cout, radius):
+def test_mesh_upsample_block(s3dx, O, W, level, cin, cout, radius, parent_skip):
     dtype = s3dx.BF16
     parents = W.shell_64(res=12, centre=(6.0, 6.0, 6.0), radius=radius)
     p = parents.shape[0]
     child, kmap = O.subdivide2(parents)
     n = 8 * p
-    print(f"mesh block level={level} parents={p} children={n}", flush=True)
+    print(f"mesh block level={level} parents={p} children={n} parent_skip={parent_skip}", flush=True)
     seed = 40 + level
     x = W.normal_f32(seed, 1, (p, cin))
     g1, b1 = W.normal_f32(seed, 2, (cin,), 0.2) + 1.0, W.normal_f32(seed, 3, (cin,), 0.2)
@@ -86,13 +87,16 @@ def test_mesh_upsample_block(s3dx, O, W, level, cin, cout, radius):
              .set_gather_parent(True).set_input_affine_silu(s1, h1))
     y1 = s3dx.DeviceArray((n, cout), np.uint16)
     conv1.run(xd, p, dk, n, y1, dtype)
-    skip = (s3dx.SparseConv(cin, cout, 1, dtype).set_weights(ws, s3dx.WEIGHT_MESH, cs)
-            .set_gather_parent(True))
-    ys = s3dx.DeviceArray((n, cout), np.uint16)
-    skip.run(xd, p, None, n, ys, dtype)
+    # The skip on the repeated input, or once per parent with conv2 reading
+    # residual row i >> 3: the same values.
+    skip = s3dx.SparseConv(cin, cout, 1, dtype).set_weights(ws, s3dx.WEIGHT_MESH, cs)
+    skip.set_gather_parent(not parent_skip)
+    ns = p if parent_skip else n
+    ys = s3dx.DeviceArray((ns, cout), np.uint16)
+    skip.run(xd, p, None, ns, ys, dtype)
     s2, h2, keep2 = _gn_dev(s3dx, y1, dtype, n, cout, g2, b2)
     conv2 = (s3dx.SparseConv(cout, cout, 27, dtype).set_weights(w2, s3dx.WEIGHT_MESH, c2)
-             .set_input_affine_silu(s2, h2))
+             .set_input_affine_silu(s2, h2).set_residual_parent(parent_skip))
     y2 = s3dx.DeviceArray((n, cout), np.uint16)
     conv2.run(y1, n, dk, n, y2, dtype, ys)
     got = _host(s3dx, W, y2, dtype)

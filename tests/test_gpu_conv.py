@@ -137,6 +137,35 @@ def test_gather_parent_slot_offset_and_input_affine(s3dx, O, W, dtype, cin, cout
     assert rel_l2(got, ref) <= TOL[dtype] * (2 if dtype == 0 else 1)
 
 
+@pytest.mark.parametrize("dtype", [0, 1])
+@pytest.mark.parametrize("cout,ln", [(128, True), (160, True), (64, False), (40, False)])
+def test_residual_at_parent_resolution(s3dx, O, W, dtype, cout, ln):
+    # Output row i adds residual row i >> 3, through the fused-LN (128),
+    # separate-LN (160), plain MFMA (64) and generic (40) epilogues.
+    parents = W.shell_64(res=20, centre=(10.0, 10.0, 10.0), radius=5.0)
+    p = parents.shape[0]
+    _, kmap = O.subdivide2(parents)
+    n = 8 * p
+    print(f"residual parent dtype={dtype} cout={cout} ln={ln} n={n}", flush=True)
+    cin = 64
+    x = W.normal_f32(9, 1, (n, cin))
+    w = W.conv_weight(9, 2, cin, cout)
+    b = W.normal_f32(9, 3, (cout,))
+    res = W.normal_f32(9, 4, (p, cout))
+
+    def setup(conv):
+        conv.set_residual_parent(True)
+        if ln:
+            conv.set_layernorm(True, 1e-6).set_silu(True)
+
+    got = gpu_conv(s3dx, x, kmap, n, w, s3dx.WEIGHT_SLAT, b, dtype, cout, residual=res, setup=setup)
+    h = O.conv(rnd(s3dx, x, dtype), kmap, n, rnd(s3dx, w, dtype), 0, cout, b)
+    if ln:
+        h = O.silu(O.layernorm(h, 1e-6))
+    ref = h + O.repeat_children(rnd(s3dx, res, dtype))
+    assert rel_l2(got, ref) <= TOL[dtype] * (3 if dtype == 0 else 1)
+
+
 def test_transform_buffer_regrows(s3dx, O, W):
     # One layer object run on a small, a larger, then the small parent set:
     # the transformed-input buffer grows once and stays valid.
