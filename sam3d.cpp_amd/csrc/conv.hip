@@ -261,7 +261,8 @@ KernelFn tiling_kernel(int id, bool bf, int kc, bool xf) {
 // Picks the workgroup tiling for nb 32-column blocks per workgroup.  The
 // split-K kernel (each weight fragment loaded once per workgroup, straight
 // into the one wave that uses it) is preferred whenever it is compiled for
-// the shape; otherwise waves that own all 128 columns of a row (tiling 10)
+// the shape, with 128-channel tasks (32- or 64-channel chunks joined) ahead
+// of 64-channel ones; otherwise waves that own all 128 columns of a row (tiling 10)
 // gather each row once and stream two tasks per stage, and two 32-row blocks
 // per wave halve the LDS traffic per MFMA when that still leaves one
 // workgroup per CU.  S3DX_CONV_TILING=<id> overrides (tuning).
@@ -282,7 +283,7 @@ const Tiling *choose_tiling(int64_t n_out, int nb, int ntiles, bool bf, int kc, 
     for (const Tiling &t : kTilings) {
         if (!usable(t)) continue;
         int rank;
-        if (t.splitk) rank = 0;
+        if (t.splitk) rank = t.id >= 15 ? 0 : 1;  // 128-channel tasks (chunks joined) first
         else if (t.wn == 1 && t.nbw == 4) rank = blocks(t) >= 192 ? 1 : 10;  // 32x128 wave tiles
         else if (t.mbw == 2) rank = blocks(t) >= 256 ? 2 : 20;
         else rank = 5;
@@ -299,10 +300,20 @@ struct LaunchPlan {
     bool mfma = false;      // MFMA kernel (else the generic VALU kernel)
     bool xf = false;        // 64-bit addressed gathers (source above 2 GiB)
     bool fused_ln = false;  // LayerNorm in the MFMA epilogue
+    int nb = 0, kc = 0;     // 32-column blocks per workgroup, channels per task
     const Tiling *tl = nullptr;
     KernelFn fn = nullptr;
     dim3 grid;
 };
+
+// Channels per task for nb column blocks: the largest of 128 / 64 / 32 that
+// divides cin and keeps one weight stage (kc x nb*32) within 32 KiB (FP32:
+// at most 64); 0 if none.
+int task_channels(int cin, int nb, bool bf) {
+    for (int cand : {128, 64, 32})
+        if (cin % cand == 0 && (bf || cand <= 64) && cand * nb * 32 * (bf ? 2 : 4) <= 32768) return cand;
+    return cin % 32 == 0 ? 32 : 0;
+}
 
 // What the conv gathers from: the caller's rows, or the transformed rows the
 // pre-pass writes (children when slot offsets are set), and the shift that
@@ -329,18 +340,46 @@ LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bo
     const bool bf = conv->dtype == S3DX_BF16;
     p.mfma = conv->mfma && aligned16;
     if (p.mfma) {
-        p.fused_ln = conv->ln && conv->nb * 32 == conv->cout;
         // Buffer-resource gathers address at most 2 GiB; larger inputs take
         // the XF=1 (64-bit addressed) variant.
         p.xf = x_bytes >= (int64_t(1) << 31);
-        const int ntiles = conv->cout / (32 * conv->nb);
         const int64_t w_bytes = static_cast<int64_t>(conv->kvol) * conv->cin * conv->cout * (bf ? 2 : 4);
-        p.tl = choose_tiling(n_out, conv->nb, ntiles, bf, conv->kc, p.xf, w_bytes < (int64_t(1) << 31));
-        require(p.tl != nullptr, "no MFMA kernel for this shape");
-        p.fn = tiling_kernel(p.tl->id, bf, conv->kc, p.xf);
+        const bool splitk_ok = w_bytes < (int64_t(1) << 31);
+        // The whole row per workgroup (conv->nb) unless a narrower column
+        // tile has a split-K kernel and no LayerNorm needs the full row:
+        // then each column tile re-gathers A (from L2), but every weight
+        // fragment is loaded once, straight into the wave that uses it.
+        // S3DX_CONV_NB=<blocks> overrides (tuning).
+        const int blocks = conv->cout / 32;
+        int forced = 0;
+        if (const char *e = std::getenv("S3DX_CONV_NB")) forced = std::atoi(e);
+        auto try_nb = [&](int nb) {
+            const int kc = task_channels(conv->cin, nb, bf);
+            if (kc == 0) return false;
+            const Tiling *t = choose_tiling(n_out, nb, blocks / nb, bf, kc, p.xf, splitk_ok);
+            if (!t) return false;
+            p.nb = nb;
+            p.kc = kc;
+            p.tl = t;
+            return true;
+        };
+        const bool use_forced =
+            forced > 0 && blocks % forced == 0 && (!conv->ln || forced * 32 == conv->cout) && try_nb(forced);
+        if (!use_forced) {
+            require(try_nb(conv->nb), "no MFMA kernel for this shape");
+            if (!p.tl->splitk && !conv->ln && conv->kvol == kMaxKvol) {
+                const LaunchPlan whole = p;
+                bool found = false;
+                for (int nb : {4, 3, 2})
+                    if (!found && nb < conv->nb && blocks % nb == 0 && try_nb(nb)) found = p.tl->splitk;
+                if (!found) p = whole;
+            }
+        }
+        p.fused_ln = conv->ln && p.nb * 32 == conv->cout;
+        p.fn = tiling_kernel(p.tl->id, bf, p.kc, p.xf);
         require(p.fn != nullptr, "no MFMA kernel for this shape");
         const int64_t mt = (n_out + p.tl->rows() - 1) / p.tl->rows();
-        p.grid = dim3(static_cast<unsigned>(mt), static_cast<unsigned>(ntiles));
+        p.grid = dim3(static_cast<unsigned>(mt), static_cast<unsigned>(blocks / p.nb));
     } else {
         p.grid = dim3(static_cast<unsigned>((n_out + kGM - 1) / kGM),
                       static_cast<unsigned>((conv->cout + kGN - 1) / kGN));
@@ -426,15 +465,7 @@ S3DX_API s3dx_status s3dx_conv_create(int32_t cin, int32_t cout, int32_t kvol, i
                     if (nb == 0 && blocks % cand == 0) nb = cand;
             }
         }
-        // Channels per task: keep one weight stage <= 32 KiB of LDS.
-        int kc = 0;
-        const int elem = bf ? 2 : 4;
-        for (int cand : {128, 64, 32}) {
-            if (kc == 0 && cin % cand == 0 && (!bf ? cand <= 64 : true) &&
-                cand * nb * 32 * elem <= 32768)
-                kc = cand;
-        }
-        if (kc == 0 && cin % 32 == 0 && nb != 0) kc = 32;
+        const int kc = nb != 0 ? task_channels(cin, nb, bf) : 0;
         c->mfma = kc != 0 && nb != 0;
         c->kc = kc;
         c->nb = nb;
@@ -572,7 +603,7 @@ S3DX_API s3dx_status s3dx_conv_plan(const s3dx_conv *conv, int64_t n_in, int64_t
         char text[256];
         if (p.mfma)
             std::snprintf(text, sizeof(text), "mfma tiling=%d%s rows=%d cols=%d kc=%d xf=%d ln=%s grid=%ux%u",
-                          p.tl->id, p.tl->splitk ? " split-k" : "", p.tl->rows(), p.tl->cols(), conv->kc,
+                          p.tl->id, p.tl->splitk ? " split-k" : "", p.tl->rows(), p.tl->cols(), p.kc,
                           p.xf ? 1 : 0, conv->ln ? (p.fused_ln ? "fused" : "separate") : "none", p.grid.x,
                           p.grid.y);
         else

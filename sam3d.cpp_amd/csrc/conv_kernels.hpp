@@ -39,7 +39,8 @@ using KernelFn = void (*)(ConvArgs);
 // Workgroup tilings of the MFMA kernel: 4 waves in WM x WN (WM = 4/WN), each
 // wave MBW x NBW blocks of 32x32 outputs.
 // Split-K tilings (splitk = 1): 128 rows x 32*nbw columns, each wave owning
-// the whole tile for a quarter of the k-steps.
+// the whole tile for a quarter of the k-steps.  Ids 15 and 16 (BF16, 32- or
+// 64-channel chunks) build each 128-channel task from 4 or 2 chunks.
 struct Tiling {
     int id, mbw, nbw, wn, splitk;
     int rows() const { return splitk ? 128 : 32 * mbw * (4 / wn); }
@@ -49,6 +50,7 @@ inline constexpr Tiling kTilings[] = {
     {0, 1, 1, 1, 0}, {1, 1, 1, 2, 0}, {2, 1, 3, 1, 0}, {3, 1, 2, 2, 0}, {4, 1, 3, 2, 0},
     {5, 1, 4, 2, 0}, {6, 2, 1, 2, 0}, {7, 2, 3, 1, 0}, {8, 2, 2, 2, 0}, {9, 2, 3, 2, 0},
     {10, 1, 4, 1, 0}, {11, 4, 4, 1, 1}, {12, 4, 2, 1, 1}, {13, 4, 3, 1, 1}, {14, 4, 1, 1, 1},
+    {15, 4, 3, 1, 1}, {16, 4, 4, 1, 1},
 };
 
 // MFMA kernel for tiling `id`, kc channels per task, xf 64-bit gathers;
@@ -664,7 +666,10 @@ struct SplitSmem {
     static constexpr int TOTAL = REGION0 + ROWS_BYTES + 128;
 };
 
-template <class T, int NB, int KC, int XF>
+// SUB > 1: a task is SUB consecutive sub-tasks (offset, KC/SUB-channel
+// chunk), so that Cin of 96 (32-channel chunks) or 192 (64) still gives each
+// wave whole k-steps of a 128-channel task.
+template <class T, int NB, int KC, int XF, int SUB>
 __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
     using SM = SplitSmem<T, NB, KC>;
     constexpr int E = Frag<T>::E;
@@ -676,6 +681,11 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
     constexpr int BM = SM::BM;
     constexpr int PPR = SM::ROWB / 16;       // 16-byte pieces per row
     constexpr int APT = BM * PPR / 256;      // pieces per thread per task
+    constexpr int KCS = KC / SUB;            // channels per sub-task
+    constexpr int KSS = KS / SUB;            // k-steps per sub-task
+    constexpr int PPS = PPR / SUB;           // pieces per sub-task row
+    static_assert(KC % SUB == 0 && KS % SUB == 0 && PPR % SUB == 0 && 256 % PPR == 0,
+                  "sub-tasks must be whole k-steps and whole pieces");
     __shared__ __align__(16) char smem[SM::TOTAL];
     float *stg = reinterpret_cast<float *>(smem);
     float *part = reinterpret_cast<float *>(smem + SM::STG_BYTES);
@@ -693,7 +703,7 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
     const int nbtot = a.cout / 32;
     const int kvol = a.kvol;
     const int ksteps_total = a.cin / CPK;
-    const int chunks = a.cin / KC;
+    const int chunks = a.cin / KCS;  // sub-task chunks per offset
     const int tile_rows = static_cast<int>(min(static_cast<int64_t>(BM), a.n_out - m0));
     const int32_t xbytes = static_cast<int32_t>(a.x_bytes < INT32_MAX ? a.x_bytes : INT32_MAX);
     constexpr int ES = static_cast<int>(sizeof(T));
@@ -705,10 +715,15 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
     const auto x_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(a.x), static_cast<short>(0),
                                                           xbytes, 0x00020000);
 
-    // Tasks are the (present offset, Cin chunk) pairs in ascending order.  A
-    // cursor walks them in scalar registers: the offsets not yet visited as a
-    // bit mask, the current offset and chunk.  Past the last task it stays
-    // on the last one (prefetches beyond the end reload it harmlessly).
+    // Sub-tasks are the (present offset, Cin chunk) pairs in ascending
+    // order.  A cursor walks them in scalar registers: the offsets not yet
+    // visited as a bit mask, the current offset and chunk.  Past the last
+    // sub-task it stays on the last one (prefetches beyond the end reload it
+    // harmlessly).  A task takes the next SUB sub-tasks, packed as 16-bit
+    // fields (offset | chunk << 5; chunks < 2048 as Cin <= 65536) of one
+    // scalar, not an array the compiler would move to memory; `left` counts
+    // the sub-tasks from its first one on, so those past the end
+    // (left <= k) gather and multiply zeros.
     struct Cursor {
         uint32_t rest;
         int o, kc;
@@ -721,16 +736,51 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
         c.kc = wrap ? (more ? 0 : c.kc) : c.kc + 1;
         c.rest = wrap && more ? (c.rest & (c.rest - 1u)) : c.rest;
     };
+    static_assert(SUB <= 4, "four 16-bit sub-task fields");
+    struct Task {
+        int o, kc;    // SUB == 1
+        uint64_t pk;  // SUB > 1
+        int left;
+    };
+    auto next_task = [&](Cursor &cur, int &left, Task &t) __attribute__((always_inline)) {
+        if constexpr (SUB == 1) {
+            advance(cur);
+            t.o = cur.o;
+            t.kc = cur.kc;
+        } else {
+            uint64_t pk = 0;
+#pragma unroll
+            for (int k = 0; k < SUB; ++k) {
+                advance(cur);
+                pk |= static_cast<uint64_t>(static_cast<uint32_t>(cur.o | (cur.kc << 5))) << (16 * k);
+            }
+            t.pk = pk;
+            t.left = left;
+            left -= SUB;
+        }
+    };
+    // (offset, chunk) of sub-task s (s may be per lane)
+    auto sub_o = [&](const Task &t, int s) __attribute__((always_inline)) {
+        return SUB == 1 ? t.o : static_cast<int>(static_cast<uint32_t>(t.pk >> (16 * s)) & 31u);
+    };
+    auto sub_kc = [&](const Task &t, int s) __attribute__((always_inline)) {
+        return SUB == 1 ? t.kc : static_cast<int>((static_cast<uint32_t>(t.pk >> (16 * s)) & 0xffffu) >> 5);
+    };
+    const int my_sub = (tid % PPR) / PPS;  // this thread's pieces all lie in one sub-task
     // Fragment (k-step ks, column block cb) of the packed weights sits at
     // byte ((ks * nbtot + cb) * 64 + lane) * 16.  With ROT (NB = 4) wave w
     // keeps column block (k + w) mod 4 in accumulator k, so the block it owns
     // in the final reduction is always accumulator 0.
     constexpr bool ROT = NB == 4;
-    auto load_b = [&](const Cursor &c, uint4 (&bf)[KSW][NB]) __attribute__((always_inline)) {
-        const int ks0 = c.o * ksteps_total + c.kc * KS + wave;
+    auto load_b = [&](const Task &t, uint4 (&bf)[KSW][NB]) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < KSW; ++i) {
-            const int32_t sbase = ((ks0 + 4 * i) * nbtot + nb0) * 1024;
+            // k-step wave + 4 i of the task: step (wave + 4 i) % KSS of
+            // sub-task (wave + 4 i) / KSS (wave-uniform, scalar)
+            const int s = wave + 4 * i, sub = s / KSS;
+            const int ks = sub_o(t, sub) * ksteps_total + sub_kc(t, sub) * KSS + (s - sub * KSS);
+            int32_t sbase = (ks * nbtot + nb0) * 1024;
+            if constexpr (SUB > 1) sbase = sub < t.left ? sbase : static_cast<int32_t>(0xC0000000u);
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
                 // the column block goes into the scalar offset (rotated) or the immediate
@@ -746,21 +796,38 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
     // the neighbour's byte offset in x (plain gathers; out of range when
     // missing, which the buffer load answers with zeros) or its row index
     // (64-bit gathers; -1 when missing), at a fixed stride of 27.
-    auto rows_of = [&](const Cursor &c, int32_t (&jn)[APT]) __attribute__((always_inline)) {
+    constexpr int32_t kNoRow = XF == 0 ? static_cast<int32_t>(0x80000000u) : -1;
+    auto rows_of = [&](const Task &t, int32_t (&jn)[APT]) __attribute__((always_inline)) {
+        const int o = sub_o(t, my_sub);
 #pragma unroll
-        for (int q = 0; q < APT; ++q) jn[q] = rows[((tid + q * 256) / PPR) * kMaxKvol + c.o];
-    };
-    auto gather = [&](const Cursor &c, int32_t j, int q) __attribute__((always_inline)) {
-        const int piece = (tid + q * 256) % PPR;
-        if constexpr (XF == 0) {
-            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
-                x_rsrc, static_cast<int32_t>(static_cast<uint32_t>(j) + piece * 16), c.kc * KC * ES, 0);
-            return make_uint4(v.x, v.y, v.z, v.w);
-        } else {
-            return load_fragment<T>(a, j, c.kc * KC + piece * E);
+        for (int q = 0; q < APT; ++q) {
+            jn[q] = rows[((tid + q * 256) / PPR) * kMaxKvol + o];
+            if constexpr (SUB > 1) jn[q] = my_sub < t.left ? jn[q] : kNoRow;
         }
     };
-    auto load_a = [&](const Cursor &c, uint4 (&ra)[APT]) __attribute__((always_inline)) {
+    auto gather = [&](const Task &t, int32_t j, int q) __attribute__((always_inline)) {
+        const int piece = (tid + q * 256) % PPR;
+        if constexpr (SUB == 1) {
+            if constexpr (XF == 0) {
+                const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
+                    x_rsrc, static_cast<int32_t>(static_cast<uint32_t>(j) + piece * 16), t.kc * KC * ES, 0);
+                return make_uint4(v.x, v.y, v.z, v.w);
+            } else {
+                return load_fragment<T>(a, j, t.kc * KC + piece * E);
+            }
+        } else {
+            // the chunk is per lane: it goes into the vector offset
+            const int c0 = sub_kc(t, my_sub) * KCS + (piece % PPS) * E;
+            if constexpr (XF == 0) {
+                const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
+                    x_rsrc, static_cast<int32_t>(static_cast<uint32_t>(j) + static_cast<uint32_t>(c0 * ES)), 0, 0);
+                return make_uint4(v.x, v.y, v.z, v.w);
+            } else {
+                return load_fragment<T>(a, j, c0);
+            }
+        }
+    };
+    auto load_a = [&](const Task &c, uint4 (&ra)[APT]) __attribute__((always_inline)) {
         int32_t jn[APT];
         rows_of(c, jn);
 #pragma unroll
@@ -825,7 +892,7 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
     constexpr int MJ = NMF2 / (NFR + 1);
     constexpr int MK = NMF2 - MJ * NFR;
     auto body = [&](const uint4 (&afc)[KSW][4], uint4 (&afn)[KSW][4], uint4 (&bc)[KSW][NB], char *wbuf,
-                    uint4 (&ra)[APT], Cursor &nx) __attribute__((always_inline)) {
+                    uint4 (&ra)[APT], Task &nx, Cursor &cur, int &left) __attribute__((always_inline)) {
         int32_t jn[APT];
         rows_of(nx, jn);
         mfma_range(std::integral_constant<int, 0>{}, std::integral_constant<int, HALF>{}, afc, bc);
@@ -854,7 +921,7 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
         }
         if constexpr (MK > 0) __builtin_amdgcn_sched_group_barrier(0x008, MK, 0);
         __builtin_amdgcn_sched_group_barrier(0x020, KSW * NB, 0); // VMEM read: weights
-        advance(nx);
+        next_task(cur, left, nx);
     };
 
     // ---- stage this tile's neighbour rows and offset mask
@@ -926,7 +993,8 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
     if (lane == 0 && my_mask) atomicOr(omask, my_mask);
     lds_barrier();
     const uint32_t mask = __builtin_amdgcn_readfirstlane(*omask);
-    const int ntasks = __popc(mask) * chunks;
+    const int nsub = __popc(mask) * chunks;
+    const int ntasks = (nsub + SUB - 1) / SUB;
 
     // ---- main loop.  Entering task t: A(t)'s fragments in registers, A(t+1)
     // on its way into ra, B(t) and B(t+1) in registers or on their way.
@@ -939,22 +1007,24 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
         // runs whole pairs; the peel's weights and fragments then live in the
         // other register sets, and the two LDS buffers swap roles.
         const bool odd = ntasks & 1;
-        Cursor nx{mask, -1, chunks - 1};
-        advance(nx);  // task 0
+        Cursor cur{mask, -1, chunks - 1};
+        int left = nsub;
+        Task nx;
+        next_task(cur, left, nx);  // task 0
         load_a(nx, ra);
         if (odd) load_b(nx, b1);
         else load_b(nx, b0);
 #pragma unroll
         for (int q = 0; q < APT; ++q) *a_slot(buf0, q) = ra[q];
-        advance(nx);  // task 1
+        next_task(cur, left, nx);  // task 1
         load_a(nx, ra);
         if (odd) load_b(nx, b0);
         else load_b(nx, b1);
-        advance(nx);  // task 2
+        next_task(cur, left, nx);  // task 2
         lds_barrier();
         if (odd) {
             read_frags(buf0, fy);
-            body(fy, fx, b1, buf1, ra, nx);
+            body(fy, fx, b1, buf1, ra, nx, cur, left);
             char *tmp = buf0;
             buf0 = buf1;
             buf1 = tmp;
@@ -962,8 +1032,8 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
             read_frags(buf0, fx);
         }
         for (int t = odd ? 1 : 0; t < ntasks; t += 2) {
-            body(fx, fy, b0, buf1, ra, nx);
-            body(fy, fx, b1, buf0, ra, nx);
+            body(fx, fy, b0, buf1, ra, nx, cur, left);
+            body(fy, fx, b1, buf0, ra, nx, cur, left);
         }
         lds_barrier();  // the last fragment reads finish before the tile reuses LDS
     }
@@ -1090,10 +1160,18 @@ KernelFn pick_tiling(int id) {
     case 11: case 12: case 13: case 14: {
         constexpr int KS = KC / (2 * Frag<T>::E);
         if constexpr (KS % 4 == 0) {
-            if (id == 11) return conv_splitk_kernel<T, 4, KC, XF>;
-            if (id == 12) return conv_splitk_kernel<T, 2, KC, XF>;
-            if (id == 13) return conv_splitk_kernel<T, 3, KC, XF>;
-            return conv_splitk_kernel<T, 1, KC, XF>;
+            if (id == 11) return conv_splitk_kernel<T, 4, KC, XF, 1>;
+            if (id == 12) return conv_splitk_kernel<T, 2, KC, XF, 1>;
+            if (id == 13) return conv_splitk_kernel<T, 3, KC, XF, 1>;
+            return conv_splitk_kernel<T, 1, KC, XF, 1>;
+        } else {
+            return nullptr;
+        }
+    }
+    case 15: case 16: {
+        if constexpr (sizeof(T) == 2 && XF == 0 && (KC == 32 || KC == 64)) {
+            if (id == 15) return conv_splitk_kernel<T, 3, 128, XF, 128 / KC>;
+            return conv_splitk_kernel<T, 4, 128, XF, 128 / KC>;
         } else {
             return nullptr;
         }

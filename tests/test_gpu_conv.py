@@ -279,6 +279,37 @@ def test_row_block_tilings(s3dx, O, W, monkeypatch, dtype, cin, cout, tiling):
     assert rel_l2(got, ref) <= TOL[dtype] * (3 if dtype == 0 else 1)
 
 
+@pytest.mark.parametrize("cin,cout,tiling,kvol", [
+    (96, 96, "15", 27), (192, 96, "15", 27), (96, 128, "16", 27), (192, 128, "16", 27),
+    (160, 96, "15", 27), (224, 128, "16", 27),  # 5 and 7 chunks: the last task is part empty
+    (96, 96, "15", 1), (160, 128, "16", 1),     # one task holding an empty sub-task
+])
+def test_subtask_tilings(s3dx, O, W, monkeypatch, cin, cout, tiling, kvol):
+    # Split-K tasks of 128 channels made of 32- or 64-channel chunks (bf16),
+    # with the fused LayerNorm + SiLU + residual epilogue.
+    monkeypatch.setenv("S3DX_CONV_TILING", tiling)
+    dtype = 1
+    coords = W.shells_union(1)[:2900]
+    n = coords.shape[0]
+    kmap = O.kmap_subm3(coords, n) if kvol == 27 else None
+    x = W.normal_f32(16, 1, (n, cin))
+    w = W.conv_weight(16, 2, cin, cout, kvol=kvol)
+    b = W.normal_f32(16, 3, (cout,))
+    res = W.normal_f32(16, 4, (n, cout))
+
+    def setup(conv):
+        conv.set_layernorm(True, 1e-6)
+        conv.set_silu(True)
+        plan = conv.plan(n, n)
+        print(f"subtask cin={cin} cout={cout} kvol={kvol}: {plan}", flush=True)
+        assert plan.startswith(f"mfma tiling={tiling} split-k"), plan
+
+    got = gpu_conv(s3dx, x, kmap, n, w, s3dx.WEIGHT_SLAT, b, dtype, cout, kvol=kvol, residual=res, setup=setup)
+    h = O.conv(rnd(s3dx, x, dtype), kmap, n, rnd(s3dx, w, dtype), 0, cout, b, kvol=kvol)
+    ref = O.silu(O.layernorm(h, 1e-6)) + rnd(s3dx, res, dtype)
+    assert rel_l2(got, ref) <= TOL[dtype]
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [0, 1])
 def test_centre_column_not_identity(s3dx, O, W, dtype):
