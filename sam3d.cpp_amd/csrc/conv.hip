@@ -284,8 +284,8 @@ const Tiling *choose_tiling(int64_t n_out, int nb, int ntiles, bool bf, int kc, 
         if (!usable(t)) continue;
         int rank;
         if (t.splitk) rank = t.id >= 15 ? 0 : 1;  // 128-channel tasks (chunks joined) first
-        else if (t.wn == 1 && t.nbw == 4) rank = blocks(t) >= 192 ? 1 : 10;  // 32x128 wave tiles
-        else if (t.mbw == 2) rank = blocks(t) >= 256 ? 2 : 20;
+        else if (t.wn == 1 && t.nbw == 4) rank = blocks(t) >= 192 ? 2 : 10;  // 32x128 wave tiles
+        else if (t.mbw == 2) rank = blocks(t) >= 256 ? 3 : 20;
         else rank = 5;
         if (rank < best_rank) {
             best_rank = rank;
