@@ -224,6 +224,7 @@ void add_rows_launch(const void *a, const void *b, int32_t dtype, int64_t n, int
 // ---------------------------------------------------------------------------
 struct s3dx_conv {
     int32_t cin = 0, cout = 0, kvol = 0, dtype = 0;
+    int32_t cout_pad = 0;  // packed MFMA weight columns (whole 32-column blocks)
     bool mfma = false;
     int nb = 0, kc = 0;  // MFMA tiling
     void *w = nullptr;   // packed weights (device)
@@ -343,14 +344,14 @@ LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bo
         // Buffer-resource gathers address at most 2 GiB; larger inputs take
         // the XF=1 (64-bit addressed) variant.
         p.xf = x_bytes >= (int64_t(1) << 31);
-        const int64_t w_bytes = static_cast<int64_t>(conv->kvol) * conv->cin * conv->cout * (bf ? 2 : 4);
+        const int64_t w_bytes = static_cast<int64_t>(conv->kvol) * conv->cin * conv->cout_pad * (bf ? 2 : 4);
         const bool splitk_ok = w_bytes < (int64_t(1) << 31);
         // The whole row per workgroup (conv->nb) unless a narrower column
         // tile has a split-K kernel and no LayerNorm needs the full row:
         // then each column tile re-gathers A (from L2), but every weight
         // fragment is loaded once, straight into the wave that uses it.
         // S3DX_CONV_NB=<blocks> overrides (tuning).
-        const int blocks = conv->cout / 32;
+        const int blocks = conv->cout_pad / 32;
         int forced = 0;
         if (const char *e = std::getenv("S3DX_CONV_NB")) forced = std::atoi(e);
         auto try_nb = [&](int nb) {
@@ -452,19 +453,20 @@ S3DX_API s3dx_status s3dx_conv_create(int32_t cin, int32_t cout, int32_t kvol, i
         c->dtype = dtype;
         const bool bf = dtype == S3DX_BF16;
         // Column blocks per workgroup: the whole row when Cout <= 256 (so a
-        // LayerNorm epilogue sees it), else 128-column tiles.
+        // LayerNorm epilogue sees it), else 128-column tiles.  A Cout that
+        // is not a multiple of 32 is padded to whole blocks with zero
+        // weights; the epilogue stores only the real columns.
         int nb = 0;
-        if (cout % 32 == 0) {
-            const int blocks = cout / 32;
-            if (blocks <= 8) {
-                for (int cand : {8, 6, 4, 3, 2, 1})
-                    if (cand == blocks) nb = cand;
-                if (nb == 0) nb = 1;  // 5 or 7 blocks: 32-column tiles
-            } else {
-                for (int cand : {4, 2, 1})
-                    if (nb == 0 && blocks % cand == 0) nb = cand;
-            }
+        const int blocks = (cout + 31) / 32;
+        if (blocks <= 8) {
+            for (int cand : {8, 6, 4, 3, 2, 1})
+                if (cand == blocks) nb = cand;
+            if (nb == 0) nb = 1;  // 5 or 7 blocks: 32-column tiles
+        } else {
+            for (int cand : {4, 2, 1})
+                if (nb == 0 && blocks % cand == 0) nb = cand;
         }
+        c->cout_pad = blocks * 32;
         const int kc = nb != 0 ? task_channels(cin, nb, bf) : 0;
         c->mfma = kc != 0 && nb != 0;
         c->kc = kc;
@@ -487,7 +489,7 @@ S3DX_API s3dx_status s3dx_conv_set_weights(s3dx_conv *conv, const float *host_we
         if (conv->mfma) {
             // [o][k-step][col block][lane][16 bytes], the B-operand lane order.
             const int E = bf ? 8 : 4, CPK = 2 * E;
-            const int ksteps = cin / CPK, nbtot = cout / 32;
+            const int ksteps = cin / CPK, nbtot = conv->cout_pad / 32;
             const size_t frags = static_cast<size_t>(kvol) * ksteps * nbtot * 64;
             packed.resize(frags * 16);
             size_t f = 0;
@@ -499,7 +501,8 @@ S3DX_API s3dx_status s3dx_conv_set_weights(s3dx_conv *conv, const float *host_we
                             uint8_t *dst = packed.data() + f * 16;
                             for (int e = 0; e < E; ++e) {
                                 const int ci = s * CPK + (l >> 5) * E + e;
-                                const float v = weight_at(host_weight, layout, kvol, cin, cout, o, co, ci);
+                                const float v = co < cout ? weight_at(host_weight, layout, kvol, cin, cout, o, co, ci)
+                                                          : 0.0f;
                                 if (bf) {
                                     const uint16_t h = f32_to_bf16(v);
                                     std::memcpy(dst + e * 2, &h, 2);
@@ -667,6 +670,7 @@ S3DX_API s3dx_status s3dx_conv_run(const s3dx_conv *conv, const void *x, int64_t
         a.w = conv->w;
         a.bias = conv->bias;
         a.cout = conv->cout;
+        a.cout_pad = conv->cout_pad;
         a.residual = residual;
         a.residual_shift = conv->residual_parent ? 3 : 0;
         a.y = y;

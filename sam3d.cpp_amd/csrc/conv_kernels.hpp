@@ -19,7 +19,8 @@ struct ConvArgs {
     int32_t kvol;
     const void *w;
     const float *bias;
-    int32_t cout;
+    int32_t cout;      // output columns (row stride of y and residual)
+    int32_t cout_pad;  // packed weight columns: cout rounded up to 32
     const void *residual;
     int32_t residual_shift;  // output row i adds residual row i >> residual_shift
     void *y;
@@ -192,8 +193,26 @@ __device__ __forceinline__ void load_residual(const ConvArgs &a, int64_t m0, int
     for (int p = 0; p < RM::PASSES; ++p) {
         res[p][0] = res[p][1] = make_uint4(0, 0, 0, 0);
         const int rl = p * RM::RPP + rsub;
-        if (!a.residual || rsub >= RM::RPP || rl >= tile_rows) continue;
+        if (!a.residual || rsub >= RM::RPP || rl >= tile_rows || col0 >= a.cout) continue;
         const int64_t off = ((m0 + rl) >> a.residual_shift) * a.cout + col0;
+        if (a.cout % 8 != 0) {  // rows not 16-byte aligned: element loads of the real columns
+            uint32_t w[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                w[k] = 0u;
+                if (col0 + k < a.cout)
+                    w[k] = a.y_bf16 ? static_cast<const uint16_t *>(a.residual)[off + k]
+                                    : static_cast<const uint32_t *>(a.residual)[off + k];
+            }
+            if (a.y_bf16) {
+                res[p][0] = make_uint4(w[0] | (w[1] << 16), w[2] | (w[3] << 16), w[4] | (w[5] << 16),
+                                       w[6] | (w[7] << 16));
+            } else {
+                res[p][0] = make_uint4(w[0], w[1], w[2], w[3]);
+                res[p][1] = make_uint4(w[4], w[5], w[6], w[7]);
+            }
+            continue;
+        }
         if (a.y_bf16) {
             res[p][0] = *reinterpret_cast<const uint4 *>(static_cast<const uint16_t *>(a.residual) + off);
         } else {
@@ -220,9 +239,13 @@ __device__ __forceinline__ void finish_rows(const ConvArgs &a, const float *stg,
     const bool active = rsub < RPP;
     const int col0 = nb0 * 32 + cg * 8;  // global column of this thread's 8 values
     const float inv_c = 1.0f / static_cast<float>(a.cout);
+    // Padded columns (col >= cout, zero weights) read no parameters and are
+    // not stored.  Rows of a cout that is not a multiple of 8 are not
+    // 16-byte aligned: element stores.
+    const bool ragged = a.cout % 8 != 0;
     float bias8[8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) bias8[k] = a.bias ? a.bias[col0 + k] : 0.0f;
+    for (int k = 0; k < 8; ++k) bias8[k] = a.bias && col0 + k < a.cout ? a.bias[col0 + k] : 0.0f;
 
     auto tile_vals = [&](int rl, float (&v)[8]) __attribute__((always_inline)) {
         const float4 *p = reinterpret_cast<const float4 *>(stg + rl * STG_LD + cg * 8);
@@ -279,10 +302,11 @@ __device__ __forceinline__ void finish_rows(const ConvArgs &a, const float *stg,
     float lw[8], lb[8], ms[8], mh[8];
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
-        lw[k] = a.ln_w ? a.ln_w[col0 + k] : 1.0f;
-        lb[k] = a.ln_b ? a.ln_b[col0 + k] : 0.0f;
-        ms[k] = a.mod_scale ? a.mod_scale[col0 + k] : 0.0f;
-        mh[k] = a.mod_shift ? a.mod_shift[col0 + k] : 0.0f;
+        const bool real = col0 + k < a.cout;
+        lw[k] = a.ln_w && real ? a.ln_w[col0 + k] : 1.0f;
+        lb[k] = a.ln_b && real ? a.ln_b[col0 + k] : 0.0f;
+        ms[k] = a.mod_scale && real ? a.mod_scale[col0 + k] : 0.0f;
+        mh[k] = a.mod_shift && real ? a.mod_shift[col0 + k] : 0.0f;
     }
     // Power-of-two groups: LayerNorm statistics of every pass first, all
     // passes in lockstep so the cross-lane sums overlap (two-pass mean /
@@ -352,8 +376,25 @@ __device__ __forceinline__ void finish_rows(const ConvArgs &a, const float *stg,
 #pragma unroll
             for (int k = 0; k < 8; ++k) v[k] = silu(v[k]);
         }
-        if (rl >= tile_rows) continue;
+        if (rl >= tile_rows || col0 >= a.cout) continue;
         const int64_t off = (m0 + rl) * a.cout + col0;
+        if (ragged) {
+            if (a.residual) {
+                const uint32_t rw[8] = {res[p][0].x, res[p][0].y, res[p][0].z, res[p][0].w,
+                                        res[p][1].x, res[p][1].y, res[p][1].z, res[p][1].w};
+#pragma unroll
+                for (int k = 0; k < 8; ++k)
+                    v[k] += a.y_bf16 ? bf16_to_f32(static_cast<uint16_t>(k & 1 ? rw[k >> 1] >> 16 : rw[k >> 1] & 0xffffu))
+                                     : __builtin_bit_cast(float, rw[k]);
+            }
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                if (col0 + k >= a.cout) continue;
+                if (a.y_bf16) static_cast<uint16_t *>(a.y)[off + k] = f32_to_bf16(v[k]);
+                else static_cast<float *>(a.y)[off + k] = v[k];
+            }
+            continue;
+        }
         if (a.y_bf16) {
             if (a.residual) {
                 const uint32_t rw[4] = {res[p][0].x, res[p][0].y, res[p][0].z, res[p][0].w};
@@ -446,7 +487,7 @@ conv_mfma_kernel(ConvArgs a) {
     const int tile = xcd_tile(blockIdx.x, gridDim.x);
     const int64_t m0 = static_cast<int64_t>(tile) * BM;
     const int nb0 = blockIdx.y * NBB;  // first 32-column block of this workgroup
-    const int nbtot = a.cout / 32;
+    const int nbtot = a.cout_pad / 32;
     const int kvol = a.kvol;
     const int ksteps_total = a.cin / CPK;
     const int chunks = a.cin / KC;
@@ -700,7 +741,7 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
     const int tile = xcd_tile(blockIdx.x, gridDim.x);
     const int64_t m0 = static_cast<int64_t>(tile) * BM;
     const int nb0 = blockIdx.y * NB;
-    const int nbtot = a.cout / 32;
+    const int nbtot = a.cout_pad / 32;
     const int kvol = a.kvol;
     const int ksteps_total = a.cin / CPK;
     const int chunks = a.cin / KCS;  // sub-task chunks per offset
@@ -709,7 +750,7 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
     constexpr int ES = static_cast<int>(sizeof(T));
     // Packed weights through a buffer resource (the host keeps them < 2 GiB):
     // per task a scalar byte offset, per column block an immediate.
-    const int64_t w_bytes = static_cast<int64_t>(kvol) * a.cin * a.cout * ES;
+    const int64_t w_bytes = static_cast<int64_t>(kvol) * a.cin * a.cout_pad * ES;
     const auto w_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(a.w), static_cast<short>(0),
                                                           static_cast<int32_t>(w_bytes), 0x00020000);
     const auto x_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(a.x), static_cast<short>(0),

@@ -6,11 +6,13 @@
 //   SlatTables downsample src/objects_runtime/sparse_ops.cpp:53-104
 //   MeshSubdivideTables   src/objects_runtime/sparse_ops.cpp:272-404
 //
-// The hash is open addressing with linear probing at load <= 1/4.  A 32-byte
-// slot holds the full (b, x, y, z) int32 key and its row (0xFFFFFFFF =
-// empty), so one probe is one cache line and verifies a hit by itself.  A
-// wave waits for its longest probe chain, which is what the low load keeps
-// short.  A slot is claimed with a 32-bit CAS on the row; a second row with
+// The hash is open addressing with linear probing at load <= 1/8.  A slot is
+// one 32-bit row (0xFFFFFFFF = empty); the key of a slot is the row's
+// (b, x, y, z) in the input, so a probe reads the slot, then the key it
+// names.  The table (4 bytes a slot, 1 MB at 30k voxels) stays resident in
+// L2 and clears with one coalesced fill.  A wave waits for its longest probe
+// chain, which is what the low load keeps short.  A slot is claimed with a
+// 32-bit CAS on the row; a second row with
 // the same coordinates lowers it with atomicMin, so after the insert kernel
 // every key maps to its smallest row -- exactly std::map::emplace's "first
 // occurrence wins".  Any int32 coordinates are handled exactly.
@@ -26,7 +28,7 @@ constexpr int kThreads = 256;
 
 // Workspace flag words.
 constexpr int kFlagDuplicate = 0;  // some coordinate occurs twice
-constexpr int kFlagOverflow = 1;   // probe sequence exhausted (never at load <= 1/4)
+constexpr int kFlagOverflow = 1;   // probe sequence exhausted (never at load <= 1/8)
 
 // 32-bit hash of (b, x, y, z): a multiply-add chain over the four words and
 // a murmur3-style finalizer (five 32-bit multiplies).
@@ -46,15 +48,13 @@ __device__ __forceinline__ bool same_key(int4 a, int4 b) {
     return a.x == b.x && a.y == b.y && a.z == b.z && a.w == b.w;
 }
 
-struct __align__(32) Slot {
-    int4 key;
-    uint32_t row;
-    uint32_t pad[3];
-};
-
-// Device view of the table: cap = mask + 1 slots.
+// Device view of the table: cap = mask + 1 slots of one row index each
+// (kEmpty when free).  A slot's key is keys[row], read from the array the
+// table was built from, so the table stays small (4 bytes a slot, load
+// <= 1/8) and one coalesced fill clears it.
 struct Hash {
-    Slot *slots;
+    uint32_t *slots;
+    const int4 *keys;
     int32_t *flags;
     uint32_t mask;
 };
@@ -63,10 +63,9 @@ struct Hash {
 __device__ __forceinline__ int32_t hash_find(const Hash &h, int4 c) {
     uint32_t pos = key_hash(c) & h.mask;
     for (uint32_t probe = 0; probe <= h.mask; ++probe) {
-        const int4 k = h.slots[pos].key;
-        const uint32_t row = h.slots[pos].row;
+        const uint32_t row = h.slots[pos];
         if (row == kEmpty) return -1;
-        if (same_key(k, c)) return static_cast<int32_t>(row);
+        if (same_key(h.keys[row], c)) return static_cast<int32_t>(row);
         pos = (pos + 1) & h.mask;
     }
     return -1;
@@ -75,7 +74,7 @@ __device__ __forceinline__ int32_t hash_find(const Hash &h, int4 c) {
 // Empties the slots and zeroes the flag words (one launch for both).
 __global__ void __launch_bounds__(kThreads) hash_clear_kernel(Hash h) {
     const uint32_t i = blockIdx.x * kThreads + threadIdx.x;
-    if (i <= h.mask) h.slots[i].row = kEmpty;
+    if (i <= h.mask) h.slots[i] = kEmpty;
     if (i < 64) h.flags[i] = 0;
 }
 
@@ -86,16 +85,12 @@ hash_insert_kernel(const int4 *__restrict__ keys, int32_t n, Hash h) {
     const int4 c = keys[i];
     uint32_t pos = key_hash(c) & h.mask;
     for (uint32_t probe = 0; probe <= h.mask; ++probe) {
-        const uint32_t prev = atomicCAS(&h.slots[pos].row, kEmpty, static_cast<uint32_t>(i));
-        if (prev == kEmpty) {
-            h.slots[pos].key = c;
-            return;
-        }
-        // The slot's key is that of its first claimant, read from the input
-        // (its key entry may not be written yet).  Rows sharing a key only
-        // ever lower the row, so any row seen here carries the slot's key.
+        const uint32_t prev = atomicCAS(&h.slots[pos], kEmpty, static_cast<uint32_t>(i));
+        if (prev == kEmpty) return;
+        // Rows sharing a key only ever lower the slot's row, so any row seen
+        // here carries the slot's key.
         if (same_key(keys[prev], c)) {
-            atomicMin(&h.slots[pos].row, static_cast<uint32_t>(i));
+            atomicMin(&h.slots[pos], static_cast<uint32_t>(i));
             h.flags[kFlagDuplicate] = 1;
             return;
         }
@@ -341,7 +336,7 @@ unsigned blocks_for(int64_t items) { return static_cast<unsigned>((items + kThre
 
 uint64_t hash_capacity(int64_t n) {
     uint64_t cap = 256;
-    while (cap < static_cast<uint64_t>(n) * 4) cap <<= 1;
+    while (cap < static_cast<uint64_t>(n) * 8) cap <<= 1;
     return cap;
 }
 
@@ -356,17 +351,19 @@ template <class W>
 void kmap_layout(W &w, int64_t n, Hash *h) {
     const uint64_t cap = hash_capacity(n);
     if constexpr (std::is_same_v<W, Carver>) {
-        h->slots = w.template take<Slot>(cap);
+        h->slots = w.template take<uint32_t>(cap);
+        h->keys = nullptr;
         h->flags = w.template take<int32_t>(64);
         h->mask = static_cast<uint32_t>(cap - 1);
     } else {
-        w.template take<Slot>(cap);
+        w.template take<uint32_t>(cap);
         w.template take<int32_t>(64);
     }
 }
 
 // Clears the table and inserts n keys (first occurrence wins).
-void hash_build(const int4 *keys, int32_t n, const Hash &h, hipStream_t stream) {
+void hash_build(const int4 *keys, int32_t n, Hash &h, hipStream_t stream) {
+    h.keys = keys;
     const uint64_t cap = static_cast<uint64_t>(h.mask) + 1;
     hash_clear_kernel<<<blocks_for(static_cast<int64_t>(cap)), kThreads, 0, stream>>>(h);
     launch_check("hash_clear");
@@ -375,7 +372,7 @@ void hash_build(const int4 *keys, int32_t n, const Hash &h, hipStream_t stream) 
 }
 
 // Hash insert + lookup, leaving the flags in the workspace.
-void run_kmap(const int4 *coords, int32_t n, int32_t missing, int32_t *kmap, const Hash &h,
+void run_kmap(const int4 *coords, int32_t n, int32_t missing, int32_t *kmap, Hash h,
               hipStream_t stream) {
     hash_build(coords, n, h, stream);
     kmap_lookup_kernel<<<blocks_for(static_cast<int64_t>(n) * 27), kThreads, 0, stream>>>(

@@ -310,6 +310,35 @@ def test_subtask_tilings(s3dx, O, W, monkeypatch, cin, cout, tiling, kvol):
     assert rel_l2(got, ref) <= TOL[dtype]
 
 
+@pytest.mark.parametrize("cin,cout,kvol,dtype,with_res", [
+    (96, 101, 1, 0, False), (96, 101, 1, 1, True),  # the mesh output head's shape
+    (64, 101, 27, 1, True), (64, 100, 27, 0, True), (64, 40, 27, 0, False),
+    (64, 104, 27, 1, True), (32, 7, 27, 0, True),   # cout % 8 == 0 (16-byte rows), and a tiny cout
+])
+def test_padded_cout(s3dx, O, W, cin, cout, kvol, dtype, with_res):
+    # Cout not a multiple of 32: zero-padded weight blocks on the MFMA path,
+    # only the real columns stored (element stores when rows are not 16-byte
+    # aligned).
+    coords = W.shells_union(3)[:2600]
+    n = coords.shape[0]
+    kmap = O.kmap_subm3(coords, n) if kvol == 27 else None
+    x = W.normal_f32(17, 1, (n, cin))
+    w = W.conv_weight(17, 2, cin, cout, kvol=kvol)
+    b = W.normal_f32(17, 3, (cout,))
+    res = W.normal_f32(17, 4, (n, cout)) if with_res else None
+
+    def setup(conv):
+        plan = conv.plan(n, n)
+        print(f"padded cout cin={cin} cout={cout} kvol={kvol} dtype={dtype}: {plan}", flush=True)
+        assert plan.startswith("mfma"), plan
+
+    got = gpu_conv(s3dx, x, kmap, n, w, s3dx.WEIGHT_SLAT, b, dtype, cout, kvol=kvol, residual=res, setup=setup)
+    ref = O.conv(rnd(s3dx, x, dtype), kmap, n, rnd(s3dx, w, dtype), 0, cout, b, kvol=kvol)
+    if with_res:
+        ref = ref + rnd(s3dx, res, dtype)
+    assert rel_l2(got, ref) <= TOL[dtype]
+
+
 @pytest.mark.gpu
 @pytest.mark.parametrize("dtype", [0, 1])
 def test_centre_column_not_identity(s3dx, O, W, dtype):
