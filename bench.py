@@ -153,6 +153,34 @@ def extras(s3dx, W, stream, seed):
     y = s3dx.DeviceArray((nc, 1024), np.uint16)
     conv_entry("config3_bf16_conv_1024", conv, x, nc, k3, nc, y, bf, p3, 1024, 1024, PEAK_BF16_TFLOPS)
 
+    # occupancy -> coordinates (session.cpp:1437-1474) on a noisy 64^3 field
+    # with the reference fixture's density (~27% occupied, mostly surface):
+    # threshold, surface prune, downsample to 42,000 rows; buffers reused,
+    # three host synchronizations (the row counts) inside the timed region.
+    occ = s3dx.DeviceArray.from_host(W.occupancy_noise(seed), stream)
+    cells = 64 ** 3
+    b_occ = s3dx.DeviceArray((cells, 4), np.int32)
+    b_surf = s3dx.DeviceArray((cells, 4), np.int32)
+    b_down = s3dx.DeviceArray((42000, 4), np.int32)
+    ws = {}
+
+    def do_coords():
+        n1, _ = s3dx.occupancy_coords(occ, (64, 64, 64), stream, out=b_occ, workspace=ws.get("o"))
+        n2_, _ = s3dx.prune_surface(b_occ, n1, stream, out=b_surf, workspace=ws.get("p"))
+        n3, _ = (s3dx.downsample_coords(b_surf, n2_, 42000, 2, 42, stream, out=b_down, workspace=ws.get("d"))
+                 if n2_ > 42000 else (n2_, b_surf))
+        res["coords"] = (n1, n2_, n3)
+    do_coords()
+    n1, n2_, n3 = res["coords"]
+    ws["o"] = s3dx.DeviceArray(s3dx.occupancy_workspace_size((64, 64, 64)), np.uint8)
+    ws["p"] = s3dx.DeviceArray(s3dx.prune_surface_workspace_size(n1), np.uint8)
+    ws["d"] = s3dx.DeviceArray(s3dx.downsample_coords_workspace_size(n2_), np.uint8)
+    us = _wall_us(do_coords)
+    out["coords_from_occupancy_64"] = {"us_wall": us, "cells": cells, "occupied": n1, "surface": n2_,
+                                       "rows": n3, "mvox_s": cells / us,
+                                       "note": "threshold + prune + downsample, wall clock with their three "
+                                               "host synchronizations, buffers reused"}
+
     # subdivide (MeshSubdivideTables) and config 4: 192 -> 192 BF16 over the children,
     # gathering parent rows (repeat x8) plus a per-slot offset
     def do_subdivide():

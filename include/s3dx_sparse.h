@@ -143,6 +143,48 @@ S3DX_API s3dx_status s3dx_subdivide2(const int32_t *parent_coords, int64_t paren
                                      uint64_t error_capacity);
 
 /* ------------------------------------------------------------------------
+ * Occupancy -> coordinates (the step before the SLat stage,
+ * src/objects_runtime/session.cpp).  Each keeps the reference's row order and
+ * synchronizes `stream` once to read the row count.  Cells are told apart by
+ * the reference's coordinate_key (session.cpp:122-127), overlapping fields
+ * and all, so every int32 input gives the reference's rows.
+ * ---------------------------------------------------------------------- */
+
+S3DX_API s3dx_status s3dx_occupancy_workspace_size(int32_t nx, int32_t ny, int32_t nz, uint64_t *bytes,
+                                                   char *error, uint64_t error_capacity);
+/* Threshold of the decoder's occupancy: every cell with occupancy > 0, in
+ * x-major order (flat = (x*ny + y)*nz + z), as rows (0, x, y, z)
+ * (session.cpp:1437-1441).  occupancy: device float32 [nx][ny][nz];
+ * coords: device int32 [nx*ny*nz][4] capacity; *count: rows written. */
+S3DX_API s3dx_status s3dx_occupancy_coords(const float *occupancy, int32_t nx, int32_t ny, int32_t nz,
+                                           int32_t *coords, int64_t *count, void *workspace,
+                                           uint64_t workspace_bytes, s3dx_stream stream, char *error,
+                                           uint64_t error_capacity);
+
+S3DX_API s3dx_status s3dx_prune_surface_workspace_size(int64_t n, uint64_t *bytes, char *error,
+                                                       uint64_t error_capacity);
+/* prune_surface_coords (session.cpp:133-163): the rows with at least one
+ * empty cell in their 3x3x3 neighbourhood (same b), in input order.
+ * surface: int32 [n][4] capacity.  Requires 0 < n <= INT32_MAX / 27. */
+S3DX_API s3dx_status s3dx_prune_surface(const int32_t *coords, int64_t n, int32_t *surface,
+                                        int64_t *count, void *workspace, uint64_t workspace_bytes,
+                                        s3dx_stream stream, char *error, uint64_t error_capacity);
+
+S3DX_API s3dx_status s3dx_downsample_coords_workspace_size(int64_t n, uint64_t *bytes, char *error,
+                                                           uint64_t error_capacity);
+/* downsample_coords (session.cpp:168-233; the pipeline calls it with
+ * max_coords 42000, factor 2, seed 42): n <= max_coords returns the rows
+ * unchanged; otherwise each axis is mapped onto a centred range of 1/factor
+ * the bounding box (double precision, rounded half up, clamped), duplicates
+ * dropped keeping first occurrences, and more than max_coords survivors are
+ * sampled by std::shuffle under std::mt19937(seed), as the reference does.
+ * out: int32 [min(n, max_coords)][4] capacity. */
+S3DX_API s3dx_status s3dx_downsample_coords(const int32_t *coords, int64_t n, int64_t max_coords,
+                                            int32_t factor, uint32_t seed, int32_t *out, int64_t *count,
+                                            void *workspace, uint64_t workspace_bytes, s3dx_stream stream,
+                                            char *error, uint64_t error_capacity);
+
+/* ------------------------------------------------------------------------
  * Sparse convolution layer: the SLat `conv` lambda + gb_linear
  * (slat_flow_graph.cpp:105-155, graph_builder.cpp:44-54) and the mesh
  * `convolution` lambda (mesh_decoder_graph.cpp:81-103), as one

@@ -73,6 +73,12 @@ void orc_repeat_children(const float *x, int64_t p, int32_t c, float *y);
 int64_t orc_occupancy_coords(const float *occ, int32_t res, int32_t *out);
 /* session.cpp:133-163 prune_surface_coords(max_neighbor_axes_dist=1). */
 int64_t orc_prune_surface(const int32_t *coords, int64_t n, int32_t *out);
+/* session.cpp:168-233 downsample_coords (oracle_coords.cpp); out cap
+ * min(n, max_coords) rows; returns the row count. */
+int64_t orc_downsample_coords(const int32_t *coords, int64_t n, int64_t max_coords, int32_t factor,
+                              uint32_t seed, int32_t *out);
+/* k-th output (1-based) of std::mt19937(seed). */
+uint32_t orc_mt19937_draw(uint32_t seed, int64_t k);
 
 /* CPU baseline: the GGML CPU decomposition of the SLat conv
  * (slat_flow_graph.cpp:116-130): concat a zero row, get_rows im2col into

@@ -32,6 +32,8 @@ _SIGS = {
     "orc_repeat_children": (None, [_vp, _i64, _i32, _vp]),
     "orc_occupancy_coords": (_i64, [_vp, _i32, _vp]),
     "orc_prune_surface": (_i64, [_vp, _i64, _vp]),
+    "orc_downsample_coords": (_i64, [_vp, _i64, _i64, _i32, C.c_uint32, _vp]),
+    "orc_mt19937_draw": (C.c_uint32, [C.c_uint32, _i64]),
     "orc_conv_im2col_gemm_f32": (None, [_vp, _i64, _i32, _vp, _i64, _vp, _i32, _vp, _vp, _i32]),
     "orc_round_bf16": (None, [_vp, _i64, _vp]),
 }
@@ -183,6 +185,19 @@ def prune_surface(coords: np.ndarray) -> np.ndarray:
     out = np.empty_like(c)
     m = lib().orc_prune_surface(_p(c), c.shape[0], _p(out))
     return out[:m].copy()
+
+
+def downsample_coords(coords: np.ndarray, max_coords: int = 42000, factor: int = 2,
+                      seed: int = 42) -> np.ndarray:
+    c = _c(coords, np.int32)
+    n = c.shape[0]
+    out = np.empty((max(1, min(n, max_coords)), 4), np.int32)
+    m = lib().orc_downsample_coords(_p(c), n, max_coords, factor, seed, _p(out))
+    return out[:m].copy()
+
+
+def mt19937_draw(seed: int, k: int) -> int:
+    return int(lib().orc_mt19937_draw(seed, k))
 
 
 def conv_im2col_gemm_f32(x, kmap, n_in, w_slat, cout, bias, threads: int) -> np.ndarray:

@@ -60,6 +60,13 @@ SIGNATURES = {
     "s3dx_kmap_subm3": (_u32, [_vp, _i64, _i32, _vp, _vp, _u64, _vp], True),
     "s3dx_coarsen2_workspace_size": (_u32, [_i64, C.POINTER(_u64)], True),
     "s3dx_coarsen2": (_u32, [_vp, _i64, _vp, _vp, _vp, _vp, C.POINTER(_i64), _vp, _u64, _vp], True),
+    "s3dx_occupancy_workspace_size": (_u32, [_i32, _i32, _i32, C.POINTER(_u64)], True),
+    "s3dx_occupancy_coords": (_u32, [_vp, _i32, _i32, _i32, _vp, C.POINTER(_i64), _vp, _u64, _vp], True),
+    "s3dx_prune_surface_workspace_size": (_u32, [_i64, C.POINTER(_u64)], True),
+    "s3dx_prune_surface": (_u32, [_vp, _i64, _vp, C.POINTER(_i64), _vp, _u64, _vp], True),
+    "s3dx_downsample_coords_workspace_size": (_u32, [_i64, C.POINTER(_u64)], True),
+    "s3dx_downsample_coords": (_u32, [_vp, _i64, _i64, _i32, _u32, _vp, C.POINTER(_i64), _vp, _u64, _vp],
+                               True),
     "s3dx_subdivide2_workspace_size": (_u32, [_i64, C.POINTER(_u64)], True),
     "s3dx_subdivide2": (_u32, [_vp, _i64, _vp, _vp, _vp, _u64, _vp], True),
     "s3dx_conv_create": (_u32, [_i32, _i32, _i32, _i32, C.POINTER(_vp)], True),
@@ -277,6 +284,80 @@ def coarsen2(coords: DeviceArray, n: int, stream=None):
     call("s3dx_coarsen2", _dptr(coords), _i64(n), _dptr(cc), _dptr(f2c), _dptr(ch), _dptr(inv),
          C.byref(nc), _dptr(ws), _u64(ws.nbytes), _sptr(stream))
     return int(nc.value), cc, f2c, ch, inv
+
+
+def occupancy_workspace_size(shape) -> int:
+    b = _u64(0)
+    call("s3dx_occupancy_workspace_size", *(_i32(int(v)) for v in shape), C.byref(b))
+    return int(b.value)
+
+
+def prune_surface_workspace_size(n: int) -> int:
+    b = _u64(0)
+    call("s3dx_prune_surface_workspace_size", _i64(n), C.byref(b))
+    return int(b.value)
+
+
+def downsample_coords_workspace_size(n: int) -> int:
+    b = _u64(0)
+    call("s3dx_downsample_coords_workspace_size", _i64(n), C.byref(b))
+    return int(b.value)
+
+
+def occupancy_coords(occupancy: DeviceArray, shape, stream=None, out: DeviceArray = None,
+                     workspace: DeviceArray = None):
+    """Cells with occupancy > 0 in x-major order as (0, x, y, z) rows
+    (session.cpp:1437-1441).  Returns (count, coords [cells, 4]); the first
+    count rows are meaningful.  out / workspace may be passed in to reuse them."""
+    nx, ny, nz = (int(v) for v in shape)
+    b = _u64(0)
+    call("s3dx_occupancy_workspace_size", _i32(nx), _i32(ny), _i32(nz), C.byref(b))
+    ws = workspace if workspace is not None else DeviceArray(int(b.value), np.uint8)
+    out = out if out is not None else DeviceArray((nx * ny * nz, 4), np.int32)
+    cnt = _i64(0)
+    call("s3dx_occupancy_coords", _dptr(occupancy), _i32(nx), _i32(ny), _i32(nz), _dptr(out),
+         C.byref(cnt), _dptr(ws), _u64(ws.nbytes), _sptr(stream))
+    return int(cnt.value), out
+
+
+def prune_surface(coords: DeviceArray, n: int, stream=None, out: DeviceArray = None,
+                  workspace: DeviceArray = None):
+    """prune_surface_coords (session.cpp:133-163).  Returns (count, surface [n, 4])."""
+    b = _u64(0)
+    call("s3dx_prune_surface_workspace_size", _i64(n), C.byref(b))
+    ws = workspace if workspace is not None else DeviceArray(int(b.value), np.uint8)
+    out = out if out is not None else DeviceArray((n, 4), np.int32)
+    cnt = _i64(0)
+    call("s3dx_prune_surface", _dptr(coords), _i64(n), _dptr(out), C.byref(cnt), _dptr(ws),
+         _u64(ws.nbytes), _sptr(stream))
+    return int(cnt.value), out
+
+
+def downsample_coords(coords: DeviceArray, n: int, max_coords: int = 42000, factor: int = 2,
+                      seed: int = 42, stream=None, out: DeviceArray = None, workspace: DeviceArray = None):
+    """downsample_coords (session.cpp:168-233).  Returns (count, out [min(n, max_coords), 4])."""
+    b = _u64(0)
+    call("s3dx_downsample_coords_workspace_size", _i64(n), C.byref(b))
+    ws = workspace if workspace is not None else DeviceArray(int(b.value), np.uint8)
+    out = out if out is not None else DeviceArray((max(1, min(n, max_coords)), 4), np.int32)
+    cnt = _i64(0)
+    call("s3dx_downsample_coords", _dptr(coords), _i64(n), _i64(max_coords), _i32(factor), _u32(seed),
+         _dptr(out), C.byref(cnt), _dptr(ws), _u64(ws.nbytes), _sptr(stream))
+    return int(cnt.value), out
+
+
+def coords_from_occupancy(occupancy: DeviceArray, shape, max_coords: int = 42000, seed: int = 42,
+                          stream=None):
+    """The SLat stage's coordinate table from the decoder's occupancy, as
+    session.cpp:1437-1474 builds it: threshold, surface prune, then the
+    downsample when more than max_coords rows remain.  Returns (count, coords)."""
+    n, coords = occupancy_coords(occupancy, shape, stream)
+    if n == 0:
+        return 0, coords
+    n, coords = prune_surface(coords, n, stream)
+    if n > max_coords:
+        n, coords = downsample_coords(coords, n, max_coords, 2, seed, stream)
+    return n, coords
 
 
 class SlatTables:

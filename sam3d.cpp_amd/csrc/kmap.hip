@@ -6,104 +6,14 @@
 //   SlatTables downsample src/objects_runtime/sparse_ops.cpp:53-104
 //   MeshSubdivideTables   src/objects_runtime/sparse_ops.cpp:272-404
 //
-// The hash is open addressing with linear probing at load <= 1/8.  A slot is
-// one 32-bit row (0xFFFFFFFF = empty); the key of a slot is the row's
-// (b, x, y, z) in the input, so a probe reads the slot, then the key it
-// names.  The table (4 bytes a slot, 1 MB at 30k voxels) stays resident in
-// L2 and clears with one coalesced fill.  A wave waits for its longest probe
-// chain, which is what the low load keeps short.  A slot is claimed with a
-// 32-bit CAS on the row; a second row with
-// the same coordinates lowers it with atomicMin, so after the insert kernel
-// every key maps to its smallest row -- exactly std::map::emplace's "first
-// occurrence wins".  Any int32 coordinates are handled exactly.
-#include "common.hpp"
+// The coordinate hash (coord_hash.hpp) gives every key its smallest row, as
+// std::map::emplace's "first occurrence wins" does.
+#include "coord_hash.hpp"
 
 #include <vector>
 
 namespace s3dx {
 namespace {
-
-constexpr uint32_t kEmpty = 0xFFFFFFFFu;
-constexpr int kThreads = 256;
-
-// Workspace flag words.
-constexpr int kFlagDuplicate = 0;  // some coordinate occurs twice
-constexpr int kFlagOverflow = 1;   // probe sequence exhausted (never at load <= 1/8)
-
-// 32-bit hash of (b, x, y, z): a multiply-add chain over the four words and
-// a murmur3-style finalizer (five 32-bit multiplies).
-__device__ __forceinline__ uint32_t key_hash(int4 c) {
-    uint32_t h = static_cast<uint32_t>(c.x) * 0x9E3779B1u + static_cast<uint32_t>(c.y);
-    h = h * 0x85EBCA77u + static_cast<uint32_t>(c.z);
-    h = h * 0xC2B2AE3Du + static_cast<uint32_t>(c.w);
-    h ^= h >> 16;
-    h *= 0x7FEB352Du;
-    h ^= h >> 15;
-    h *= 0x846CA68Bu;
-    h ^= h >> 16;
-    return h;
-}
-
-__device__ __forceinline__ bool same_key(int4 a, int4 b) {
-    return a.x == b.x && a.y == b.y && a.z == b.z && a.w == b.w;
-}
-
-// Device view of the table: cap = mask + 1 slots of one row index each
-// (kEmpty when free).  A slot's key is keys[row], read from the array the
-// table was built from, so the table stays small (4 bytes a slot, load
-// <= 1/8) and one coalesced fill clears it.
-struct Hash {
-    uint32_t *slots;
-    const int4 *keys;
-    int32_t *flags;
-    uint32_t mask;
-};
-
-// Smallest inserted row whose key equals c, or -1 (after the insert kernel).
-__device__ __forceinline__ int32_t hash_find(const Hash &h, int4 c) {
-    uint32_t pos = key_hash(c) & h.mask;
-    for (uint32_t probe = 0; probe <= h.mask; ++probe) {
-        const uint32_t row = h.slots[pos];
-        if (row == kEmpty) return -1;
-        if (same_key(h.keys[row], c)) return static_cast<int32_t>(row);
-        pos = (pos + 1) & h.mask;
-    }
-    return -1;
-}
-
-// Empties the slots and zeroes the flag words (one launch for both).
-__global__ void __launch_bounds__(kThreads) hash_clear_kernel(Hash h) {
-    const uint32_t i = blockIdx.x * kThreads + threadIdx.x;
-    if (i <= h.mask) h.slots[i] = kEmpty;
-    if (i < 64) h.flags[i] = 0;
-}
-
-__global__ void __launch_bounds__(kThreads)
-hash_insert_kernel(const int4 *__restrict__ keys, int32_t n, Hash h) {
-    const int32_t i = blockIdx.x * kThreads + threadIdx.x;
-    if (i >= n) return;
-    const int4 c = keys[i];
-    uint32_t pos = key_hash(c) & h.mask;
-    for (uint32_t probe = 0; probe <= h.mask; ++probe) {
-        const uint32_t prev = atomicCAS(&h.slots[pos], kEmpty, static_cast<uint32_t>(i));
-        if (prev == kEmpty) return;
-        // Rows sharing a key only ever lower the slot's row, so any row seen
-        // here carries the slot's key.
-        if (same_key(keys[prev], c)) {
-            atomicMin(&h.slots[pos], static_cast<uint32_t>(i));
-            h.flags[kFlagDuplicate] = 1;
-            return;
-        }
-        pos = (pos + 1) & h.mask;
-    }
-    h.flags[kFlagOverflow] = 1;
-}
-
-__device__ __forceinline__ bool add_fits(int32_t v, int32_t d, int32_t *out) {
-    const int64_t s = static_cast<int64_t>(v) + d;
-    *out = static_cast<int32_t>(s);
-    return s >= INT32_MIN && s <= INT32_MAX;
-}
 
 // One thread per (voxel, offset): kmap[i*27+o] = first row at coords[i]+d(o).
 __global__ void __launch_bounds__(kThreads)
@@ -332,14 +242,6 @@ child_select_kernel(const int32_t *__restrict__ bucket, const int32_t *__restric
     inv_count[c] = 1.0f / static_cast<float>(k + 1);
 }
 
-unsigned blocks_for(int64_t items) { return static_cast<unsigned>((items + kThreads - 1) / kThreads); }
-
-uint64_t hash_capacity(int64_t n) {
-    uint64_t cap = 256;
-    while (cap < static_cast<uint64_t>(n) * 8) cap <<= 1;
-    return cap;
-}
-
 // Dense coarse grids up to this many cells use the scan path.
 uint64_t dense_cell_cap(int64_t n) {
     const uint64_t a = uint64_t(1) << 21;
@@ -349,26 +251,7 @@ uint64_t dense_cell_cap(int64_t n) {
 
 template <class W>
 void kmap_layout(W &w, int64_t n, Hash *h) {
-    const uint64_t cap = hash_capacity(n);
-    if constexpr (std::is_same_v<W, Carver>) {
-        h->slots = w.template take<uint32_t>(cap);
-        h->keys = nullptr;
-        h->flags = w.template take<int32_t>(64);
-        h->mask = static_cast<uint32_t>(cap - 1);
-    } else {
-        w.template take<uint32_t>(cap);
-        w.template take<int32_t>(64);
-    }
-}
-
-// Clears the table and inserts n keys (first occurrence wins).
-void hash_build(const int4 *keys, int32_t n, Hash &h, hipStream_t stream) {
-    h.keys = keys;
-    const uint64_t cap = static_cast<uint64_t>(h.mask) + 1;
-    hash_clear_kernel<<<blocks_for(static_cast<int64_t>(cap)), kThreads, 0, stream>>>(h);
-    launch_check("hash_clear");
-    hash_insert_kernel<<<blocks_for(n), kThreads, 0, stream>>>(keys, n, h);
-    launch_check("hash_insert");
+    hash_layout(w, n, h);
 }
 
 // Hash insert + lookup, leaving the flags in the workspace.

@@ -87,6 +87,15 @@ def shells_union(seed: int = 0, res: int = 64, count: int = 8, half_thickness: f
     return _coords_from_mask(mask)
 
 
+def occupancy_noise(seed: int = 0, res: int = 64, density: float = 0.265) -> np.ndarray:
+    """A float32 [res]^3 occupancy field (x-major) with about `density` of the
+    cells > 0, scattered like a noisy decoder output: N(0,1) shifted by the
+    normal quantile of 1 - density (0.628 for the default)."""
+    from statistics import NormalDist
+    shift = NormalDist().inv_cdf(1.0 - density)
+    return (normal_f32(seed, 7, (res, res, res)) - np.float32(shift)).astype(np.float32)
+
+
 def or_pool2(coords: np.ndarray) -> np.ndarray:
     """Unique (b, x//2, y//2, z//2), lexicographically sorted (non-negative coords)."""
     c = coords.copy()

@@ -57,6 +57,57 @@ def test_real_occupancy_counts(O, golden):
     assert (coords.shape[0], surface.shape[0]) == (69537, 67783)
 
 
+# ---- downsample_coords (session.cpp:168-233) ---------------------------------
+def test_mt19937_standard_value(O):
+    # [rand.predef]: the 10000th draw of a default-constructed std::mt19937
+    # (seed 5489) is 4123659995.  Pins the generator the sample is drawn with.
+    assert O.mt19937_draw(5489, 10000) == 4123659995
+
+
+def test_downsample_dense_cube_closed_form(O):
+    # 64^3 cube, factor 2: each axis maps 0..63 onto the centred 32-cell range
+    # 16..47 (offset (64-32)/2), monotonically and onto, so the first
+    # occurrences are exactly [16, 47]^3 in lexicographic order; 32768 <=
+    # 42000 rows, so no sample.
+    g = np.arange(64, dtype=np.int32)
+    x, y, z = np.meshgrid(g, g, g, indexing="ij")
+    cube = np.stack([np.zeros_like(x), x, y, z], -1).reshape(-1, 4)
+    out = O.downsample_coords(cube, 42000, 2, 42)
+    t = np.arange(16, 48, dtype=np.int32)
+    a, b, c = np.meshgrid(t, t, t, indexing="ij")
+    want = np.stack([np.zeros_like(a), a, b, c], -1).reshape(-1, 4)
+    assert np.array_equal(out, want)
+
+
+def test_downsample_negative_odd_box_by_hand(O):
+    # x in -5..10 (16 cells -> 8: target_min = -5 + 4 = -1, target_max = 6),
+    # y in 0..2 (3 -> 1.5 cells: target_min 0.75, target_max 1.25, ends
+    # truncating to 0 and 1; value = 0.75 + 0.5 * y/2 rounds half up to 1 for
+    # y = 0, 1, 2), z = 0 (1 -> 0.5: target_max -0.25 truncates toward zero
+    # to 0; a zero denominator maps to target_min 0.25, which rounds to 0).
+    # 16*3 = 48 rows > max 10: 8 cells (x' = -1..6, y' = 1, z' = 0) in
+    # first-occurrence order.
+    rows = [(0, x, y, 0) for x in range(-5, 11) for y in range(3)]
+    out = O.downsample_coords(np.array(rows, np.int32), 10, 2, 42)
+    want = np.array([(0, x, 1, 0) for x in range(-1, 7)], np.int32)
+    assert np.array_equal(out, want)
+
+
+def test_downsample_small_set_unchanged_and_sample_invariants(O, W):
+    rng = np.random.default_rng(5)
+    c = rng.integers(0, 40, size=(900, 4)).astype(np.int32)
+    c[:, 0] = rng.integers(0, 2, size=900)
+    c[100] = c[7]  # a duplicate: kept, since n <= max_coords returns the input
+    assert np.array_equal(O.downsample_coords(c, 900, 2, 42), c)
+    full = O.downsample_coords(c, 899, 2, 42)   # n > max: mapped and deduplicated
+    assert len({tuple(r) for r in full.tolist()}) == full.shape[0] < 899
+    s = O.downsample_coords(c, 50, 2, 42)       # sampled: 50 distinct rows of that set
+    assert s.shape == (50, 4)
+    pool = {tuple(r) for r in full.tolist()}  # every mapped cell (fewer than 899)
+    assert all(tuple(r) in pool for r in s.tolist()) and len({tuple(r) for r in s.tolist()}) == 50
+    assert not np.array_equal(s, O.downsample_coords(c, 50, 2, 7))  # the seed drives the sample
+
+
 @pytest.mark.skipif("not __import__('s3dx_oracle').ref_available()")
 def test_oracle_equals_compiled_reference_random(O):
     rng = np.random.default_rng(99)
