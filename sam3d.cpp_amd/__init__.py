@@ -19,6 +19,7 @@ from pathlib import Path
 
 import numpy as np
 
+from . import formats  # noqa: F401  (re-exported)
 from . import workloads  # noqa: F401  (re-exported)
 
 HERE = Path(__file__).resolve().parent
