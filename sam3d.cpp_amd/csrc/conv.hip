@@ -302,10 +302,27 @@ struct LaunchPlan {
     bool xf = false;        // 64-bit addressed gathers (source above 2 GiB)
     bool fused_ln = false;  // LayerNorm in the MFMA epilogue
     int nb = 0, kc = 0;     // 32-column blocks per workgroup, channels per task
+    bool linear = false;    // the 1x1-layer kernel (weights resident in LDS)
+    unsigned smem = 0;      // dynamic LDS bytes
     const Tiling *tl = nullptr;
     KernelFn fn = nullptr;
     dim3 grid;
 };
+
+// Workgroups of 256 threads of `fn` with `smem` dynamic LDS that the device
+// holds at once (at least one per CU).  Without a device (a host-only plan
+// query) it assumes 256 CUs holding two each.
+int64_t resident_blocks(KernelFn fn, unsigned smem) {
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(fn), 256, smem) !=
+            hipSuccess) {
+        (void)hipGetLastError();
+        return 512;
+    }
+    return static_cast<int64_t>(std::max(cus, 1)) * std::max(per_cu, 1);
+}
 
 // Channels per task for nb column blocks: the largest of 128 / 64 / 32 that
 // divides cin and keeps one weight stage (kc x nb*32) within 32 KiB (FP32:
@@ -340,6 +357,24 @@ LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bo
     LaunchPlan p;
     const bool bf = conv->dtype == S3DX_BF16;
     p.mfma = conv->mfma && aligned16;
+    if (p.mfma && conv->kvol == 1 && x_bytes < (int64_t(1) << 31)) {
+        // 1x1 layer: every weight fragment fits in LDS -> the linear kernel.
+        const int nbt = conv->cout_pad / 32;
+        const int frags = conv->cin / (bf ? 16 : 8) * nbt * 64;
+        KernelFn fn = bf ? pick_linear_bf16(nbt) : pick_linear_f32(nbt);
+        if (fn && frags <= kLinearMaxFrags && !std::getenv("S3DX_CONV_TILING")) {
+            p.linear = true;
+            p.fn = fn;
+            p.nb = nbt;
+            // weights, then 8 staged output rows of (nbt*32 + 4) floats per wave
+            p.smem = static_cast<unsigned>(frags) * 16 + 4 * 8 * (nbt * 32 + 4) * 4;
+            // One pass of resident workgroups: a second, partial pass would
+            // cost a whole workgroup's time for a fraction of the rows.
+            const int64_t wave_blocks = (n_out + 127) / 128;  // four 32-row blocks per workgroup pass
+            p.grid = dim3(static_cast<unsigned>(std::min<int64_t>(wave_blocks, resident_blocks(fn, p.smem))));
+            return p;
+        }
+    }
     if (p.mfma) {
         // Buffer-resource gathers address at most 2 GiB; larger inputs take
         // the XF=1 (64-bit addressed) variant.
@@ -604,7 +639,11 @@ S3DX_API s3dx_status s3dx_conv_plan(const s3dx_conv *conv, int64_t n_in, int64_t
         const int64_t x_bytes = src.rows * conv->cin * static_cast<int64_t>(dtype_size(conv->dtype));
         const LaunchPlan p = plan_launch(conv, x_bytes, n_out, true);
         char text[256];
-        if (p.mfma)
+        if (p.linear)
+            std::snprintf(text, sizeof(text), "linear cols=%d ksteps=%d ln=%s grid=%u", p.nb * 32,
+                          conv->cin / (conv->dtype == S3DX_BF16 ? 16 : 8),
+                          conv->ln ? "separate" : "none", p.grid.x);
+        else if (p.mfma)
             std::snprintf(text, sizeof(text), "mfma tiling=%d%s rows=%d cols=%d kc=%d xf=%d ln=%s grid=%ux%u",
                           p.tl->id, p.tl->splitk ? " split-k" : "", p.tl->rows(), p.tl->cols(), p.kc,
                           p.xf ? 1 : 0, conv->ln ? (p.fused_ln ? "fused" : "separate") : "none", p.grid.x,
@@ -690,8 +729,8 @@ S3DX_API s3dx_status s3dx_conv_run(const s3dx_conv *conv, const void *x, int64_t
                 a.silu = 0;
                 a.residual = nullptr;
             }
-            hipLaunchKernelGGL(plan.fn, plan.grid, dim3(256), 0, s, a);
-            launch_check("conv_mfma");
+            hipLaunchKernelGGL(plan.fn, plan.grid, dim3(256), plan.smem, s, a);
+            launch_check(plan.linear ? "conv_linear" : "conv_mfma");
         } else {
             a.ln = 0;
             if (conv->ln) {

@@ -13,4 +13,6 @@ KernelFn pick_mfma_bf16(int id, int kc, bool xf) {
     }
 }
 
+KernelFn pick_linear_bf16(int nbt) { return pick_linear<uint16_t>(nbt); }
+
 }  // namespace s3dx

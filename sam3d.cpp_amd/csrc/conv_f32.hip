@@ -12,4 +12,6 @@ KernelFn pick_mfma_f32(int id, int kc, bool xf) {
     }
 }
 
+KernelFn pick_linear_f32(int nbt) { return pick_linear<float>(nbt); }
+
 }  // namespace s3dx

@@ -58,6 +58,9 @@ inline constexpr Tiling kTilings[] = {
 // nullptr if that combination is not compiled.
 KernelFn pick_mfma_bf16(int id, int kc, bool xf);
 KernelFn pick_mfma_f32(int id, int kc, bool xf);
+// 1x1-layer kernel for nbt 32-column blocks (1, 2, 3, 4, 6, 8), else nullptr.
+KernelFn pick_linear_bf16(int nbt);
+KernelFn pick_linear_f32(int nbt);
 
 namespace {
 
@@ -1179,6 +1182,146 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
 //   0: 1,1,1,1  1: 1,1,2,1  2: 1,3,1,1  3: 1,2,2,1  4: 1,3,2,1  5: 1,4,2,1
 //   6: 2,1,2,1  7: 2,3,1,1  8: 2,2,2,1  9: 2,3,2,1  10: 1,4,1,2
 //   11-14: split-K, 128 rows x 128 / 64 / 96 / 32 columns
+// 1x1 layers (kvol 1, no map): y[r] = W x[r >> row_shift] + bias, then SiLU
+// and the residual.  Persistent workgroups: the packed weights (every k-step
+// of all NBT column blocks) are copied to LDS once; each wave then takes
+// 32-row blocks of the grid-stride sequence, streams its A fragments straight
+// from the rows two k-steps ahead (a row past the end reads zeros through
+// the buffer resource), and stores from the accumulators: no split-K
+// reduction and no staging, which dominate a 27-offset kernel run on one
+// offset.  Requires x_bytes < 2 GiB and at most kLinearMaxFrags packed
+// weight fragments.
+constexpr int kLinearMaxFrags = 4096;  // 64 KiB of LDS
+
+template <class T, int NBT>
+__global__ void __launch_bounds__(256) linear_kernel(ConvArgs a) {
+    extern __shared__ uint4 wl[];
+    constexpr int E = Frag<T>::E, CPK = 2 * E;
+    constexpr int ES = static_cast<int>(sizeof(T));
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5;
+    const int ks_total = a.cin / CPK;
+    const uint4 *wg = static_cast<const uint4 *>(a.w);
+    for (int f = tid; f < ks_total * NBT * 64; f += 256) wl[f] = wg[f];
+    __syncthreads();
+    // Output staging after the weights: 8 rows of SLD floats per wave.
+    constexpr int SLD = NBT * 32 + 4;
+    constexpr int EPC = sizeof(T) == 2 ? 8 : 4;  // output elements per 16-byte store (fp32 out: 4)
+    float *stg = reinterpret_cast<float *>(wl + ks_total * NBT * 64) + wave * 8 * SLD;
+    const auto x_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(a.x), static_cast<short>(0),
+                                                          static_cast<int32_t>(a.x_bytes), 0x00020000);
+    float bias[NBT];
+#pragma unroll
+    for (int cb = 0; cb < NBT; ++cb) {
+        const int col = cb * 32 + (lane & 31);
+        bias[cb] = a.bias && col < a.cout ? a.bias[col] : 0.0f;
+    }
+    const int64_t nblk = (a.n_out + 31) / 32;
+    for (int64_t blk = static_cast<int64_t>(blockIdx.x) * 4 + wave; blk < nblk;
+         blk += static_cast<int64_t>(gridDim.x) * 4) {
+        const int64_t r = blk * 32 + (lane & 31);
+        const uint32_t base = r < a.n_out
+                                  ? static_cast<uint32_t>(((r >> a.row_shift) * a.cin + half * E) * ES)
+                                  : 0x80000000u;
+        auto load_a = [&](int st) __attribute__((always_inline)) {
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
+                x_rsrc, static_cast<int32_t>(base + static_cast<uint32_t>(st * CPK * ES)), 0, 0);
+            return make_uint4(v.x, v.y, v.z, v.w);
+        };
+        f32x16 acc[NBT];
+#pragma unroll
+        for (int cb = 0; cb < NBT; ++cb) acc[cb] = f32x16{};
+        // Loads run two k-steps ahead without a branch (one around a load
+        // would make the compiler wait for every load at the join); the two
+        // past the row's end read the next row or zeros and go unused.
+        uint4 a0 = load_a(0);
+        uint4 a1 = load_a(1);
+        for (int st = 0; st < ks_total; ++st) {
+            const uint4 cur = a0;
+            a0 = a1;
+            a1 = load_a(st + 2);
+#pragma unroll
+            for (int cb = 0; cb < NBT; ++cb) acc[cb] = mfma_step<T>(cur, wl[(st * NBT + cb) * 64 + lane], acc[cb]);
+        }
+        // D layout: lane l holds column l % 32; register j holds row
+        // 8*(j/4) + 4*(l/32) + j%4 of the block.  Rows 8g..8g+7 (registers
+        // 4g..4g+3) go through this wave's LDS rows, then leave as one
+        // contiguous, 16-byte-aligned span of 8*cout elements (8*cout*size is
+        // a multiple of 16): full-width stores, not row pieces that straddle
+        // cache lines.
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int64_t row0 = blk * 32 + 8 * g;
+            if (row0 >= a.n_out) break;
+#pragma unroll
+            for (int cb = 0; cb < NBT; ++cb)
+#pragma unroll
+                for (int q = 0; q < 4; ++q)
+                    stg[(4 * half + q) * SLD + cb * 32 + (lane & 31)] = acc[cb][4 * g + q] + bias[cb];
+            const int elems = static_cast<int>(min(static_cast<int64_t>(8), a.n_out - row0)) * a.cout;
+            for (int c = lane; c * EPC < elems; c += 64) {
+                const int e0 = c * EPC;
+                int rr = e0 / a.cout, cc = e0 - rr * a.cout;
+                float v[EPC];
+#pragma unroll
+                for (int i = 0; i < EPC; ++i) {
+                    const bool in = e0 + i < elems;
+                    v[i] = in ? stg[rr * SLD + cc] : 0.0f;
+                    if (a.silu) v[i] = silu(v[i]);
+                    if (a.residual && in) {
+                        const int64_t roff = ((row0 + rr) >> a.residual_shift) * a.cout + cc;
+                        v[i] += a.y_bf16 ? bf16_to_f32(static_cast<const uint16_t *>(a.residual)[roff])
+                                         : static_cast<const float *>(a.residual)[roff];
+                    }
+                    if (++cc == a.cout) {
+                        cc = 0;
+                        ++rr;
+                    }
+                }
+                const int64_t off = row0 * a.cout + e0;
+                if (e0 + EPC <= elems) {
+                    if (a.y_bf16) {
+                        uint32_t w[EPC / 2];
+#pragma unroll
+                        for (int i = 0; i < EPC / 2; ++i)
+                            w[i] = static_cast<uint32_t>(f32_to_bf16(v[2 * i])) |
+                                   (static_cast<uint32_t>(f32_to_bf16(v[2 * i + 1])) << 16);
+                        if constexpr (EPC == 8)
+                            *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.y) + off) = make_uint4(w[0], w[1], w[2], w[3]);
+                        else
+                            *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(a.y) + off) = make_uint2(w[0], w[1]);
+                    } else {
+                        if constexpr (EPC == 4)
+                            *reinterpret_cast<float4 *>(static_cast<float *>(a.y) + off) = make_float4(v[0], v[1], v[2], v[3]);
+                        else
+#pragma unroll
+                            for (int i = 0; i < EPC; ++i) static_cast<float *>(a.y)[off + i] = v[i];
+                    }
+                } else {
+#pragma unroll
+                    for (int i = 0; i < EPC; ++i) {
+                        if (e0 + i >= elems) break;
+                        if (a.y_bf16) static_cast<uint16_t *>(a.y)[off + i] = f32_to_bf16(v[i]);
+                        else static_cast<float *>(a.y)[off + i] = v[i];
+                    }
+                }
+            }
+        }
+    }
+}
+
+template <class T>
+KernelFn pick_linear(int nbt) {
+    switch (nbt) {
+    case 1: return linear_kernel<T, 1>;
+    case 2: return linear_kernel<T, 2>;
+    case 3: return linear_kernel<T, 3>;
+    case 4: return linear_kernel<T, 4>;
+    case 6: return linear_kernel<T, 6>;
+    case 8: return linear_kernel<T, 8>;
+    default: return nullptr;
+    }
+}
+
 template <class T, int KC, int XF>
 KernelFn pick_tiling(int id) {
 #define S3DX_T(MBW, NBW, WN, S)                                                     \

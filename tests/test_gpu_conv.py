@@ -166,6 +166,39 @@ def test_residual_at_parent_resolution(s3dx, O, W, dtype, cout, ln):
     assert rel_l2(got, ref) <= TOL[dtype] * (3 if dtype == 0 else 1)
 
 
+@pytest.mark.parametrize("dtype", [0, 1])
+@pytest.mark.parametrize("cin,cout,n,parent,res_parent,silu", [
+    (96, 101, 300001, False, False, False),  # the head's shape; > 2 passes of the persistent grid
+    (160, 96, 4099, True, True, True),       # parent rows, per-parent residual, SiLU
+    (128, 128, 5, False, True, False),        # fewer rows than one 32-row block
+    (64, 256, 777, False, False, True),
+])
+def test_linear_kernel(s3dx, O, W, dtype, cin, cout, n, parent, res_parent, silu):
+    # 1x1 layers on the LDS-resident-weight kernel against a plain GEMM.
+    rows_in = (n + 7) // 8 if parent else n
+    x = W.normal_f32(18, 1, (rows_in, cin))
+    w = W.conv_weight(18, 2, cin, cout, kvol=1)
+    b = W.normal_f32(18, 3, (cout,))
+    res = W.normal_f32(18, 4, ((n + 7) // 8 if res_parent else n, cout))
+
+    def setup(conv):
+        conv.set_gather_parent(parent).set_residual_parent(res_parent).set_silu(silu)
+        plan = conv.plan(rows_in, n)
+        print(f"linear cin={cin} cout={cout} n={n} dtype={dtype}: {plan}", flush=True)
+        assert "linear" in plan, plan
+
+    got = gpu_conv(s3dx, x, None, rows_in, w, s3dx.WEIGHT_SLAT, b, dtype, cout, kvol=1, n_out=n,
+                   residual=res, setup=setup)
+    xs = rnd(s3dx, x, dtype)
+    xs = O.repeat_children(xs)[:n] if parent else xs
+    h = O.conv(xs, None, n, rnd(s3dx, w, dtype), 0, cout, b, kvol=1)
+    if silu:
+        h = O.silu(h)
+    rr = rnd(s3dx, res, dtype)
+    ref = h + (O.repeat_children(rr)[:n] if res_parent else rr)
+    assert rel_l2(got, ref) <= TOL[dtype] * (2 if dtype == 0 else 1)
+
+
 def test_transform_buffer_regrows(s3dx, O, W):
     # One layer object run on a small, a larger, then the small parent set:
     # the transformed-input buffer grows once and stays valid.
@@ -330,7 +363,7 @@ def test_padded_cout(s3dx, O, W, cin, cout, kvol, dtype, with_res):
     def setup(conv):
         plan = conv.plan(n, n)
         print(f"padded cout cin={cin} cout={cout} kvol={kvol} dtype={dtype}: {plan}", flush=True)
-        assert plan.startswith("mfma"), plan
+        assert plan.startswith(("mfma", "linear")), plan
 
     got = gpu_conv(s3dx, x, kmap, n, w, s3dx.WEIGHT_SLAT, b, dtype, cout, kvol=kvol, residual=res, setup=setup)
     ref = O.conv(rnd(s3dx, x, dtype), kmap, n, rnd(s3dx, w, dtype), 0, cout, b, kvol=kvol)
