@@ -309,6 +309,17 @@ struct LaunchPlan {
     dim3 grid;
 };
 
+// Compute units of the current device (256 without one: a host-only query).
+int64_t device_cus() {
+    int dev = 0, cus = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+        (void)hipGetLastError();
+        return 256;
+    }
+    return cus;
+}
+
 // Workgroups of 256 threads of `fn` with `smem` dynamic LDS that the device
 // holds at once (at least one per CU).  Without a device (a host-only plan
 // query) it assumes 256 CUs holding two each.
@@ -409,6 +420,23 @@ LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bo
                 for (int nb : {4, 3, 2})
                     if (!found && nb < conv->nb && blocks % nb == 0 && try_nb(nb)) found = p.tl->splitk;
                 if (!found) p = whole;
+            }
+            // Few row tiles (small voxel sets): split-K runs one workgroup
+            // per CU, so narrower column tiles that still fit in one pass
+            // over the CUs finish sooner (each re-gathers A from L2).
+            if (p.tl->splitk && !conv->ln) {
+                const int64_t rt = (n_out + 127) / 128;
+                const int64_t cus = device_cus();
+                if (rt * (blocks / p.nb) < cus) {
+                    const LaunchPlan wide = p;
+                    LaunchPlan best = p;
+                    for (int nb : {3, 2, 1}) {
+                        if (nb >= wide.nb || blocks % nb != 0 || rt * (blocks / nb) > cus) continue;
+                        if (try_nb(nb) && p.tl->splitk) best = p;
+                        p = wide;
+                    }
+                    p = best;
+                }
             }
         }
         p.fused_ln = conv->ln && p.nb * 32 == conv->cout;
