@@ -412,7 +412,11 @@ __device__ __forceinline__ void finish_rows(const ConvArgs &a, const float *stg,
             for (int k = 0; k < 4; ++k)
                 o4[k] = static_cast<uint32_t>(f32_to_bf16(v[2 * k])) |
                         (static_cast<uint32_t>(f32_to_bf16(v[2 * k + 1])) << 16);
-            *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.y) + off) = make_uint4(o4[0], o4[1], o4[2], o4[3]);
+            // Streaming stores: the rows are read by the next kernel, likely
+            // on another XCD, so they need not sit dirty in this XCD's L2
+            // (whose write-back at kernel end is on the critical path).
+            __builtin_nontemporal_store(u32x4{o4[0], o4[1], o4[2], o4[3]},
+                                        reinterpret_cast<u32x4 *>(static_cast<uint16_t *>(a.y) + off));
         } else {
             float4 *yp = reinterpret_cast<float4 *>(static_cast<float *>(a.y) + off);
             if (a.residual) {
@@ -422,8 +426,14 @@ __device__ __forceinline__ void finish_rows(const ConvArgs &a, const float *stg,
                 v[4] += __builtin_bit_cast(float, r1.x); v[5] += __builtin_bit_cast(float, r1.y);
                 v[6] += __builtin_bit_cast(float, r1.z); v[7] += __builtin_bit_cast(float, r1.w);
             }
-            yp[0] = make_float4(v[0], v[1], v[2], v[3]);
-            yp[1] = make_float4(v[4], v[5], v[6], v[7]);
+            __builtin_nontemporal_store(
+                u32x4{__builtin_bit_cast(uint32_t, v[0]), __builtin_bit_cast(uint32_t, v[1]),
+                      __builtin_bit_cast(uint32_t, v[2]), __builtin_bit_cast(uint32_t, v[3])},
+                reinterpret_cast<u32x4 *>(yp));
+            __builtin_nontemporal_store(
+                u32x4{__builtin_bit_cast(uint32_t, v[4]), __builtin_bit_cast(uint32_t, v[5]),
+                      __builtin_bit_cast(uint32_t, v[6]), __builtin_bit_cast(uint32_t, v[7])},
+                reinterpret_cast<u32x4 *>(yp) + 1);
         }
     }
 }
