@@ -74,30 +74,69 @@ __device__ __forceinline__ float xform_one(const XformArgs &a, float v, int64_t 
     return v;
 }
 
-// 16-byte pieces (cin a multiple of the piece's element count).
+// 16-byte pieces (cin a multiple of the piece's element count): each
+// thread takes pieces of a grid-stride sequence (32-bit indices: rows*cin
+// pieces < 2^32 is checked by the host), reading the piece's per-channel
+// scale / shift / slot offsets as float4 vectors.
 template <class T>
 __global__ void __launch_bounds__(256) xform_rows_kernel(XformArgs a) {
     constexpr int E = 16 / sizeof(T);
-    const int32_t ppr = a.cin / E;
-    const int64_t total = a.rows * ppr;
-    for (int64_t u = blockIdx.x * 256ll + threadIdx.x; u < total; u += gridDim.x * 256ll) {
-        const int64_t r = u / ppr;
+    const uint32_t ppr = static_cast<uint32_t>(a.cin) / E;
+    const uint32_t total = static_cast<uint32_t>(a.rows) * ppr;
+    for (uint32_t u = blockIdx.x * 256u + threadIdx.x; u < total; u += gridDim.x * 256u) {
+        const uint32_t r = u / ppr;
         const int32_t c0 = static_cast<int32_t>(u - r * ppr) * E;
         const int64_t src = a.children ? (r >> 3) : r;
         const uint4 raw = *reinterpret_cast<const uint4 *>(static_cast<const T *>(a.x) + src * a.cin + c0);
-        const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
-        uint32_t o4[4];
+        float v[E];
+        if constexpr (E == 8) {
+            const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            if constexpr (E == 8) {
-                const float lo = xform_one<T>(a, bf16_to_f32(static_cast<uint16_t>(w4[k] & 0xffffu)), r, c0 + 2 * k);
-                const float hi = xform_one<T>(a, bf16_to_f32(static_cast<uint16_t>(w4[k] >> 16)), r, c0 + 2 * k + 1);
-                o4[k] = static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
-            } else {
-                o4[k] = __builtin_bit_cast(uint32_t, xform_one<T>(a, __builtin_bit_cast(float, w4[k]), r, c0 + k));
+            for (int k = 0; k < 4; ++k) {
+                v[2 * k] = bf16_to_f32(static_cast<uint16_t>(w4[k] & 0xffffu));
+                v[2 * k + 1] = bf16_to_f32(static_cast<uint16_t>(w4[k] >> 16));
             }
+        } else {
+            v[0] = __builtin_bit_cast(float, raw.x);
+            v[1] = __builtin_bit_cast(float, raw.y);
+            v[2] = __builtin_bit_cast(float, raw.z);
+            v[3] = __builtin_bit_cast(float, raw.w);
         }
-        *reinterpret_cast<uint4 *>(static_cast<T *>(a.out) + r * a.cin + c0) = make_uint4(o4[0], o4[1], o4[2], o4[3]);
+        auto load = [&](const float *p, float (&out)[E]) __attribute__((always_inline)) {
+#pragma unroll
+            for (int k = 0; k < E; k += 4) {
+                const float4 q = *reinterpret_cast<const float4 *>(p + k);
+                out[k] = q.x;
+                out[k + 1] = q.y;
+                out[k + 2] = q.z;
+                out[k + 3] = q.w;
+            }
+        };
+        if (a.children) {
+            float so[E];
+            load(a.slot_offset + (r & 7) * a.cin + c0, so);
+#pragma unroll
+            for (int k = 0; k < E; ++k) v[k] += so[k];
+        }
+        if (a.scale) {
+            float sc[E], sh[E];
+            load(a.scale + c0, sc);
+            load(a.shift + c0, sh);
+#pragma unroll
+            for (int k = 0; k < E; ++k) v[k] = silu(v[k] * sc[k] + sh[k]);
+        }
+        uint4 o;
+        if constexpr (E == 8) {
+            uint32_t w4[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                w4[k] = static_cast<uint32_t>(f32_to_bf16(v[2 * k])) | (static_cast<uint32_t>(f32_to_bf16(v[2 * k + 1])) << 16);
+            o = make_uint4(w4[0], w4[1], w4[2], w4[3]);
+        } else {
+            o = make_uint4(__builtin_bit_cast(uint32_t, v[0]), __builtin_bit_cast(uint32_t, v[1]),
+                           __builtin_bit_cast(uint32_t, v[2]), __builtin_bit_cast(uint32_t, v[3]));
+        }
+        *reinterpret_cast<uint4 *>(static_cast<T *>(a.out) + static_cast<int64_t>(r) * a.cin + c0) = o;
     }
 }
 
@@ -712,7 +751,10 @@ S3DX_API s3dx_status s3dx_conv_run(const s3dx_conv *conv, const void *x, int64_t
             xa.slot_offset = conv->slot_offset;
             xa.scale = conv->pre_scale;
             xa.shift = conv->pre_shift;
-            const bool vec = conv->cin % (bf ? 8 : 4) == 0;
+            // 16-byte pieces with 32-bit piece indices; else one element per thread.
+            const bool vec = conv->cin % (bf ? 8 : 4) == 0 &&
+                             src.rows * (conv->cin / (bf ? 8 : 4)) < (int64_t(1) << 32) &&
+                             aligned(conv->pre_scale, 16) && aligned(conv->pre_shift, 16);
             const int64_t items = src.rows * (vec ? conv->cin / (bf ? 8 : 4) : conv->cin);
             const dim3 grid(static_cast<unsigned>(std::min<int64_t>((items + 255) / 256, 16384)));
             if (vec) {

@@ -103,6 +103,38 @@ __device__ __forceinline__ bool add_fits(int32_t v, int32_t d, int32_t *out) {
 
 unsigned blocks_for(int64_t items) { return static_cast<unsigned>((items + kThreads - 1) / kThreads); }
 
+// Grid of a bounds reduction: at most 128 blocks, each thread striding over
+// the items, so the per-block atomics stay few.
+unsigned bounds_blocks(int64_t items) { return blocks_for(items) < 128u ? blocks_for(items) : 128u; }
+
+// Block-wide min of v[0..M) and max of v[M..2M), committed with one atomic
+// per value per block: a wave butterfly, then the block's waves through LDS.
+// Every thread of the block must call it.
+template <int M>
+__device__ __forceinline__ void block_bounds_atomic(int (&v)[2 * M], int32_t *out) {
+    __shared__ int part[kThreads / 64][2 * M];
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) {
+#pragma unroll
+        for (int a = 0; a < M; ++a) v[a] = min(v[a], __shfl_xor(v[a], d, 64));
+#pragma unroll
+        for (int a = M; a < 2 * M; ++a) v[a] = max(v[a], __shfl_xor(v[a], d, 64));
+    }
+    if ((threadIdx.x & 63) == 0)
+#pragma unroll
+        for (int a = 0; a < 2 * M; ++a) part[threadIdx.x >> 6][a] = v[a];
+    __syncthreads();
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int a = 0; a < 2 * M; ++a) {
+            int r = part[0][a];
+            for (int w = 1; w < kThreads / 64; ++w) r = a < M ? min(r, part[w][a]) : max(r, part[w][a]);
+            if (a < M) atomicMin(&out[a], r);
+            else atomicMax(&out[a], r);
+        }
+    }
+}
+
 uint64_t hash_capacity(int64_t n) {
     uint64_t cap = 256;
     while (cap < static_cast<uint64_t>(n) * 8) cap <<= 1;

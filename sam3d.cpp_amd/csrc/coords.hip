@@ -89,27 +89,13 @@ compact_rows_kernel(const int4 *__restrict__ in, int32_t n, const int32_t *__res
 // Bounding box of (x, y, z): bbox[0..2] min, bbox[3..5] max.
 __global__ void __launch_bounds__(kThreads)
 xyz_bbox_kernel(const int4 *__restrict__ coords, int32_t n, int32_t *bbox) {
-    const int32_t i = blockIdx.x * kThreads + threadIdx.x;
     int v[6] = {INT32_MAX, INT32_MAX, INT32_MAX, INT32_MIN, INT32_MIN, INT32_MIN};
-    if (i < n) {
+    for (int32_t i = blockIdx.x * kThreads + threadIdx.x; i < n; i += gridDim.x * kThreads) {
         const int4 c = coords[i];
-        v[0] = v[3] = c.y;
-        v[1] = v[4] = c.z;
-        v[2] = v[5] = c.w;
+        v[0] = min(v[0], c.y); v[1] = min(v[1], c.z); v[2] = min(v[2], c.w);
+        v[3] = max(v[3], c.y); v[4] = max(v[4], c.z); v[5] = max(v[5], c.w);
     }
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) {
-#pragma unroll
-        for (int a = 0; a < 3; ++a) v[a] = min(v[a], __shfl_xor(v[a], d, 64));
-#pragma unroll
-        for (int a = 3; a < 6; ++a) v[a] = max(v[a], __shfl_xor(v[a], d, 64));
-    }
-    if ((threadIdx.x & 63) == 0) {
-#pragma unroll
-        for (int a = 0; a < 3; ++a) atomicMin(&bbox[a], v[a]);
-#pragma unroll
-        for (int a = 3; a < 6; ++a) atomicMax(&bbox[a], v[a]);
-    }
+    block_bounds_atomic<3>(v, bbox);
 }
 
 // One axis of downsample_coords (session.cpp:180-211): the coordinate's
@@ -371,7 +357,7 @@ S3DX_API s3dx_status s3dx_downsample_coords(const int32_t *coords, int64_t n, in
         const int4 *c4 = reinterpret_cast<const int4 *>(coords);
         fill_u32(reinterpret_cast<uint32_t *>(l.bbox), 3, static_cast<uint32_t>(INT32_MAX), s);
         fill_u32(reinterpret_cast<uint32_t *>(l.bbox) + 3, 3, static_cast<uint32_t>(INT32_MIN), s);
-        xyz_bbox_kernel<<<blocks_for(n), kThreads, 0, s>>>(c4, ni, l.bbox);
+        xyz_bbox_kernel<<<bounds_blocks(n), kThreads, 0, s>>>(c4, ni, l.bbox);
         launch_check("xyz_bbox");
         downsample_map_kernel<<<blocks_for(n), kThreads, 0, s>>>(c4, ni, l.bbox, factor, l.mapped);
         launch_check("downsample_map");

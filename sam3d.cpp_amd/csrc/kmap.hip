@@ -89,30 +89,16 @@ child_kmap_kernel(const int32_t *__restrict__ parent_kmap, int32_t p, int32_t *_
 __global__ void __launch_bounds__(kThreads)
 coarse_keys_kernel(const int4 *__restrict__ coords, int32_t n, int4 *__restrict__ ckeys,
                    int32_t *bbox) {
-    const int32_t i = blockIdx.x * kThreads + threadIdx.x;
-    int4 k = make_int4(INT32_MAX, INT32_MAX, INT32_MAX, INT32_MAX);
-    int4 kmax = make_int4(INT32_MIN, INT32_MIN, INT32_MIN, INT32_MIN);
-    if (i < n) {
+    int v[8] = {INT32_MAX, INT32_MAX, INT32_MAX, INT32_MAX, INT32_MIN, INT32_MIN, INT32_MIN, INT32_MIN};
+    for (int32_t i = blockIdx.x * kThreads + threadIdx.x; i < n; i += gridDim.x * kThreads) {
         const int4 c = coords[i];
         // C++ integer division truncates toward zero (sparse_ops.cpp:63-64).
-        k = make_int4(c.x, c.y / 2, c.z / 2, c.w / 2);
+        const int4 k = make_int4(c.x, c.y / 2, c.z / 2, c.w / 2);
         ckeys[i] = k;
-        kmax = k;
+        v[0] = min(v[0], k.x); v[1] = min(v[1], k.y); v[2] = min(v[2], k.z); v[3] = min(v[3], k.w);
+        v[4] = max(v[4], k.x); v[5] = max(v[5], k.y); v[6] = max(v[6], k.z); v[7] = max(v[7], k.w);
     }
-    int v[8] = {k.x, k.y, k.z, k.w, kmax.x, kmax.y, kmax.z, kmax.w};
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) {
-#pragma unroll
-        for (int a = 0; a < 4; ++a) v[a] = min(v[a], __shfl_xor(v[a], d, 64));
-#pragma unroll
-        for (int a = 4; a < 8; ++a) v[a] = max(v[a], __shfl_xor(v[a], d, 64));
-    }
-    if ((threadIdx.x & 63) == 0) {
-#pragma unroll
-        for (int a = 0; a < 4; ++a) atomicMin(&bbox[a], v[a]);
-#pragma unroll
-        for (int a = 4; a < 8; ++a) atomicMax(&bbox[a], v[a]);
-    }
+    block_bounds_atomic<4>(v, bbox);
 }
 
 struct DenseGrid {
@@ -451,7 +437,7 @@ S3DX_API s3dx_status s3dx_coarsen2(const int32_t *coords, int64_t n, int32_t *co
         // 1. coarse keys + their bounding box.
         fill_u32(reinterpret_cast<uint32_t *>(l.bbox), 4, static_cast<uint32_t>(INT32_MAX), s);
         fill_u32(reinterpret_cast<uint32_t *>(l.bbox) + 4, 4, static_cast<uint32_t>(INT32_MIN), s);
-        coarse_keys_kernel<<<blocks_for(ni), kThreads, 0, s>>>(c4, ni, l.ckeys, l.bbox);
+        coarse_keys_kernel<<<bounds_blocks(ni), kThreads, 0, s>>>(c4, ni, l.ckeys, l.bbox);
         launch_check("coarse_keys");
         int32_t bbox[8];
         hip_check(hipMemcpyAsync(bbox, l.bbox, sizeof(bbox), hipMemcpyDeviceToHost, s),
