@@ -77,12 +77,18 @@ def test_down_up_sample(s3dx, O, W):
     assert np.array_equal(up.download(), O.upsample_nearest(down.download(), f2c.download()))
 
 
-def test_convert_roundtrip(s3dx, W):
-    x = W.normal_f32(14, 1, (4096,), 100.0)
+@pytest.mark.parametrize("count", [4096, 4099, 13, 40_000_003])
+def test_convert_roundtrip(s3dx, W, count):
+    # 8-element vector steps plus a scalar tail; 40M elements also runs more
+    # than one grid-stride pass.
+    x = W.normal_f32(14, 1, (count,), 100.0)
     d = dev(s3dx, x)
-    b = s3dx.DeviceArray((4096,), np.uint16)
-    s3dx.convert(d, s3dx.F32, 4096, b, s3dx.BF16)
+    b = s3dx.DeviceArray((count,), np.uint16)
+    s3dx.convert(d, s3dx.F32, count, b, s3dx.BF16)
     assert np.array_equal(b.download(), W.f32_to_bf16_bits(x))
-    back = s3dx.DeviceArray((4096,), np.float32)
-    s3dx.convert(b, s3dx.BF16, 4096, back, s3dx.F32)
+    back = s3dx.DeviceArray((count,), np.float32)
+    s3dx.convert(b, s3dx.BF16, count, back, s3dx.F32)
     assert np.array_equal(back.download(), W.round_bf16(x))
+    same = s3dx.DeviceArray((count,), np.float32)
+    s3dx.convert(back, s3dx.F32, count, same, s3dx.F32)
+    assert np.array_equal(same.download(), back.download())
