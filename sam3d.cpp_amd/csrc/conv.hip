@@ -323,6 +323,7 @@ const Tiling *choose_tiling(int64_t n_out, int nb, int ntiles, bool bf, int kc, 
     for (const Tiling &t : kTilings) {
         if (!usable(t)) continue;
         int rank;
+        if (t.id == 17) continue;                  // 64-row tiles: chosen by plan_launch
         if (t.splitk) rank = t.id >= 15 ? 0 : 1;  // 128-channel tasks (chunks joined) first
         else if (t.wn == 1 && t.nbw == 4) rank = blocks(t) >= 192 ? 2 : 10;  // 32x128 wave tiles
         else if (t.mbw == 2) rank = blocks(t) >= 256 ? 3 : 20;
@@ -459,6 +460,16 @@ LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bo
                 for (int nb : {4, 3, 2})
                     if (!found && nb < conv->nb && blocks % nb == 0 && try_nb(nb)) found = p.tl->splitk;
                 if (!found) p = whole;
+            }
+            // More 128-row tiles than one pass over the CUs: the 64-row
+            // split-K tiling (two workgroups per CU) shortens the last pass
+            // (config 3, 320 tiles: ~15%); where it exists for the shape.
+            if (p.tl->id == 11 && forced == 0 && !std::getenv("S3DX_CONV_TILING")) {
+                const int64_t rt = (n_out + 127) / 128;
+                if (rt * (blocks / p.nb) > device_cus() && tiling_kernel(17, bf, p.kc, p.xf)) {
+                    for (const Tiling &t : kTilings)
+                        if (t.id == 17) p.tl = &t;
+                }
             }
             // Few row tiles (small voxel sets): split-K runs one workgroup
             // per CU, so narrower column tiles that still fit in one pass

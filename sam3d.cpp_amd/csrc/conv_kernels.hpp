@@ -44,14 +44,14 @@ using KernelFn = void (*)(ConvArgs);
 // 64-channel chunks) build each 128-channel task from 4 or 2 chunks.
 struct Tiling {
     int id, mbw, nbw, wn, splitk;
-    int rows() const { return splitk ? 128 : 32 * mbw * (4 / wn); }
+    int rows() const { return splitk ? 32 * mbw : 32 * mbw * (4 / wn); }
     int cols() const { return 32 * nbw * wn; }
 };
 inline constexpr Tiling kTilings[] = {
     {0, 1, 1, 1, 0}, {1, 1, 1, 2, 0}, {2, 1, 3, 1, 0}, {3, 1, 2, 2, 0}, {4, 1, 3, 2, 0},
     {5, 1, 4, 2, 0}, {6, 2, 1, 2, 0}, {7, 2, 3, 1, 0}, {8, 2, 2, 2, 0}, {9, 2, 3, 2, 0},
     {10, 1, 4, 1, 0}, {11, 4, 4, 1, 1}, {12, 4, 2, 1, 1}, {13, 4, 3, 1, 1}, {14, 4, 1, 1, 1},
-    {15, 4, 3, 1, 1}, {16, 4, 4, 1, 1},
+    {15, 4, 3, 1, 1}, {16, 4, 4, 1, 1}, {17, 2, 4, 1, 1},
 };
 
 // MFMA kernel for tiling `id`, kc channels per task, xf 64-bit gathers;
@@ -702,16 +702,17 @@ conv_mfma_kernel(ConvArgs a) {
 // tiles are summed through LDS in a fixed order (deterministic), then
 // finished by the same row-major epilogue.
 // ---------------------------------------------------------------------------
-template <class T, int NB, int KC>
+template <class T, int NB, int KC, int MB>
 struct SplitSmem {
-    static constexpr int BM = 128;
+    static constexpr int BM = 32 * MB;
+    static constexpr int RPH = MB == 4 ? 2 : 1;  // 32-row blocks reduced per phase
     static constexpr int NT = 32 * NB;
     static constexpr int ROWB = KC * static_cast<int>(sizeof(T));  // A bytes per row per task
     static constexpr int A_LD = ROWB + 16;                          // padded LDS row
     static constexpr int A_BYTES = 2 * BM * A_LD;                   // double buffer
     static constexpr int STG_LD = NT + 8;
     static constexpr int TPR = NT / 8;
-    static constexpr int RED_BYTES = 8 * NB * 16 * 64 * 4;  // 8 partial 32-row blocks
+    static constexpr int RED_BYTES = RPH * NB * 4 * 4096;  // per phase: RPH x NB blocks x 4 writers, 4 KiB each
     static constexpr int STG_BYTES = BM * STG_LD * 4;
     static constexpr int PART_BYTES = 2 * BM * TPR * 4;
     static constexpr int R0A = RED_BYTES > A_BYTES ? RED_BYTES : A_BYTES;
@@ -723,9 +724,10 @@ struct SplitSmem {
 // SUB > 1: a task is SUB consecutive sub-tasks (offset, KC/SUB-channel
 // chunk), so that Cin of 96 (32-channel chunks) or 192 (64) still gives each
 // wave whole k-steps of a 128-channel task.
-template <class T, int NB, int KC, int XF, int SUB>
-__global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
-    using SM = SplitSmem<T, NB, KC>;
+template <class T, int NB, int KC, int XF, int SUB, int MB>
+__global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_splitk_kernel(ConvArgs a) {
+    using SM = SplitSmem<T, NB, KC, MB>;
+    constexpr int RPH = SM::RPH;
     constexpr int E = Frag<T>::E;
     constexpr int CPK = 2 * E;
     constexpr int KS = KC / CPK;  // k-steps per task
@@ -892,9 +894,9 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
         return reinterpret_cast<uint4 *>(buf + (u / PPR) * SM::A_LD + (u % PPR) * 16);
     };
 
-    f32x16 acc[4][NB];
+    f32x16 acc[MB][NB];
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
+    for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f32x16{};
     // A fragments of k-step (wave + 4 i) from an LDS buffer (lane: row
@@ -904,7 +906,7 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
 #pragma unroll
         for (int i = 0; i < KSW; ++i)
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb)
+            for (int mb = 0; mb < MB; ++mb)
                 af[i][mb] = *reinterpret_cast<const uint4 *>(base + mb * 32 * SM::A_LD +
                                                              i * 4 * CPK * static_cast<int>(sizeof(T)));
     };
@@ -917,10 +919,10 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
 #pragma unroll
         for (int i = 0; i < KSW; ++i)
 #pragma unroll
-            for (int mb = 0; mb < 4; ++mb)
+            for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
                 for (int nb = 0; nb < NB; ++nb) {
-                    const int idx = (i * 4 + mb) * NB + nb;
+                    const int idx = (i * MB + mb) * NB + nb;
                     if (idx >= lo && idx < hi) acc[mb][nb] = mfma_step<T>(af[i][mb], bf[i][nb], acc[mb][nb]);
                 }
     };
@@ -936,13 +938,13 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
     //                into bc.
     // The next body starts its MFMAs at once: its fragments are in registers.
     constexpr int MPS = sizeof(T) == 2 ? 1 : 4;  // MFMA instructions per fragment pair
-    constexpr int NPAIR = KSW * 4 * NB;           // fragment pairs per task
+    constexpr int NPAIR = KSW * MB * NB;          // fragment pairs per task
     constexpr int HALF = NPAIR / 2;
     constexpr int NMF1 = HALF * MPS, NMF2 = (NPAIR - HALF) * MPS;
     constexpr int M0 = NMF1 < 4 ? NMF1 : 4;       // MFMAs before the first LDS store
     constexpr int MI = (NMF1 - M0) / APT;
     constexpr int MR = NMF1 - M0 - MI * APT;
-    constexpr int NFR = KSW * 4;                  // fragment reads
+    constexpr int NFR = KSW * MB;                 // fragment reads
     constexpr int MJ = NMF2 / (NFR + 1);
     constexpr int MK = NMF2 - MJ * NFR;
     auto body = [&](const uint4 (&afc)[KSW][4], uint4 (&afn)[KSW][4], uint4 (&bc)[KSW][NB], char *wbuf,
@@ -1092,15 +1094,16 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
         lds_barrier();  // the last fragment reads finish before the tile reuses LDS
     }
 
-    // ---- reduce the 4 partial tiles through LDS, 64 rows per phase ----
-    // Phase p covers row blocks 2p, 2p+1; pair (h, c) = (block 2p+h, column
+    // ---- reduce the 4 partial tiles through LDS, in two phases ----
+    // Phase p covers row blocks RPH*p .. RPH*p+RPH-1 (RPH = 2 for 128-row
+    // tiles, 1 for 64-row ones); pair (h, c) = (block RPH*p+h, column
     // block c) is summed by wave (h*NB + c) % 4 into registers, the other
     // waves handing their partials over as float4 [4][lane] slots (16-byte
     // lane stride, conflict-free).  With ROT the owner keeps its own partial
     // (accumulator 0) and only three cross LDS.  Sums run in a fixed order,
     // so results are deterministic.  Accumulators are only indexed by
     // compile-time constants.
-    constexpr int PPW = (2 * NB + 3) / 4;  // pairs per wave per phase
+    constexpr int PPW = (RPH * NB + 3) / 4;  // pairs per wave per phase
     auto slot_of = [&](int h, int c, int writer) __attribute__((always_inline)) {
         return red + ((h * NB + c) * 4 + writer) * (4 * 64);
     };
@@ -1109,26 +1112,26 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
     for (int p = 0; p < 2; ++p) {
         if (p) __syncthreads();
 #pragma unroll
-        for (int h = 0; h < 2; ++h)
+        for (int h = 0; h < RPH; ++h)
 #pragma unroll
             for (int k = ROT ? 1 : 0; k < NB; ++k) {
                 const int c = ROT ? ((k + wave) & 3) : k;
                 float4 *slot = slot_of(h, c, wave);
 #pragma unroll
                 for (int g = 0; g < 4; ++g)
-                    slot[g * 64 + lane] = make_float4(acc[2 * p + h][k][4 * g], acc[2 * p + h][k][4 * g + 1],
-                                                      acc[2 * p + h][k][4 * g + 2], acc[2 * p + h][k][4 * g + 3]);
+                    slot[g * 64 + lane] = make_float4(acc[RPH * p + h][k][4 * g], acc[RPH * p + h][k][4 * g + 1],
+                                                      acc[RPH * p + h][k][4 * g + 2], acc[RPH * p + h][k][4 * g + 3]);
             }
         __syncthreads();
         if constexpr (ROT) {
             // Wave w owns (h, w) for h = 0, 1: its accumulator 0 plus the
             // other three waves' slots.
 #pragma unroll
-            for (int h = 0; h < 2; ++h)
+            for (int h = 0; h < RPH; ++h)
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
-                    float4 sum = make_float4(acc[2 * p + h][0][4 * g], acc[2 * p + h][0][4 * g + 1],
-                                             acc[2 * p + h][0][4 * g + 2], acc[2 * p + h][0][4 * g + 3]);
+                    float4 sum = make_float4(acc[RPH * p + h][0][4 * g], acc[RPH * p + h][0][4 * g + 1],
+                                             acc[RPH * p + h][0][4 * g + 2], acc[RPH * p + h][0][4 * g + 3]);
 #pragma unroll
                     for (int s2 = 1; s2 < 4; ++s2) {
                         const float4 v = slot_of(h, wave, (wave + s2) & 3)[g * 64 + lane];
@@ -1146,7 +1149,7 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
 #pragma unroll
             for (int i = 0; i < PPW; ++i) {
                 const int q = wave + 4 * i;
-                if (q >= 2 * NB) continue;
+                if (q >= RPH * NB) continue;
                 const int h = q / NB, c = q - h * NB;
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
@@ -1174,10 +1177,10 @@ __global__ void __launch_bounds__(256, 1) conv_splitk_kernel(ConvArgs a) {
 #pragma unroll
         for (int i = 0; i < PPW; ++i) {
             const int q = wave + 4 * i;
-            if (q >= 2 * NB) continue;
+            if (q >= RPH * NB) continue;
             const int h = q / NB, c = q - h * NB;
             const int col = c * 32 + (lane & 31);
-            const int rb = (2 * p + h) * 32 + 4 * half;
+            const int rb = (RPH * p + h) * 32 + 4 * half;
 #pragma unroll
             for (int r = 0; r < 16; ++r) stg[(rb + 8 * (r >> 2) + (r & 3)) * SM::STG_LD + col] = fin[p][i][r];
         }
@@ -1354,21 +1357,27 @@ KernelFn pick_tiling(int id) {
     case 11: case 12: case 13: case 14: {
         constexpr int KS = KC / (2 * Frag<T>::E);
         if constexpr (KS % 4 == 0) {
-            if (id == 11) return conv_splitk_kernel<T, 4, KC, XF, 1>;
-            if (id == 12) return conv_splitk_kernel<T, 2, KC, XF, 1>;
-            if (id == 13) return conv_splitk_kernel<T, 3, KC, XF, 1>;
-            return conv_splitk_kernel<T, 1, KC, XF, 1>;
+            if (id == 11) return conv_splitk_kernel<T, 4, KC, XF, 1, 4>;
+            if (id == 12) return conv_splitk_kernel<T, 2, KC, XF, 1, 4>;
+            if (id == 13) return conv_splitk_kernel<T, 3, KC, XF, 1, 4>;
+            return conv_splitk_kernel<T, 1, KC, XF, 1, 4>;
         } else {
             return nullptr;
         }
     }
     case 15: case 16: {
         if constexpr (sizeof(T) == 2 && XF == 0 && (KC == 32 || KC == 64)) {
-            if (id == 15) return conv_splitk_kernel<T, 3, 128, XF, 128 / KC>;
-            return conv_splitk_kernel<T, 4, 128, XF, 128 / KC>;
+            if (id == 15) return conv_splitk_kernel<T, 3, 128, XF, 128 / KC, 4>;
+            return conv_splitk_kernel<T, 4, 128, XF, 128 / KC, 4>;
         } else {
             return nullptr;
         }
+    }
+    case 17: {  // 64-row tiles, two workgroups per CU
+        if constexpr (sizeof(T) == 2 && XF == 0 && KC == 128)
+            return conv_splitk_kernel<T, 4, 128, XF, 1, 2>;
+        else
+            return nullptr;
     }
     default: return nullptr;
     }
