@@ -323,7 +323,7 @@ const Tiling *choose_tiling(int64_t n_out, int nb, int ntiles, bool bf, int kc, 
     for (const Tiling &t : kTilings) {
         if (!usable(t)) continue;
         int rank;
-        if (t.id == 17) continue;                  // 64-row tiles: chosen by plan_launch
+        if (t.id == 17 || t.id == 18) continue;   // 64-row tiles: chosen by plan_launch
         if (t.splitk) rank = t.id >= 15 ? 0 : 1;  // 128-channel tasks (chunks joined) first
         else if (t.wn == 1 && t.nbw == 4) rank = blocks(t) >= 192 ? 2 : 10;  // 32x128 wave tiles
         else if (t.mbw == 2) rank = blocks(t) >= 256 ? 3 : 20;
@@ -454,6 +454,15 @@ LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bo
             forced > 0 && blocks % forced == 0 && (!conv->ln || forced * 32 == conv->cout) && try_nb(forced);
         if (!use_forced) {
             require(try_nb(conv->nb), "no MFMA kernel for this shape");
+            // S3DX_CONV_TILING=18 (tuning, tests): its tasks are 64 channels.
+            if (const char *e = std::getenv("S3DX_CONV_TILING"))
+                if (std::atoi(e) == 18 && conv->cin % 64 == 0 && tiling_kernel(18, bf, 64, p.xf) &&
+                    p.nb == 4)
+                    for (const Tiling &t : kTilings)
+                        if (t.id == 18) {
+                            p.tl = &t;
+                            p.kc = 64;
+                        }
             if (!p.tl->splitk && !conv->ln && conv->kvol == kMaxKvol) {
                 const LaunchPlan whole = p;
                 bool found = false;
@@ -461,20 +470,27 @@ LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bo
                     if (!found && nb < conv->nb && blocks % nb == 0 && try_nb(nb)) found = p.tl->splitk;
                 if (!found) p = whole;
             }
-            // More 128-row tiles than one pass over the CUs: the 64-row
-            // split-K tiling (two workgroups per CU) shortens the last pass
-            // (config 3, 320 tiles: ~15%); where it exists for the shape.
+            // 128-column BF16 tiles: 64-row tiles with two workgroups per CU
+            // overlap one workgroup's gathers, barriers and epilogue with the
+            // other's MFMAs.  More 128-row tiles than one pass over the CUs:
+            // 128-channel tasks (tiling 17; shortens the last pass, config 3
+            // ~15%); one reasonably full pass: 64-channel tasks (tiling 18,
+            // fewer registers; config 2 ~5%).
             if (p.tl->id == 11 && forced == 0 && !std::getenv("S3DX_CONV_TILING")) {
                 const int64_t rt = (n_out + 127) / 128;
-                if (rt * (blocks / p.nb) > device_cus() && tiling_kernel(17, bf, p.kc, p.xf)) {
+                const int64_t cus = device_cus(), tiles = rt * (blocks / p.nb);
+                const int id = tiles > cus ? 17 : (2 * tiles >= cus && conv->cin % 64 == 0 ? 18 : 0);
+                const int kc = id == 18 ? 64 : p.kc;
+                if (id != 0 && tiling_kernel(id, bf, kc, p.xf)) {
                     for (const Tiling &t : kTilings)
-                        if (t.id == 17) p.tl = &t;
+                        if (t.id == id) p.tl = &t;
+                    p.kc = kc;
                 }
             }
             // Few row tiles (small voxel sets): split-K runs one workgroup
             // per CU, so narrower column tiles that still fit in one pass
             // over the CUs finish sooner (each re-gathers A from L2).
-            if (p.tl->splitk && !conv->ln) {
+            if (p.tl->splitk && !conv->ln && !std::getenv("S3DX_CONV_TILING")) {
                 const int64_t rt = (n_out + 127) / 128;
                 const int64_t cus = device_cus();
                 if (rt * (blocks / p.nb) < cus) {

@@ -41,7 +41,9 @@ using KernelFn = void (*)(ConvArgs);
 // wave MBW x NBW blocks of 32x32 outputs.
 // Split-K tilings (splitk = 1): 128 rows x 32*nbw columns, each wave owning
 // the whole tile for a quarter of the k-steps.  Ids 15 and 16 (BF16, 32- or
-// 64-channel chunks) build each 128-channel task from 4 or 2 chunks.
+// 64-channel chunks) build each 128-channel task from 4 or 2 chunks.  Ids 17
+// and 18 (BF16, 128 columns) use 64-row tiles, two workgroups per CU, with
+// 128- and 64-channel tasks.
 struct Tiling {
     int id, mbw, nbw, wn, splitk;
     int rows() const { return splitk ? 32 * mbw : 32 * mbw * (4 / wn); }
@@ -51,7 +53,7 @@ inline constexpr Tiling kTilings[] = {
     {0, 1, 1, 1, 0}, {1, 1, 1, 2, 0}, {2, 1, 3, 1, 0}, {3, 1, 2, 2, 0}, {4, 1, 3, 2, 0},
     {5, 1, 4, 2, 0}, {6, 2, 1, 2, 0}, {7, 2, 3, 1, 0}, {8, 2, 2, 2, 0}, {9, 2, 3, 2, 0},
     {10, 1, 4, 1, 0}, {11, 4, 4, 1, 1}, {12, 4, 2, 1, 1}, {13, 4, 3, 1, 1}, {14, 4, 1, 1, 1},
-    {15, 4, 3, 1, 1}, {16, 4, 4, 1, 1}, {17, 2, 4, 1, 1},
+    {15, 4, 3, 1, 1}, {16, 4, 4, 1, 1}, {17, 2, 4, 1, 1}, {18, 2, 4, 1, 1},
 };
 
 // MFMA kernel for tiling `id`, kc channels per task, xf 64-bit gathers;
@@ -1373,9 +1375,11 @@ KernelFn pick_tiling(int id) {
             return nullptr;
         }
     }
-    case 17: {  // 64-row tiles, two workgroups per CU
+    case 17: case 18: {  // 64-row tiles, two workgroups per CU (18: 64-channel tasks)
         if constexpr (sizeof(T) == 2 && XF == 0 && KC == 128)
-            return conv_splitk_kernel<T, 4, 128, XF, 1, 2>;
+            return id == 17 ? conv_splitk_kernel<T, 4, 128, XF, 1, 2> : nullptr;
+        else if constexpr (sizeof(T) == 2 && XF == 0 && KC == 64)
+            return id == 18 ? conv_splitk_kernel<T, 4, 64, XF, 1, 2> : nullptr;
         else
             return nullptr;
     }

@@ -106,7 +106,8 @@ def test_conv_plan_names_the_launched_kernel(s3dx, monkeypatch):
     monkeypatch.delenv("S3DX_CONV_TILING", raising=False)
     n = 28265  # 64^3 eight-shell union, seed 0
     c128 = s3dx.SparseConv(128, 128, 27, s3dx.BF16)
-    assert c128.plan(n, n) == "mfma tiling=11 split-k rows=128 cols=128 kc=128 xf=0 ln=none grid=221x1"
+    # one pass of 128-row tiles on 256 CUs: 64-row tiles, two per CU, 64-channel tasks
+    assert c128.plan(n, n) == "mfma tiling=18 split-k rows=64 cols=128 kc=64 xf=0 ln=none grid=442x1"
     c128.set_layernorm(True, 1e-6)
     assert "ln=fused" in c128.plan(n, n)
     f64 = s3dx.SparseConv(64, 64, 27, s3dx.F32)
