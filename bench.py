@@ -90,10 +90,16 @@ class Block:
 
 
 def _event_us(s3dx, stream, fn, reps=10, warm=2):
-    """Median device time of fn() on `stream`, HIP events around each call."""
-    for _ in range(warm):
+    """Median device time of fn() on `stream`, HIP timing events around each
+    call, after >= `warm` calls and ~50 ms of untimed calls (clocks settle)."""
+    t0 = time.perf_counter()
+    done = 0
+    while done < warm or time.perf_counter() - t0 < 0.05:
         fn()
-    ev = [(s3dx.Event(), s3dx.Event()) for _ in range(reps)]
+        done += 1
+        if done % 8 == 0:
+            stream.synchronize()
+    ev = [(s3dx.Event(timing=True), s3dx.Event(timing=True)) for _ in range(reps)]
     for a, b in ev:
         a.record(stream)
         fn()
@@ -367,14 +373,22 @@ def main():
             ev_k[1].record(stream)
         bf.run(kmap, ev_b)
 
+    # Clock settle: the GPU ramps its clocks over tens of milliseconds of
+    # load, so the step runs untimed for ~150 ms before the W warm-up steps
+    # (10 warm-up steps alone leave the timed region ~6% below steady state).
+    t_settle = time.perf_counter()
+    while time.perf_counter() - t_settle < 0.15:
+        for _ in range(20):
+            step()
+        stream.synchronize()
     for _ in range(args.warmup):
         step()
         f32.run(kmap)
     stream.synchronize()
 
     K = args.steps
-    evk = [[s3dx.Event(), s3dx.Event()] for _ in range(K)]
-    evb = [[s3dx.Event(), s3dx.Event(), s3dx.Event()] for _ in range(K)]
+    evk = [[s3dx.Event(timing=True), s3dx.Event(timing=True)] for _ in range(K)]
+    evb = [[s3dx.Event(timing=True), s3dx.Event(timing=True), s3dx.Event(timing=True)] for _ in range(K)]
     stream.synchronize()
     t0 = time.perf_counter()
     for i in range(K):
@@ -390,7 +404,7 @@ def main():
     kmap_avg = statistics.mean(kmap_ms)
 
     # FP32 block, timed the same way after the BF16 region.
-    evf = [[s3dx.Event(), s3dx.Event(), s3dx.Event()] for _ in range(K)]
+    evf = [[s3dx.Event(timing=True), s3dx.Event(timing=True), s3dx.Event(timing=True)] for _ in range(K)]
     for i in range(K):
         f32.run(kmap, evf[i])
     stream.synchronize()

@@ -79,6 +79,11 @@ S3DX_API s3dx_status s3dx_stream_create(s3dx_stream *out, char *error, uint64_t 
 S3DX_API s3dx_status s3dx_stream_destroy(s3dx_stream stream, char *error, uint64_t error_capacity);
 S3DX_API s3dx_status s3dx_stream_synchronize(s3dx_stream stream, char *error, uint64_t error_capacity);
 S3DX_API s3dx_status s3dx_event_create(s3dx_event *out, char *error, uint64_t error_capacity);
+/* An event for timing only (no counterpart in the reference; for benchmarks):
+ * recording it skips the system-scope memory fence, whose cache write-back and
+ * invalidation would otherwise land between the timed launches.  Not for
+ * making device writes visible to the host. */
+S3DX_API s3dx_status s3dx_timing_event_create(s3dx_event *out, char *error, uint64_t error_capacity);
 S3DX_API s3dx_status s3dx_event_destroy(s3dx_event event, char *error, uint64_t error_capacity);
 S3DX_API s3dx_status s3dx_event_record(s3dx_event event, s3dx_stream stream, char *error,
                                        uint64_t error_capacity);

@@ -54,6 +54,7 @@ SIGNATURES = {
     "s3dx_stream_destroy": (_u32, [_vp], True),
     "s3dx_stream_synchronize": (_u32, [_vp], True),
     "s3dx_event_create": (_u32, [C.POINTER(_vp)], True),
+    "s3dx_timing_event_create": (_u32, [C.POINTER(_vp)], True),
     "s3dx_event_destroy": (_u32, [_vp], True),
     "s3dx_event_record": (_u32, [_vp, _vp], True),
     "s3dx_event_elapsed_ms": (_u32, [_vp, _vp, C.POINTER(_f32)], True),
@@ -196,9 +197,12 @@ class Stream:
 
 
 class Event:
-    def __init__(self):
+    """A HIP event; timing=True: for measuring intervals only (no system-scope
+    fence on record, see s3dx_timing_event_create)."""
+
+    def __init__(self, timing: bool = False):
         p = _vp()
-        call("s3dx_event_create", C.byref(p))
+        call("s3dx_timing_event_create" if timing else "s3dx_event_create", C.byref(p))
         self.handle = p.value
 
     def record(self, stream=None):

@@ -233,6 +233,17 @@ S3DX_API s3dx_status s3dx_event_create(s3dx_event *out, char *error, uint64_t er
     });
 }
 
+S3DX_API s3dx_status s3dx_timing_event_create(s3dx_event *out, char *error, uint64_t error_capacity) {
+    return boundary(error, error_capacity, [&] {
+        require(out != nullptr, "out is NULL");
+        hipEvent_t e = nullptr;
+        // No system-scope fence on record: no cache write-back / invalidate
+        // between the timed launches, so the interval is the work's own.
+        hip_check(hipEventCreateWithFlags(&e, hipEventDisableSystemFence), "hipEventCreateWithFlags");
+        *out = e;
+    });
+}
+
 S3DX_API s3dx_status s3dx_event_destroy(s3dx_event event, char *error, uint64_t error_capacity) {
     return boundary(error, error_capacity, [&] {
         if (event) hip_check(hipEventDestroy(reinterpret_cast<hipEvent_t>(event)), "hipEventDestroy");
