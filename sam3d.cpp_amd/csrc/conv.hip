@@ -456,12 +456,12 @@ LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bo
             require(try_nb(conv->nb), "no MFMA kernel for this shape");
             // S3DX_CONV_TILING=18 (tuning, tests): its tasks are 64 channels.
             if (const char *e = std::getenv("S3DX_CONV_TILING"))
-                if (std::atoi(e) == 18 && conv->cin % 64 == 0 && tiling_kernel(18, bf, 64, p.xf) &&
-                    p.nb == 4)
+                if (std::atoi(e) == 18 && conv->cin % (bf ? 64 : 32) == 0 &&
+                    tiling_kernel(18, bf, bf ? 64 : 32, p.xf) && p.nb == 4)
                     for (const Tiling &t : kTilings)
                         if (t.id == 18) {
                             p.tl = &t;
-                            p.kc = 64;
+                            p.kc = bf ? 64 : 32;
                         }
             if (!p.tl->splitk && !conv->ln && conv->kvol == kMaxKvol) {
                 const LaunchPlan whole = p;
@@ -479,8 +479,9 @@ LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bo
             if (p.tl->id == 11 && forced == 0 && !std::getenv("S3DX_CONV_TILING")) {
                 const int64_t rt = (n_out + 127) / 128;
                 const int64_t cus = device_cus(), tiles = rt * (blocks / p.nb);
-                const int id = tiles > cus ? 17 : (2 * tiles >= cus && conv->cin % 64 == 0 ? 18 : 0);
-                const int kc = id == 18 ? 64 : p.kc;
+                const int kc18 = bf ? 64 : 32;  // half-width tasks
+                const int id = tiles > cus ? 17 : (2 * tiles >= cus && conv->cin % kc18 == 0 ? 18 : 0);
+                const int kc = id == 18 ? kc18 : p.kc;
                 if (id != 0 && tiling_kernel(id, bf, kc, p.xf)) {
                     for (const Tiling &t : kTilings)
                         if (t.id == id) p.tl = &t;

@@ -1375,11 +1375,13 @@ KernelFn pick_tiling(int id) {
             return nullptr;
         }
     }
-    case 17: case 18: {  // 64-row tiles, two workgroups per CU (18: 64-channel tasks)
+    case 17: case 18: {  // 64-row tiles, two workgroups per CU (18: half-width tasks)
         if constexpr (sizeof(T) == 2 && XF == 0 && KC == 128)
             return id == 17 ? conv_splitk_kernel<T, 4, 128, XF, 1, 2> : nullptr;
         else if constexpr (sizeof(T) == 2 && XF == 0 && KC == 64)
             return id == 18 ? conv_splitk_kernel<T, 4, 64, XF, 1, 2> : nullptr;
+        else if constexpr (sizeof(T) == 4 && XF == 0 && KC == 32)
+            return id == 18 ? conv_splitk_kernel<T, 4, 32, XF, 1, 2> : nullptr;
         else
             return nullptr;
     }
