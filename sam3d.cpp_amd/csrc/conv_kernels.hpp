@@ -1076,6 +1076,10 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_splitk_kernel(ConvA
         for (int q = 0; q < APT; ++q) *a_slot(buf0, q) = ra[q];
         next_task(cur, left, nx);  // task 1
         load_a(nx, ra);
+        // Gathers before weights, as in the loop body: the wait counts at the
+        // loop head then match steady state (else the first body of each pair
+        // also waits for the weights issued after its gathers).
+        sched_fence();
         if (odd) load_b(nx, b0);
         else load_b(nx, b1);
         next_task(cur, left, nx);  // task 2
