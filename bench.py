@@ -159,6 +159,22 @@ def extras(s3dx, W, stream, seed):
     y = s3dx.DeviceArray((nc, 1024), np.uint16)
     conv_entry("config3_bf16_conv_1024", conv, x, nc, k3, nc, y, bf, p3, 1024, 1024, PEAK_BF16_TFLOPS)
 
+    # SLat sparse I/O (slat_flow_graph.cpp:159-190) at C=128 BF16: 2x mean-pool
+    # of the fine rows onto the coarse set, then nearest upsample back.
+    # Compulsory bytes: every source row, index and output row once.
+    f2c, ch, inv = res["c"][2], res["c"][3], res["c"][4]
+    xf = s3dx.DeviceArray.from_host(W.f32_to_bf16_bits(W.normal_f32(seed, 310, (n2, 128))), stream)
+    yc = s3dx.DeviceArray((nc, 128), np.uint16)
+    yf = s3dx.DeviceArray((n2, 128), np.uint16)
+    for name, fn, nbytes in (
+            ("downsample_mean_bf16_128", lambda: s3dx.downsample_mean(xf, bf, n2, 128, ch, inv, nc, yc, stream),
+             n2 * 256 + nc * (8 * 4 + 4 + 256)),
+            ("upsample_nearest_bf16_128", lambda: s3dx.upsample_nearest(yc, bf, nc, 128, f2c, n2, yf, stream),
+             nc * 256 + n2 * (4 + 256))):
+        us = _event_us(s3dx, stream, fn)
+        out[name] = {"us": us, "gb_s": nbytes / us / 1e3, "peak_gb_s": PEAK_HBM_GBS,
+                     "frac": nbytes / us / 1e3 / PEAK_HBM_GBS, "fine": n2, "coarse": nc, "bytes": nbytes}
+
     # occupancy -> coordinates (session.cpp:1437-1474) on a noisy 64^3 field
     # with the reference fixture's density (~27% occupied, mostly surface):
     # threshold, surface prune, downsample to 42,000 rows; buffers reused,

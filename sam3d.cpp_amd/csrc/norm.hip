@@ -271,6 +271,59 @@ upsample_kernel(const void *coarse, int64_t nc, int32_t c, const int32_t *f2c, i
     }
 }
 
+// Row-piece variants: rows of whole 16-byte pieces (E = 8 BF16 or 4 FP32
+// values), both buffers 16-byte aligned, fewer than 2^30 pieces.  Each
+// element sums its children in the same order as the kernels above.
+template <class T>
+__global__ void __launch_bounds__(256)
+downsample16_kernel(const uint4 *x, int64_t nf, int32_t ppr, const int32_t *children,
+                    const float *inv_count, int32_t count, uint4 *y) {
+    constexpr int E = 16 / static_cast<int>(sizeof(T));
+    for (int32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < count; i += gridDim.x * blockDim.x) {
+        const int32_t r = i / ppr, pc = i - r * ppr;
+        float acc[E];
+#pragma unroll
+        for (int e = 0; e < E; ++e) acc[e] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int32_t f = children[static_cast<int64_t>(r) * 8 + j];
+            if (f < 0 || f >= nf) continue;
+            const uint4 v = x[static_cast<int64_t>(f) * ppr + pc];
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int e = 0; e < E; ++e) {
+                if constexpr (sizeof(T) == 2)
+                    acc[e] += bf16_to_f32(static_cast<uint16_t>(e & 1 ? w[e >> 1] >> 16 : w[e >> 1] & 0xffffu));
+                else
+                    acc[e] += __builtin_bit_cast(float, w[e]);
+            }
+        }
+        const float k = inv_count[r];
+        uint32_t o[4];
+        if constexpr (sizeof(T) == 2) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                o[q] = static_cast<uint32_t>(f32_to_bf16(acc[2 * q] * k)) |
+                       (static_cast<uint32_t>(f32_to_bf16(acc[2 * q + 1] * k)) << 16);
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) o[q] = __builtin_bit_cast(uint32_t, acc[q] * k);
+        }
+        y[i] = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+}
+
+// Nearest upsample as a row gather of 16-byte pieces (a copy: any dtype).
+__global__ void __launch_bounds__(256)
+upsample16_kernel(const uint4 *coarse, int64_t nc, int32_t ppr, const int32_t *f2c, int32_t count,
+                  uint4 *y) {
+    for (int32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < count; i += gridDim.x * blockDim.x) {
+        const int32_t r = i / ppr, pc = i - r * ppr;
+        const int32_t src = f2c[r];
+        y[i] = src >= 0 && src < nc ? coarse[static_cast<int64_t>(src) * ppr + pc] : make_uint4(0u, 0u, 0u, 0u);
+    }
+}
+
 template <class TI, class TO>
 __global__ void __launch_bounds__(256) convert_kernel(const void *x, int64_t count, void *y) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
@@ -454,10 +507,21 @@ S3DX_API s3dx_status s3dx_downsample_mean(const void *x, int32_t dtype, int64_t 
         require(nf > 0 && nc > 0 && c > 0, "sizes must be positive");
         require_dtype(dtype);
         const hipStream_t s = as_stream(stream);
-        if (dtype == S3DX_BF16)
+        const int64_t rowb = static_cast<int64_t>(c) * dtype_size(dtype);
+        if (rowb % 16 == 0 && aligned(x, 16) && aligned(y, 16) && nc * (rowb / 16) < (int64_t(1) << 30)) {
+            const int32_t ppr = static_cast<int32_t>(rowb / 16), count = static_cast<int32_t>(nc * ppr);
+            const uint4 *xv = static_cast<const uint4 *>(x);
+            if (dtype == S3DX_BF16)
+                downsample16_kernel<uint16_t><<<grid_for(count), 256, 0, s>>>(xv, nf, ppr, children, inv_count, count,
+                                                                             static_cast<uint4 *>(y));
+            else
+                downsample16_kernel<float><<<grid_for(count), 256, 0, s>>>(xv, nf, ppr, children, inv_count, count,
+                                                                          static_cast<uint4 *>(y));
+        } else if (dtype == S3DX_BF16) {
             downsample_kernel<uint16_t><<<grid_for(nc * c), 256, 0, s>>>(x, nf, c, children, inv_count, nc, y);
-        else
+        } else {
             downsample_kernel<float><<<grid_for(nc * c), 256, 0, s>>>(x, nf, c, children, inv_count, nc, y);
+        }
         launch_check("downsample");
     });
 }
@@ -471,10 +535,16 @@ S3DX_API s3dx_status s3dx_upsample_nearest(const void *coarse, int32_t dtype, in
         require(nf > 0 && nc > 0 && c > 0, "sizes must be positive");
         require_dtype(dtype);
         const hipStream_t s = as_stream(stream);
-        if (dtype == S3DX_BF16)
+        const int64_t rowb = static_cast<int64_t>(c) * dtype_size(dtype);
+        if (rowb % 16 == 0 && aligned(coarse, 16) && aligned(y, 16) && nf * (rowb / 16) < (int64_t(1) << 30)) {
+            const int32_t ppr = static_cast<int32_t>(rowb / 16), count = static_cast<int32_t>(nf * ppr);
+            upsample16_kernel<<<grid_for(count), 256, 0, s>>>(static_cast<const uint4 *>(coarse), nc, ppr,
+                                                             fine_to_coarse, count, static_cast<uint4 *>(y));
+        } else if (dtype == S3DX_BF16) {
             upsample_kernel<uint16_t><<<grid_for(nf * c), 256, 0, s>>>(coarse, nc, c, fine_to_coarse, nf, y);
-        else
+        } else {
             upsample_kernel<float><<<grid_for(nf * c), 256, 0, s>>>(coarse, nc, c, fine_to_coarse, nf, y);
+        }
         launch_check("upsample");
     });
 }

@@ -61,20 +61,29 @@ def test_groupnorm_stats_bf16_input(s3dx, O, W, n, c):
     assert rel_l2(y.download(), ref) <= 1e-5
 
 
-def test_down_up_sample(s3dx, O, W):
+@pytest.mark.parametrize("dtype,c", [(0, 64), (1, 64), (1, 128), (0, 20), (1, 20), (0, 6)])
+def test_down_up_sample(s3dx, O, W, dtype, c):
+    # Rows of whole 16-byte pieces take the vector path (FP32 64/20, BF16
+    # 64/128), the others one element per thread.  Children are summed in
+    # order in FP32, as the oracle does: results are bit-identical (BF16 after
+    # one rounding of the oracle's FP32 value).
     coords = W.shells_union(0)
     n = coords.shape[0]
     nc, cc, f2c, ch, inv = s3dx.coarsen2(dev(s3dx, coords), n)
-    c = 64
+    print(f"down/up dtype={dtype} c={c} n={n} nc={nc}", flush=True)
     x = W.normal_f32(13, 1, (n, c))
-    dx = dev(s3dx, x)
-    down = s3dx.DeviceArray((nc, c), np.float32)
-    s3dx.downsample_mean(dx, s3dx.F32, n, c, ch, inv, nc, down)
-    ref = O.downsample_mean(x, ch.download()[: 8 * nc], inv.download()[:nc], nc)
-    assert rel_l2(down.download(), ref) <= 1e-6
-    up = s3dx.DeviceArray((n, c), np.float32)
-    s3dx.upsample_nearest(down, s3dx.F32, nc, c, f2c, n, up)
-    assert np.array_equal(up.download(), O.upsample_nearest(down.download(), f2c.download()))
+    bf = dtype == s3dx.BF16
+    xr = W.round_bf16(x) if bf else x
+    dx = dev(s3dx, W.f32_to_bf16_bits(x) if bf else x)
+    store = np.uint16 if bf else np.float32
+    host = (lambda d: W.bf16_bits_to_f32(d.download())) if bf else (lambda d: d.download())
+    down = s3dx.DeviceArray((nc, c), store)
+    s3dx.downsample_mean(dx, dtype, n, c, ch, inv, nc, down)
+    ref = O.downsample_mean(xr, ch.download()[: 8 * nc], inv.download()[:nc], nc)
+    assert np.array_equal(host(down), W.round_bf16(ref) if bf else ref)
+    up = s3dx.DeviceArray((n, c), store)
+    s3dx.upsample_nearest(down, dtype, nc, c, f2c, n, up)
+    assert np.array_equal(host(up), O.upsample_nearest(host(down), f2c.download()))
 
 
 @pytest.mark.parametrize("count", [4096, 4099, 13, 40_000_003])
