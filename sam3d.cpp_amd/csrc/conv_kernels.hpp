@@ -786,13 +786,17 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_splitk_kernel(ConvA
         uint32_t rest;
         int o, kc;
     };
+    // Offsets are below 27, so bit 31 of the mask is never set: `more` comes
+    // from the ctz (testing rest itself next to rest - 1 makes the compiler
+    // use a vector subtract and a readfirstlane, ~20 cycles per task).
     auto advance = [&](Cursor &c) __attribute__((always_inline)) {
         const bool wrap = c.kc + 1 == chunks;
-        const bool more = c.rest != 0u;
         const int next_o = __builtin_ctz(c.rest | 0x80000000u);
+        const bool more = next_o != 31;
+        const uint32_t cleared = c.rest & (c.rest - 1u);
         c.o = wrap && more ? next_o : c.o;
         c.kc = wrap ? (more ? 0 : c.kc) : c.kc + 1;
-        c.rest = wrap && more ? (c.rest & (c.rest - 1u)) : c.rest;
+        c.rest = wrap && more ? cleared : c.rest;
     };
     static_assert(SUB <= 4, "four 16-bit sub-task fields");
     struct Task {
@@ -830,6 +834,14 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_splitk_kernel(ConvA
     // keeps column block (k + w) mod 4 in accumulator k, so the block it owns
     // in the final reduction is always accumulator 0.
     constexpr bool ROT = NB == 4;
+    // With one k-step per wave per task, the column block (rotated for ROT)
+    // goes into a per-lane offset computed once: no scalar work per load.
+    // With more, those registers would add spills: it goes into the scalar
+    // offset (rotated) or the immediate.
+    constexpr bool BVO = KSW == 1;
+    int32_t bvo[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) bvo[nb] = lane * 16 + (ROT ? ((nb + wave) & 3) : nb) * 1024;
     auto load_b = [&](const Task &t, uint4 (&bf)[KSW][NB]) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < KSW; ++i) {
@@ -841,10 +853,10 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_splitk_kernel(ConvA
             if constexpr (SUB > 1) sbase = sub < t.left ? sbase : static_cast<int32_t>(0xC0000000u);
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
-                // the column block goes into the scalar offset (rotated) or the immediate
-                const u32x4 v = ROT ? __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, lane * 16,
-                                                                            sbase + ((nb + wave) & 3) * 1024, 0)
-                                    : __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, lane * 16 + nb * 1024, sbase, 0);
+                const u32x4 v =
+                    BVO ? __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, bvo[nb], sbase, 0)
+                    : ROT ? __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, lane * 16, sbase + ((nb + wave) & 3) * 1024, 0)
+                          : __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, lane * 16 + nb * 1024, sbase, 0);
                 bf[i][nb] = make_uint4(v.x, v.y, v.z, v.w);
             }
         }
