@@ -861,19 +861,40 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_splitk_kernel(ConvA
             }
         }
     };
-    // Row-major gather: piece u = tid + 256 q is row u / PPR, channels
-    // kc*KC + (u % PPR)*E .. +E.  The staged map holds, per (row, offset),
-    // the neighbour's byte offset in x (plain gathers; out of range when
-    // missing, which the buffer load answers with zeros) or its row index
-    // (64-bit gathers; -1 when missing), at a fixed stride of 27.
+    // Row-major gather: piece u = tid + 256 q is row u / PPR = tid / PPR +
+    // q * RS, channels kc*KC + (u % PPR)*E .. +E.  The staged map holds, per
+    // (row, offset), the neighbour's byte offset in x (plain gathers; out of
+    // range when missing, which the buffer load answers with zeros) or its
+    // row index (64-bit gathers; -1 when missing), laid out [offset][row %
+    // RS][row / RS] so that a thread's APT rows of an offset are one vector
+    // read.
+    constexpr int RS = 256 / PPR;  // rows apart of a thread's pieces
+    static_assert(RS * APT == BM, "a thread's pieces cover one row per RS rows");
+    auto map_slot = [&](int r, int o) __attribute__((always_inline)) { return (o * RS + r % RS) * APT + r / RS; };
     constexpr int32_t kNoRow = XF == 0 ? static_cast<int32_t>(0x80000000u) : -1;
     auto rows_of = [&](const Task &t, int32_t (&jn)[APT]) __attribute__((always_inline)) {
         const int o = sub_o(t, my_sub);
+        const int32_t *src = rows + (o * RS + tid / PPR) * APT;
+        if constexpr (APT % 4 == 0) {
 #pragma unroll
-        for (int q = 0; q < APT; ++q) {
-            jn[q] = rows[((tid + q * 256) / PPR) * kMaxKvol + o];
-            if constexpr (SUB > 1) jn[q] = my_sub < t.left ? jn[q] : kNoRow;
+            for (int q4 = 0; q4 < APT / 4; ++q4) {
+                const int4 v = reinterpret_cast<const int4 *>(src)[q4];
+                jn[4 * q4] = v.x;
+                jn[4 * q4 + 1] = v.y;
+                jn[4 * q4 + 2] = v.z;
+                jn[4 * q4 + 3] = v.w;
+            }
+        } else if constexpr (APT == 2) {
+            const int2 v = *reinterpret_cast<const int2 *>(src);
+            jn[0] = v.x;
+            jn[1] = v.y;
+        } else {
+#pragma unroll
+            for (int q = 0; q < APT; ++q) jn[q] = src[q];
         }
+#pragma unroll
+        for (int q = 0; q < APT; ++q)
+            if constexpr (SUB > 1) jn[q] = my_sub < t.left ? jn[q] : kNoRow;
     };
     auto gather = [&](const Task &t, int32_t j, int q) __attribute__((always_inline)) {
         const int piece = (tid + q * 256) % PPR;
@@ -1036,7 +1057,8 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_splitk_kernel(ConvA
                 const int e = e0 + k;
                 if (e >= BM * kvol) continue;
                 const bool valid = e < count && jv[k] >= 0 && jv[k] < a.n_src;
-                rows[kvol == kMaxKvol ? e : e * kMaxKvol] = staged(valid, jv[k]);
+                const int r = kvol == kMaxKvol ? e / kMaxKvol : e;
+                rows[map_slot(r, kvol == kMaxKvol ? e - r * kMaxKvol : 0)] = staged(valid, jv[k]);
                 const int o = kvol == kMaxKvol ? e % kMaxKvol : 0;
                 if (valid) my_mask |= 1u << o;
             }
@@ -1045,7 +1067,7 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_splitk_kernel(ConvA
         for (int r = tid; r < BM; r += 256) {
             const int64_t j = m0 + r;
             const bool valid = r < tile_rows && j < a.n_src;
-            rows[r * kMaxKvol] = staged(valid, static_cast<int32_t>(j));
+            rows[map_slot(r, 0)] = staged(valid, static_cast<int32_t>(j));
             if (valid) my_mask = 1u;
         }
     }
