@@ -261,30 +261,50 @@ def kmap_subm3(coords: DeviceArray, n: int, missing: int, kmap: DeviceArray = No
     return kmap
 
 
-def subdivide2(parents: DeviceArray, p: int, with_kmap: bool = True, stream=None):
-    """MeshSubdivideTables::build (sparse_ops.cpp:272-404): (child_coords, child_kmap)."""
+def subdivide2_workspace_size(p: int) -> int:
     b = _u64(0)
     call("s3dx_subdivide2_workspace_size", _i64(p), C.byref(b))
-    ws = DeviceArray(int(b.value), np.uint8)
-    child = DeviceArray((8 * p, 4), np.int32)
-    kmap = DeviceArray((8 * p, 27), np.int32) if with_kmap else None
+    return int(b.value)
+
+
+def subdivide2(parents: DeviceArray, p: int, with_kmap: bool = True, stream=None, out=None,
+               workspace: DeviceArray = None):
+    """MeshSubdivideTables::build (sparse_ops.cpp:272-404): (child_coords, child_kmap).
+    out = (child [8p, 4], kmap [8p, 27] or None) and workspace may be passed in to
+    reuse them across calls."""
+    ws = workspace if workspace is not None else DeviceArray(subdivide2_workspace_size(p), np.uint8)
+    if out is not None:
+        child, kmap = out
+        kmap = kmap if with_kmap else None
+    else:
+        child = DeviceArray((8 * p, 4), np.int32)
+        kmap = DeviceArray((8 * p, 27), np.int32) if with_kmap else None
     call("s3dx_subdivide2", _dptr(parents), _i64(p), _dptr(child), _dptr(kmap), _dptr(ws),
          _u64(ws.nbytes), _sptr(stream))
     return child, kmap
 
 
-def coarsen2(coords: DeviceArray, n: int, stream=None):
+def coarsen2_workspace_size(n: int) -> int:
+    b = _u64(0)
+    call("s3dx_coarsen2_workspace_size", _i64(n), C.byref(b))
+    return int(b.value)
+
+
+def coarsen2(coords: DeviceArray, n: int, stream=None, out=None, workspace: DeviceArray = None):
     """SlatTables downsample tables (sparse_ops.cpp:53-104).
 
     Returns (nc, coarse_coords [n,4], fine_to_coarse [n], children [8n], inv_count [n]);
-    only the first nc (8*nc) rows of the coarse outputs are meaningful."""
-    b = _u64(0)
-    call("s3dx_coarsen2_workspace_size", _i64(n), C.byref(b))
-    ws = DeviceArray(int(b.value), np.uint8)
-    cc = DeviceArray((n, 4), np.int32)
-    f2c = DeviceArray((n,), np.int32)
-    ch = DeviceArray((8 * n,), np.int32)
-    inv = DeviceArray((n,), np.float32)
+    only the first nc (8*nc) rows of the coarse outputs are meaningful.  out =
+    (coarse_coords, fine_to_coarse, children, inv_count) and workspace may be
+    passed in to reuse them across calls."""
+    ws = workspace if workspace is not None else DeviceArray(coarsen2_workspace_size(n), np.uint8)
+    if out is not None:
+        cc, f2c, ch, inv = out
+    else:
+        cc = DeviceArray((n, 4), np.int32)
+        f2c = DeviceArray((n,), np.int32)
+        ch = DeviceArray((8 * n,), np.int32)
+        inv = DeviceArray((n,), np.float32)
     nc = _i64(0)
     call("s3dx_coarsen2", _dptr(coords), _i64(n), _dptr(cc), _dptr(f2c), _dptr(ch), _dptr(inv),
          C.byref(nc), _dptr(ws), _u64(ws.nbytes), _sptr(stream))

@@ -123,3 +123,31 @@ def test_two_level_subdivide_properties(s3dx, W):
         assert np.all(d == np.array([o // 9 - 1, (o // 3) % 3 - 1, o % 3 - 1]))
     # the subdivided map equals a from-scratch kernel map over the children
     assert np.array_equal(s3dx.kmap_subm3(t1.child_coords, n1, -1).download(), k)
+
+
+def test_coarsen_subdivide_reused_buffers(s3dx, W):
+    # Two calls into the same caller-owned outputs and workspace, the second
+    # on a smaller set: each result equals a fresh call's, byte for byte, in
+    # the meaningful rows (nothing is left over from the first call).
+    big, small = W.shells_union(0), W.shells_union(1)[:5000]
+    n = big.shape[0]
+    c_out = (s3dx.DeviceArray((n, 4), np.int32), s3dx.DeviceArray((n,), np.int32),
+             s3dx.DeviceArray((8 * n,), np.int32), s3dx.DeviceArray((n,), np.float32))
+    c_ws = s3dx.DeviceArray(s3dx.coarsen2_workspace_size(n), np.uint8)
+    s_out = (s3dx.DeviceArray((8 * n, 4), np.int32), s3dx.DeviceArray((8 * n, 27), np.int32))
+    s_ws = s3dx.DeviceArray(s3dx.subdivide2_workspace_size(n), np.uint8)
+    for coords in (big, small):
+        m = coords.shape[0]
+        d = s3dx.DeviceArray.from_host(coords)
+        print(f"reused buffers n={m}", flush=True)
+        nc, cc, f2c, ch, inv = s3dx.coarsen2(d, m, out=c_out, workspace=c_ws)
+        nc2, cc2, f2c2, ch2, inv2 = s3dx.coarsen2(d, m)
+        assert nc == nc2
+        assert np.array_equal(cc.download()[:nc], cc2.download()[:nc])
+        assert np.array_equal(f2c.download()[:m], f2c2.download()[:m])
+        assert np.array_equal(ch.download()[: 8 * nc], ch2.download()[: 8 * nc])
+        assert np.array_equal(inv.download()[:nc], inv2.download()[:nc])
+        child, kmap = s3dx.subdivide2(d, m, True, out=s_out, workspace=s_ws)
+        child2, kmap2 = s3dx.subdivide2(d, m, True)
+        assert np.array_equal(child.download()[: 8 * m], child2.download())
+        assert np.array_equal(kmap.download()[: 8 * m], kmap2.download())
