@@ -277,13 +277,13 @@ def mesh_stack(s3dx, W, stream, seed, d0, p0, ch0, k0):
     run0()
     ch1, k1 = s3dx.subdivide2(ch0, n0, True, stream)
     run1, y1, n1 = block(1, y0, n0, k1, 192, 96)
-    head = s3dx.SparseConv(96, 101, 1, f32).set_weights(W.conv_weight(seed, 590, 96, 101, kvol=1), s3dx.WEIGHT_SLAT, None)
-    y1f = s3dx.DeviceArray((n1, 96), np.float32)
+    # FP32 head fed the BF16 block output directly (rows widened exactly in the kernel)
+    head = (s3dx.SparseConv(96, 101, 1, f32).set_weights(W.conv_weight(seed, 590, 96, 101, kvol=1), s3dx.WEIGHT_SLAT, None)
+            .set_input_dtype(bf))
     out = s3dx.DeviceArray((n1, 101), np.float32)
 
     def run_head():
-        s3dx.convert(y1, bf, n1 * 96, y1f, f32, stream)
-        head.run(y1f, n1, None, n1, out, f32, None, stream)
+        head.run(y1, n1, None, n1, out, f32, None, stream)
 
     stages["level0_block_us"] = _event_us(s3dx, stream, run0, reps=5)
     stages["level1_block_us"] = _event_us(s3dx, stream, run1, reps=5)

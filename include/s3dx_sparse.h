@@ -253,7 +253,16 @@ S3DX_API s3dx_status s3dx_conv_set_silu(s3dx_conv *conv, int32_t enable, char *e
  * and let the block's second conv add it this way. */
 S3DX_API s3dx_status s3dx_conv_set_residual_parent(s3dx_conv *conv, int32_t enable, char *error,
                                                    uint64_t error_capacity);
-/* Runs the layer.  x [n_in or n_in parents][cin] in the conv's dtype; kmap
+/* Input dtype of the layer's x: its own dtype (the default), or S3DX_BF16
+ * for an S3DX_F32 layer.  No counterpart as a call: the reference's graph
+ * feeds F32 tensors throughout; this lets a BF16 producer feed an FP32 layer
+ * (the mesh head, mesh_decoder_graph.cpp:134-140) without a separate
+ * conversion pass.  The rows are widened exactly: 1x1 layers read them
+ * in the kernel, others widen them once into the layer's buffer (same rule
+ * as the transforms).  Not combinable with input transforms. */
+S3DX_API s3dx_status s3dx_conv_set_input_dtype(s3dx_conv *conv, int32_t dtype, char *error,
+                                               uint64_t error_capacity);
+/* Runs the layer.  x [n_in or n_in parents][cin] in the layer's input dtype; kmap
  * [n_out][kvol] (NULL only for kvol 1); residual [n_out][cout] in y_dtype or
  * NULL; y [n_out][cout] in y_dtype.  Asynchronous on `stream`. */
 S3DX_API s3dx_status s3dx_conv_run(const s3dx_conv *conv, const void *x, int64_t n_in,

@@ -79,6 +79,7 @@ SIGNATURES = {
     "s3dx_conv_set_layernorm": (_u32, [_vp, _i32, _f32, _vp, _vp, _vp, _vp], True),
     "s3dx_conv_set_silu": (_u32, [_vp, _i32], True),
     "s3dx_conv_set_residual_parent": (_u32, [_vp, _i32], True),
+    "s3dx_conv_set_input_dtype": (_u32, [_vp, _i32], True),
     "s3dx_conv_run": (_u32, [_vp, _vp, _i64, _vp, _i64, _vp, _vp, _i32, _vp], True),
     "s3dx_conv_plan": (_u32, [_vp, _i64, _i64, C.c_char_p, _u64], True),
     "s3dx_layernorm_rows": (_u32, [_vp, _i32, _i64, _i32, _f32, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp], True),
@@ -467,6 +468,11 @@ class SparseConv:
     def set_residual_parent(self, enable: bool = True):
         """Residual of one row per parent: output row i adds residual row i >> 3."""
         call("s3dx_conv_set_residual_parent", _vp(self.handle), _i32(int(enable)))
+        return self
+
+    def set_input_dtype(self, dtype: int):
+        """x in `dtype`: the layer's own, or BF16 rows for an FP32 layer (widened exactly)."""
+        call("s3dx_conv_set_input_dtype", _vp(self.handle), _i32(dtype))
         return self
 
     def plan(self, n_in: int, n_out: int) -> str:

@@ -255,6 +255,8 @@ void layernorm_rows_launch(const void *x, int32_t x_dtype, int64_t n, int32_t c,
                            hipStream_t stream);
 void add_rows_launch(const void *a, const void *b, int32_t dtype, int64_t n, int32_t c,
                      int32_t b_shift, void *y, hipStream_t stream);
+void convert_launch(const void *x, int32_t x_dtype, int64_t count, void *y, int32_t y_dtype,
+                    hipStream_t stream);
 
 }  // namespace s3dx
 
@@ -263,6 +265,7 @@ void add_rows_launch(const void *a, const void *b, int32_t dtype, int64_t n, int
 // ---------------------------------------------------------------------------
 struct s3dx_conv {
     int32_t cin = 0, cout = 0, kvol = 0, dtype = 0;
+    int32_t in_dtype = 0;  // dtype of x: the layer's, or BF16 rows into an FP32 layer
     int32_t cout_pad = 0;  // packed MFMA weight columns (whole 32-column blocks)
     bool mfma = false;
     int nb = 0, kc = 0;  // MFMA tiling
@@ -404,7 +407,10 @@ Source source_of(const s3dx_conv *conv, int64_t n_in) {
     return src;
 }
 
-LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bool aligned16) {
+// bf16_rows: x holds BF16 rows for an FP32 layer; only the linear kernel
+// reads them as they are (the caller converts them for any other plan).
+LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bool aligned16,
+                       bool bf16_rows = false) {
     LaunchPlan p;
     const bool bf = conv->dtype == S3DX_BF16;
     p.mfma = conv->mfma && aligned16;
@@ -412,7 +418,7 @@ LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bo
         // 1x1 layer: every weight fragment fits in LDS -> the linear kernel.
         const int nbt = conv->cout_pad / 32;
         const int frags = conv->cin / (bf ? 16 : 8) * nbt * 64;
-        KernelFn fn = bf ? pick_linear_bf16(nbt) : pick_linear_f32(nbt);
+        KernelFn fn = bf ? pick_linear_bf16(nbt) : bf16_rows ? pick_linear_f32_bf16_rows(nbt) : pick_linear_f32(nbt);
         if (fn && frags <= kLinearMaxFrags && !std::getenv("S3DX_CONV_TILING")) {
             p.linear = true;
             p.fn = fn;
@@ -581,6 +587,7 @@ S3DX_API s3dx_status s3dx_conv_create(int32_t cin, int32_t cout, int32_t kvol, i
         c->cout = cout;
         c->kvol = kvol;
         c->dtype = dtype;
+        c->in_dtype = dtype;
         const bool bf = dtype == S3DX_BF16;
         // Column blocks per workgroup: the whole row when Cout <= 256 (so a
         // LayerNorm epilogue sees it), else 128-column tiles.  A Cout that
@@ -724,6 +731,17 @@ S3DX_API s3dx_status s3dx_conv_set_residual_parent(s3dx_conv *conv, int32_t enab
     });
 }
 
+S3DX_API s3dx_status s3dx_conv_set_input_dtype(s3dx_conv *conv, int32_t dtype, char *error,
+                                              uint64_t error_capacity) {
+    return boundary(error, error_capacity, [&] {
+        require(conv != nullptr, "conv is NULL");
+        require_dtype(dtype);
+        require(dtype == conv->dtype || (dtype == S3DX_BF16 && conv->dtype == S3DX_F32),
+                "input dtype must be the layer's, or BF16 for an FP32 layer");
+        conv->in_dtype = dtype;
+    });
+}
+
 S3DX_API s3dx_status s3dx_conv_plan(const s3dx_conv *conv, int64_t n_in, int64_t n_out, char *plan,
                                     uint64_t plan_capacity, char *error, uint64_t error_capacity) {
     return boundary(error, error_capacity, [&] {
@@ -731,8 +749,11 @@ S3DX_API s3dx_status s3dx_conv_plan(const s3dx_conv *conv, int64_t n_in, int64_t
         require(plan != nullptr && plan_capacity > 0, "plan buffer is empty");
         require(n_in > 0 && n_out > 0, "row counts must be positive");
         const Source src = source_of(conv, n_in);
-        const int64_t x_bytes = src.rows * conv->cin * static_cast<int64_t>(dtype_size(conv->dtype));
-        const LaunchPlan p = plan_launch(conv, x_bytes, n_out, true);
+        const bool bf16_rows = conv->in_dtype != conv->dtype;
+        const int64_t x_bytes = src.rows * conv->cin * static_cast<int64_t>(dtype_size(conv->in_dtype));
+        LaunchPlan p = plan_launch(conv, x_bytes, n_out, true, bf16_rows);
+        const bool widen = bf16_rows && !p.linear;
+        if (widen) p = plan_launch(conv, src.rows * conv->cin * 4, n_out, true);
         char text[256];
         if (p.linear)
             std::snprintf(text, sizeof(text), "linear cols=%d ksteps=%d ln=%s grid=%u", p.nb * 32,
@@ -746,8 +767,9 @@ S3DX_API s3dx_status s3dx_conv_plan(const s3dx_conv *conv, int64_t n_in, int64_t
         else
             std::snprintf(text, sizeof(text), "generic rows=%d cols=%d ln=%s grid=%ux%u", kGM, kGN,
                           conv->ln ? "separate" : "none", p.grid.x, p.grid.y);
-        std::snprintf(plan, plan_capacity, "%s%s%s", src.pre ? (src.children ? "pre=children " : "pre=rows ") : "",
-                      src.shift ? "parent-rows " : "", text);
+        std::snprintf(plan, plan_capacity, "%s%s%s%s", bf16_rows ? (widen ? "in=bf16 pre=widen " : "in=bf16 ") : "",
+                      src.pre ? (src.children ? "pre=children " : "pre=rows ") : "", src.shift ? "parent-rows " : "",
+                      text);
     });
 }
 
@@ -768,7 +790,9 @@ S3DX_API s3dx_status s3dx_conv_run(const s3dx_conv *conv, const void *x, int64_t
         require(src.n_src <= INT32_MAX, "input rows exceed INT32_MAX");
         const hipStream_t s = as_stream(stream);
         const bool bf = conv->dtype == S3DX_BF16;
-        const int64_t x_bytes = src.rows * conv->cin * static_cast<int64_t>(dtype_size(conv->dtype));
+        const bool bf16_rows = conv->in_dtype != conv->dtype;  // BF16 rows into an FP32 layer
+        require(!(bf16_rows && src.pre), "BF16 input rows do not combine with input transforms");
+        const int64_t x_bytes = src.rows * conv->cin * static_cast<int64_t>(dtype_size(conv->in_dtype));
         if (src.pre) {
             XformArgs xa{};
             xa.x = x;
@@ -819,8 +843,18 @@ S3DX_API s3dx_status s3dx_conv_run(const s3dx_conv *conv, const void *x, int64_t
         a.mod_scale = conv->mod_scale;
         a.mod_shift = conv->mod_shift;
         // The MFMA kernel reads the map and writes rows with 16-byte accesses.
-        const LaunchPlan plan = plan_launch(conv, a.x_bytes, n_out,
-                                            aligned(kmap, 16) && aligned(y, 16) && aligned(residual, 16));
+        const bool aligned16 = aligned(kmap, 16) && aligned(y, 16) && aligned(residual, 16);
+        LaunchPlan plan = plan_launch(conv, a.x_bytes, n_out, aligned16, bf16_rows);
+        if (bf16_rows && !plan.linear) {
+            // Other kernels read the layer's dtype: the rows are widened
+            // (exactly) once, into the layer's buffer.
+            const int64_t count = src.rows * conv->cin;
+            void *xw = transform_buffer(conv, count * 4, s);
+            convert_launch(x, S3DX_BF16, count, xw, S3DX_F32, s);
+            a.x = xw;
+            a.x_bytes = count * 4;
+            plan = plan_launch(conv, a.x_bytes, n_out, aligned16);
+        }
         if (plan.mfma) {
             a.ln = plan.fused_ln;
             if (conv->ln && !plan.fused_ln) {  // LayerNorm as a separate pass

@@ -14,4 +14,6 @@ KernelFn pick_mfma_f32(int id, int kc, bool xf) {
 
 KernelFn pick_linear_f32(int nbt) { return pick_linear<float>(nbt); }
 
+KernelFn pick_linear_f32_bf16_rows(int nbt) { return pick_linear<float, true>(nbt); }
+
 }  // namespace s3dx

@@ -63,6 +63,8 @@ KernelFn pick_mfma_f32(int id, int kc, bool xf);
 // 1x1-layer kernel for nbt 32-column blocks (1, 2, 3, 4, 6, 8), else nullptr.
 KernelFn pick_linear_bf16(int nbt);
 KernelFn pick_linear_f32(int nbt);
+// The FP32 1x1-layer kernel reading BF16 rows, else nullptr.
+KernelFn pick_linear_f32_bf16_rows(int nbt);
 
 namespace {
 
@@ -1246,11 +1248,14 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_splitk_kernel(ConvA
 // weight fragments.
 constexpr int kLinearMaxFrags = 4096;  // 64 KiB of LDS
 
-template <class T, int NBT>
+// XB (FP32 layers only): x holds BF16 rows, widened exactly as each A
+// fragment is loaded (8 bytes per lane instead of 16).
+template <class T, int NBT, bool XB = false>
 __global__ void __launch_bounds__(256) linear_kernel(ConvArgs a) {
+    static_assert(!XB || sizeof(T) == 4, "BF16 rows feed FP32 layers only");
     extern __shared__ uint4 wl[];
     constexpr int E = Frag<T>::E, CPK = 2 * E;
-    constexpr int ES = static_cast<int>(sizeof(T));
+    constexpr int ES = XB ? 2 : static_cast<int>(sizeof(T));  // bytes per x element
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5;
     const int ks_total = a.cin / CPK;
     const uint4 *wg = static_cast<const uint4 *>(a.w);
@@ -1276,9 +1281,15 @@ __global__ void __launch_bounds__(256) linear_kernel(ConvArgs a) {
                                   ? static_cast<uint32_t>(((r >> a.row_shift) * a.cin + half * E) * ES)
                                   : 0x80000000u;
         auto load_a = [&](int st) __attribute__((always_inline)) {
-            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
-                x_rsrc, static_cast<int32_t>(base + static_cast<uint32_t>(st * CPK * ES)), 0, 0);
-            return make_uint4(v.x, v.y, v.z, v.w);
+            const int32_t off = static_cast<int32_t>(base + static_cast<uint32_t>(st * CPK * ES));
+            if constexpr (XB) {
+                typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+                const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(x_rsrc, off, 0, 0);
+                return make_uint4(v.x << 16, v.x & 0xffff0000u, v.y << 16, v.y & 0xffff0000u);
+            } else {
+                const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, off, 0, 0);
+                return make_uint4(v.x, v.y, v.z, v.w);
+            }
         };
         f32x16 acc[NBT];
 #pragma unroll
@@ -1362,15 +1373,15 @@ __global__ void __launch_bounds__(256) linear_kernel(ConvArgs a) {
     }
 }
 
-template <class T>
+template <class T, bool XB = false>
 KernelFn pick_linear(int nbt) {
     switch (nbt) {
-    case 1: return linear_kernel<T, 1>;
-    case 2: return linear_kernel<T, 2>;
-    case 3: return linear_kernel<T, 3>;
-    case 4: return linear_kernel<T, 4>;
-    case 6: return linear_kernel<T, 6>;
-    case 8: return linear_kernel<T, 8>;
+    case 1: return linear_kernel<T, 1, XB>;
+    case 2: return linear_kernel<T, 2, XB>;
+    case 3: return linear_kernel<T, 3, XB>;
+    case 4: return linear_kernel<T, 4, XB>;
+    case 6: return linear_kernel<T, 6, XB>;
+    case 8: return linear_kernel<T, 8, XB>;
     default: return nullptr;
     }
 }

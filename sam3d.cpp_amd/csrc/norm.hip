@@ -409,6 +409,15 @@ void add_rows_launch(const void *a, const void *b, int32_t dtype, int64_t n, int
     launch_check("add");
 }
 
+void convert_launch(const void *x, int32_t x_dtype, int64_t count, void *y, int32_t y_dtype,
+                    hipStream_t stream) {
+    if (x != y && aligned(x, 16) && aligned(y, 16))
+        S3DX_DISPATCH2(x_dtype, y_dtype, convert8_kernel, <<<grid_for((count + 7) / 8), 256, 0, stream>>>(x, count, y));
+    else
+        S3DX_DISPATCH2(x_dtype, y_dtype, convert_kernel, <<<grid_for(count), 256, 0, stream>>>(x, count, y));
+    launch_check("convert");
+}
+
 }  // namespace s3dx
 
 using namespace s3dx;
@@ -558,13 +567,7 @@ S3DX_API s3dx_status s3dx_convert(const void *x, int32_t x_dtype, int64_t count,
         require_dtype(x_dtype);
         require_dtype(y_dtype);
         require(x != y || x_dtype == y_dtype, "in-place conversion needs equal dtypes");
-        if (x != y && aligned(x, 16) && aligned(y, 16))
-            S3DX_DISPATCH2(x_dtype, y_dtype, convert8_kernel,
-                           <<<grid_for((count + 7) / 8), 256, 0, as_stream(stream)>>>(x, count, y));
-        else
-            S3DX_DISPATCH2(x_dtype, y_dtype, convert_kernel,
-                           <<<grid_for(count), 256, 0, as_stream(stream)>>>(x, count, y));
-        launch_check("convert");
+        convert_launch(x, x_dtype, count, y, y_dtype, as_stream(stream));
     });
 }
 

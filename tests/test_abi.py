@@ -122,6 +122,13 @@ def test_conv_plan_names_the_launched_kernel(s3dx, monkeypatch):
     # The parent repeat alone is a shift of the staged rows, no pre-pass.
     skip = s3dx.SparseConv(192, 192, 1, s3dx.BF16).set_gather_parent(True)
     assert skip.plan(n, 8 * n).startswith("parent-rows mfma tiling=")
+    # BF16 rows into FP32 layers: the head reads them in its kernel; a
+    # 27-offset layer widens them first.  Other combinations are refused.
+    head = s3dx.SparseConv(96, 101, 1, s3dx.F32).set_input_dtype(s3dx.BF16)
+    assert head.plan(8 * n, 8 * n).startswith("in=bf16 linear cols=128")
+    assert s3dx.SparseConv(64, 64, 27, s3dx.F32).set_input_dtype(s3dx.BF16).plan(n, n).startswith("in=bf16 pre=widen mfma")
+    with pytest.raises(s3dx.S3dxError, match="input dtype"):
+        s3dx.SparseConv(64, 64, 27, s3dx.BF16).set_input_dtype(s3dx.F32)
     monkeypatch.setenv("S3DX_CONV_TILING", "10")
     assert c128.plan(n, n).startswith("mfma tiling=10 rows=128 cols=128")
     with pytest.raises(s3dx.S3dxError):

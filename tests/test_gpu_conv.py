@@ -394,3 +394,30 @@ def test_centre_column_not_identity(s3dx, O, W, dtype):
         got = gpu_conv(s3dx, x, kmap, n, w, s3dx.WEIGHT_SLAT, b, dtype, 128)
         ref = O.conv(rnd(s3dx, x, dtype), kmap, n, rnd(s3dx, w, dtype), 0, 128, b)
         assert rel_l2(got, ref) <= TOL[dtype], name
+
+
+@pytest.mark.parametrize("cin,cout,kvol,n,plan", [
+    (96, 101, 1, 300001, "in=bf16 linear"),   # the mesh head's shape, > 2 passes of the persistent grid
+    (128, 96, 1, 4099, "in=bf16 linear"),
+    (64, 64, 27, None, "in=bf16 pre=widen mfma"),
+])
+def test_bf16_rows_into_fp32_layer(s3dx, O, W, cin, cout, kvol, n, plan):
+    # BF16 rows feeding an FP32 layer: bit-identical to widening them first
+    # (exact) and running the same FP32 layer on FP32 rows.
+    coords = W.shells_union(2)[:3000] if kvol == 27 else None
+    n = coords.shape[0] if kvol == 27 else n
+    kmap = O.kmap_subm3(coords, n) if kvol == 27 else None
+    xb = W.f32_to_bf16_bits(W.normal_f32(41, 1, (n, cin)))
+    w = W.conv_weight(41, 2, cin, cout, kvol=kvol)
+    b = W.normal_f32(41, 3, (cout,))
+    conv_b = s3dx.SparseConv(cin, cout, kvol, s3dx.F32).set_weights(w, s3dx.WEIGHT_SLAT, b).set_input_dtype(s3dx.BF16)
+    got_plan = conv_b.plan(n, n)
+    print(f"bf16 rows -> fp32 cin={cin} cout={cout} kvol={kvol} n={n}: {got_plan}", flush=True)
+    assert got_plan.startswith(plan), got_plan
+    conv_f = s3dx.SparseConv(cin, cout, kvol, s3dx.F32).set_weights(w, s3dx.WEIGHT_SLAT, b)
+    dk = s3dx.DeviceArray.from_host(kmap) if kmap is not None else None
+    y1 = s3dx.DeviceArray((n, cout), np.float32)
+    y2 = s3dx.DeviceArray((n, cout), np.float32)
+    conv_b.run(s3dx.DeviceArray.from_host(xb), n, dk, n, y1, s3dx.F32)
+    conv_f.run(s3dx.DeviceArray.from_host(W.bf16_bits_to_f32(xb)), n, dk, n, y2, s3dx.F32)
+    assert np.array_equal(y1.download(), y2.download())
