@@ -257,9 +257,11 @@ S3DX_API s3dx_status s3dx_conv_set_residual_parent(s3dx_conv *conv, int32_t enab
  * for an S3DX_F32 layer.  No counterpart as a call: the reference's graph
  * feeds F32 tensors throughout; this lets a BF16 producer feed an FP32 layer
  * (the mesh head, mesh_decoder_graph.cpp:134-140) without a separate
- * conversion pass.  The rows are widened exactly: 1x1 layers read them
- * in the kernel, others widen them once into the layer's buffer (same rule
- * as the transforms).  Not combinable with input transforms. */
+ * conversion pass.  The rows are exact in FP32: 1x1 layers read them in
+ * the kernel (with Cin 32, 64, 96 or 128 and Cout <= 128 on BF16 MFMAs,
+ * the FP32 weights split into three BF16 terms, at FP32 accuracy), others
+ * widen them once into the layer's buffer (same rule as the transforms).
+ * Not combinable with input transforms. */
 S3DX_API s3dx_status s3dx_conv_set_input_dtype(s3dx_conv *conv, int32_t dtype, char *error,
                                                uint64_t error_capacity);
 /* Runs the layer.  x [n_in or n_in parents][cin] in the layer's input dtype; kmap

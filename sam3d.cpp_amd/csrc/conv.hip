@@ -270,6 +270,9 @@ struct s3dx_conv {
     bool mfma = false;
     int nb = 0, kc = 0;  // MFMA tiling
     void *w = nullptr;   // packed weights (device)
+    // FP32 1x1 layers: the weights again as three BF16 terms, for BF16 input
+    // rows on BF16 MFMAs (linear_split_kernel); nullptr for other shapes.
+    void *w_split = nullptr;
     float *bias = nullptr;
     float *slot_offset = nullptr;
     bool gather_parent = false;
@@ -287,7 +290,7 @@ struct s3dx_conv {
     bool transforms() const { return slot_offset != nullptr || pre_scale != nullptr; }
 
     ~s3dx_conv() {
-        for (void *p : {w, static_cast<void *>(bias), static_cast<void *>(slot_offset),
+        for (void *p : {w, w_split, static_cast<void *>(bias), static_cast<void *>(slot_offset),
                         static_cast<void *>(ln_w), static_cast<void *>(ln_b),
                         static_cast<void *>(mod_scale), static_cast<void *>(mod_shift), xin})
             if (p) (void)hipFree(p);
@@ -346,7 +349,9 @@ struct LaunchPlan {
     bool fused_ln = false;  // LayerNorm in the MFMA epilogue
     int nb = 0, kc = 0;     // 32-column blocks per workgroup, channels per task
     bool linear = false;    // the 1x1-layer kernel (weights resident in LDS)
+    bool split = false;     // linear_split_kernel: BF16 rows, three-term BF16 weights
     unsigned smem = 0;      // dynamic LDS bytes
+    unsigned threads = 256; // workgroup size
     const Tiling *tl = nullptr;
     KernelFn fn = nullptr;
     dim3 grid;
@@ -363,14 +368,14 @@ int64_t device_cus() {
     return cus;
 }
 
-// Workgroups of 256 threads of `fn` with `smem` dynamic LDS that the device
+// Workgroups of `threads` threads of `fn` with `smem` dynamic LDS that the device
 // holds at once (at least one per CU).  Without a device (a host-only plan
 // query) it assumes 256 CUs holding two each.
-int64_t resident_blocks(KernelFn fn, unsigned smem) {
+int64_t resident_blocks(KernelFn fn, unsigned smem, int threads = 256) {
     int dev = 0, cus = 0, per_cu = 0;
     if (hipGetDevice(&dev) != hipSuccess ||
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(fn), 256, smem) !=
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void *>(fn), threads, smem) !=
             hipSuccess) {
         (void)hipGetLastError();
         return 512;
@@ -407,8 +412,16 @@ Source source_of(const s3dx_conv *conv, int64_t n_in) {
     return src;
 }
 
-// bf16_rows: x holds BF16 rows for an FP32 layer; only the linear kernel
-// reads them as they are (the caller converts them for any other plan).
+// FP32 1x1 layers with Cin = 32, 64, 96 or 128 and at most 128 output
+// columns keep their weights also as three BF16 terms (w_split): BF16 rows
+// then run on BF16 MFMAs (linear_split_kernel).
+bool has_split_terms(const s3dx_conv *conv) {
+    return conv->dtype == S3DX_F32 && conv->mfma && conv->kvol == 1 && conv->cin % 16 == 0 &&
+           pick_linear_split(conv->cout_pad / 32, conv->cin / 16) != nullptr;
+}
+
+// bf16_rows: x holds BF16 rows for an FP32 layer; only the linear kernels
+// read them as they are (the caller converts them for any other plan).
 LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bool aligned16,
                        bool bf16_rows = false) {
     LaunchPlan p;
@@ -419,6 +432,17 @@ LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bo
         const int nbt = conv->cout_pad / 32;
         const int frags = conv->cin / (bf ? 16 : 8) * nbt * 64;
         KernelFn fn = bf ? pick_linear_bf16(nbt) : bf16_rows ? pick_linear_f32_bf16_rows(nbt) : pick_linear_f32(nbt);
+        // BF16 rows into an FP32 layer whose weights have BF16 terms: one
+        // wave per column block, a persistent grid over 32-row blocks.
+        KernelFn split = bf16_rows && has_split_terms(conv) ? pick_linear_split(nbt, conv->cin / 16) : nullptr;
+        if (split && !std::getenv("S3DX_CONV_TILING")) {
+            p.linear = p.split = true;
+            p.fn = split;
+            p.nb = nbt;
+            p.threads = 64 * nbt;
+            p.grid = dim3(static_cast<unsigned>(std::min<int64_t>((n_out + 31) / 32, resident_blocks(split, 0, p.threads))));
+            return p;
+        }
         if (fn && frags <= kLinearMaxFrags && !std::getenv("S3DX_CONV_TILING")) {
             p.linear = true;
             p.fn = fn;
@@ -668,6 +692,38 @@ S3DX_API s3dx_status s3dx_conv_set_weights(s3dx_conv *conv, const float *host_we
         }
         if (conv->w) (void)hipFree(conv->w);
         conv->w = d;
+        if (conv->w_split) (void)hipFree(conv->w_split);
+        conv->w_split = nullptr;
+        const int nbtot = conv->cout_pad / 32;
+        if (has_split_terms(conv)) {
+            // [k-step of 16][col block][term][lane][8 BF16], the BF16 B-operand
+            // lane order; term t+1 is the BF16 rounding of what terms 0..t
+            // leave of the FP32 weight (each remainder is exact in FP32).
+            std::vector<uint16_t> terms(static_cast<size_t>(cin) * nbtot * 32 * 3);
+            size_t f = 0;
+            for (int s16 = 0; s16 < cin / 16; ++s16)
+                for (int nbk = 0; nbk < nbtot; ++nbk)
+                    for (int t = 0; t < 3; ++t)
+                        for (int l = 0; l < 64; ++l)
+                            for (int e = 0; e < 8; ++e, ++f) {
+                                const int co = nbk * 32 + (l & 31), ci = s16 * 16 + (l >> 5) * 8 + e;
+                                float v = co < cout ? weight_at(host_weight, layout, 1, cin, cout, 0, co, ci) : 0.0f;
+                                uint16_t h = f32_to_bf16(v);
+                                for (int k = 0; k < t; ++k) {
+                                    v -= bf16_to_f32(h);
+                                    h = f32_to_bf16(v);
+                                }
+                                terms[f] = h;
+                            }
+            void *ds = nullptr;
+            hip_check(hipMalloc(&ds, terms.size() * 2), "hipMalloc weight terms");
+            const hipError_t es = hipMemcpy(ds, terms.data(), terms.size() * 2, hipMemcpyHostToDevice);
+            if (es != hipSuccess) {
+                (void)hipFree(ds);
+                hip_check(es, "hipMemcpy weight terms");
+            }
+            conv->w_split = ds;
+        }
         replace(conv->bias, upload_f32(host_bias, static_cast<size_t>(cout)));
         conv->weights_set = true;
     });
@@ -756,9 +812,9 @@ S3DX_API s3dx_status s3dx_conv_plan(const s3dx_conv *conv, int64_t n_in, int64_t
         if (widen) p = plan_launch(conv, src.rows * conv->cin * 4, n_out, true);
         char text[256];
         if (p.linear)
-            std::snprintf(text, sizeof(text), "linear cols=%d ksteps=%d ln=%s grid=%u", p.nb * 32,
-                          conv->cin / (conv->dtype == S3DX_BF16 ? 16 : 8),
-                          conv->ln ? "separate" : "none", p.grid.x);
+            std::snprintf(text, sizeof(text), "linear cols=%d ksteps=%d%s ln=%s grid=%u", p.nb * 32,
+                          conv->cin / (conv->dtype == S3DX_BF16 || p.split ? 16 : 8),
+                          p.split ? " terms=3" : "", conv->ln ? "separate" : "none", p.grid.x);
         else if (p.mfma)
             std::snprintf(text, sizeof(text), "mfma tiling=%d%s rows=%d cols=%d kc=%d xf=%d ln=%s grid=%ux%u",
                           p.tl->id, p.tl->splitk ? " split-k" : "", p.tl->rows(), p.tl->cols(), p.kc,
@@ -828,7 +884,7 @@ S3DX_API s3dx_status s3dx_conv_run(const s3dx_conv *conv, const void *x, int64_t
         a.kmap = kmap;
         a.n_out = n_out;
         a.kvol = conv->kvol;
-        a.w = conv->w;
+        a.w = conv->w;  // linear_split_kernel: w_split, set below
         a.bias = conv->bias;
         a.cout = conv->cout;
         a.cout_pad = conv->cout_pad;
@@ -855,13 +911,14 @@ S3DX_API s3dx_status s3dx_conv_run(const s3dx_conv *conv, const void *x, int64_t
             a.x_bytes = count * 4;
             plan = plan_launch(conv, a.x_bytes, n_out, aligned16);
         }
+        if (plan.split) a.w = conv->w_split;
         if (plan.mfma) {
             a.ln = plan.fused_ln;
             if (conv->ln && !plan.fused_ln) {  // LayerNorm as a separate pass
                 a.silu = 0;
                 a.residual = nullptr;
             }
-            hipLaunchKernelGGL(plan.fn, plan.grid, dim3(256), plan.smem, s, a);
+            hipLaunchKernelGGL(plan.fn, plan.grid, dim3(plan.threads), plan.smem, s, a);
             launch_check(plan.linear ? "conv_linear" : "conv_mfma");
         } else {
             a.ln = 0;

@@ -16,4 +16,14 @@ KernelFn pick_linear_f32(int nbt) { return pick_linear<float>(nbt); }
 
 KernelFn pick_linear_f32_bf16_rows(int nbt) { return pick_linear<float, true>(nbt); }
 
+KernelFn pick_linear_split(int nbt, int ksx) {
+    switch (nbt) {
+    case 1: return pick_linear_split_ks<1>(ksx);
+    case 2: return pick_linear_split_ks<2>(ksx);
+    case 3: return pick_linear_split_ks<3>(ksx);
+    case 4: return pick_linear_split_ks<4>(ksx);
+    default: return nullptr;
+    }
+}
+
 }  // namespace s3dx

@@ -65,6 +65,9 @@ KernelFn pick_linear_bf16(int nbt);
 KernelFn pick_linear_f32(int nbt);
 // The FP32 1x1-layer kernel reading BF16 rows, else nullptr.
 KernelFn pick_linear_f32_bf16_rows(int nbt);
+// The same on BF16 MFMAs with three-term split weights (Cin = 16 * ksx,
+// ksx in {2, 4, 6, 8}; nbt in 1..4), else nullptr.
+KernelFn pick_linear_split(int nbt, int ksx);
 
 namespace {
 
@@ -1248,6 +1251,80 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_splitk_kernel(ConvA
 // weight fragments.
 constexpr int kLinearMaxFrags = 4096;  // 64 KiB of LDS
 
+// Stores one 32-row block of a 1x1 layer from its accumulators: bias,
+// SiLU, residual, then the output dtype (EPC output elements per 16-byte
+// store).  stg is this wave's 8 staging rows of NBT*32+4 floats.
+template <int NBT, int EPC>
+__device__ __forceinline__ void linear_store_block(const ConvArgs &a, const f32x16 (&acc)[NBT],
+                                                   const float (&bias)[NBT], float *stg, int64_t blk,
+                                                   int lane, int half) {
+    constexpr int SLD = NBT * 32 + 4;
+    // D layout: lane l holds column l % 32; register j holds row
+    // 8*(j/4) + 4*(l/32) + j%4 of the block.  Rows 8g..8g+7 (registers
+    // 4g..4g+3) go through this wave's LDS rows, then leave as one
+    // contiguous, 16-byte-aligned span of 8*cout elements (8*cout*size is
+    // a multiple of 16): full-width stores, not row pieces that straddle
+    // cache lines.
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+        const int64_t row0 = blk * 32 + 8 * g;
+        if (row0 >= a.n_out) break;
+#pragma unroll
+        for (int cb = 0; cb < NBT; ++cb)
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                stg[(4 * half + q) * SLD + cb * 32 + (lane & 31)] = acc[cb][4 * g + q] + bias[cb];
+        const int elems = static_cast<int>(min(static_cast<int64_t>(8), a.n_out - row0)) * a.cout;
+        for (int c = lane; c * EPC < elems; c += 64) {
+            const int e0 = c * EPC;
+            int rr = e0 / a.cout, cc = e0 - rr * a.cout;
+            float v[EPC];
+#pragma unroll
+            for (int i = 0; i < EPC; ++i) {
+                const bool in = e0 + i < elems;
+                v[i] = in ? stg[rr * SLD + cc] : 0.0f;
+                if (a.silu) v[i] = silu(v[i]);
+                if (a.residual && in) {
+                    const int64_t roff = ((row0 + rr) >> a.residual_shift) * a.cout + cc;
+                    v[i] += a.y_bf16 ? bf16_to_f32(static_cast<const uint16_t *>(a.residual)[roff])
+                                     : static_cast<const float *>(a.residual)[roff];
+                }
+                if (++cc == a.cout) {
+                    cc = 0;
+                    ++rr;
+                }
+            }
+            const int64_t off = row0 * a.cout + e0;
+            if (e0 + EPC <= elems) {
+                if (a.y_bf16) {
+                    uint32_t w[EPC / 2];
+#pragma unroll
+                    for (int i = 0; i < EPC / 2; ++i)
+                        w[i] = static_cast<uint32_t>(f32_to_bf16(v[2 * i])) |
+                               (static_cast<uint32_t>(f32_to_bf16(v[2 * i + 1])) << 16);
+                    if constexpr (EPC == 8)
+                        *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.y) + off) = make_uint4(w[0], w[1], w[2], w[3]);
+                    else
+                        *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(a.y) + off) = make_uint2(w[0], w[1]);
+                } else {
+                    if constexpr (EPC == 4)
+                        *reinterpret_cast<float4 *>(static_cast<float *>(a.y) + off) = make_float4(v[0], v[1], v[2], v[3]);
+                    else
+#pragma unroll
+                        for (int i = 0; i < EPC; ++i) static_cast<float *>(a.y)[off + i] = v[i];
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < EPC; ++i) {
+                    if (e0 + i >= elems) break;
+                    if (a.y_bf16) static_cast<uint16_t *>(a.y)[off + i] = f32_to_bf16(v[i]);
+                    else static_cast<float *>(a.y)[off + i] = v[i];
+                }
+            }
+        }
+    }
+}
+
 // XB (FP32 layers only): x holds BF16 rows, widened exactly as each A
 // fragment is loaded (8 bytes per lane instead of 16).
 template <class T, int NBT, bool XB = false>
@@ -1306,70 +1383,133 @@ __global__ void __launch_bounds__(256) linear_kernel(ConvArgs a) {
 #pragma unroll
             for (int cb = 0; cb < NBT; ++cb) acc[cb] = mfma_step<T>(cur, wl[(st * NBT + cb) * 64 + lane], acc[cb]);
         }
+        linear_store_block<NBT, EPC>(a, acc, bias, stg, blk, lane, half);
+    }
+}
+
+// FP32 1x1 layer fed BF16 rows, on BF16 MFMAs.  Each FP32 weight w is held as
+// three BF16 terms, w1 = bf16(w), w2 = bf16(w - w1), w3 = bf16(w - w1 - w2)
+// (each difference is exact in FP32), so w - (w1 + w2 + w3) is below
+// 2^-24 |w| (the 24 significand bits of w in three 8-bit pieces; terms too
+// small for FP32's range aside).  A BF16 row element times a BF16 term is
+// exact in the FP32 accumulator, so the layer keeps FP32 accuracy while
+// three 32x32x16 BF16 MFMAs replace eight 32x32x2 FP32 ones per 16
+// channels.
+// Workgroup: one wave per 32-column block (64 * NBT threads), each holding
+// its block's 3 * KSX term fragments in registers for the whole launch.  The
+// workgroup takes 32-row blocks of a grid-stride sequence; every wave loads
+// the next block's rows (Cin = 16 * KSX channels, one 16-byte fragment per
+// k-step) into the registers of the current one as soon as its MFMAs are
+// issued, so the loads overlap the block's epilogue while three waves per
+// SIMD fit (a second register set for the next block would leave two;
+// Cin = 128 keeps two).
+// The finished values (bias, SiLU, residual) go into an LDS tile laid out
+// exactly as the output rows (row * cout + col), so the block leaves as one
+// contiguous span of 16-byte streaming stores.  Two tiles alternate: one
+// barrier per block.
+template <int NBT, int KSX>
+__global__ void __launch_bounds__(64 * NBT) __attribute__((amdgpu_waves_per_eu(KSX <= 6 ? 3 : 2)))
+linear_split_kernel(ConvArgs a) {
+    __shared__ __align__(16) float tile[2][32 * 32 * NBT];
+    const int tid = threadIdx.x, lane = tid & 63, half = lane >> 5;
+    const int cb = __builtin_amdgcn_readfirstlane(tid >> 6);  // this wave's column block
+    const int cout = a.cout;
+    const uint4 *wg = static_cast<const uint4 *>(a.w);
+    uint4 wr[KSX][3];
+#pragma unroll
+    for (int ks = 0; ks < KSX; ++ks)
+#pragma unroll
+        for (int t = 0; t < 3; ++t) wr[ks][t] = wg[((ks * NBT + cb) * 3 + t) * 64 + lane];
+    const int col = cb * 32 + (lane & 31);
+    const bool col_ok = col < cout;
+    const float bias = a.bias && col_ok ? a.bias[col] : 0.0f;
+    const auto x_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(a.x), static_cast<short>(0),
+                                                          static_cast<int32_t>(a.x_bytes), 0x00020000);
+    const int64_t nblk = (a.n_out + 31) / 32;
+    // Lane: row lane % 32 of the block, channels ks*16 + half*8 .. +8.  Rows
+    // past the end (the block after the workgroup's last) read zeros
+    // through the buffer resource.
+    auto load_block = [&](int64_t blk, uint4 (&f)[KSX]) __attribute__((always_inline)) {
+        const int64_t r = blk * 32 + (lane & 31);
+        const uint32_t base = r < a.n_out ? static_cast<uint32_t>(((r >> a.row_shift) * a.cin + half * 8) * 2)
+                                          : 0x80000000u;
+#pragma unroll
+        for (int ks = 0; ks < KSX; ++ks) {
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, static_cast<int32_t>(base + ks * 32), 0, 0);
+            f[ks] = make_uint4(v.x, v.y, v.z, v.w);
+        }
+    };
+    uint4 cur[KSX];
+    int buf = 0;
+    load_block(blockIdx.x, cur);
+    for (int64_t blk = blockIdx.x; blk < nblk; blk += gridDim.x, buf ^= 1) {
+        f32x16 acc = f32x16{};
+        // Smallest terms first.
+#pragma unroll
+        for (int ks = 0; ks < KSX; ++ks)
+#pragma unroll
+            for (int t = 2; t >= 0; --t) acc = mfma_step<uint16_t>(cur[ks], wr[ks][t], acc);
+        load_block(blk + gridDim.x, cur);
+        const int64_t row0 = blk * 32;
+        const int rows = static_cast<int>(min(static_cast<int64_t>(32), a.n_out - row0));
+        float *tl = tile[buf];
         // D layout: lane l holds column l % 32; register j holds row
-        // 8*(j/4) + 4*(l/32) + j%4 of the block.  Rows 8g..8g+7 (registers
-        // 4g..4g+3) go through this wave's LDS rows, then leave as one
-        // contiguous, 16-byte-aligned span of 8*cout elements (8*cout*size is
-        // a multiple of 16): full-width stores, not row pieces that straddle
-        // cache lines.
+        // 8*(j/4) + 4*(l/32) + j%4 of the block.
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const int64_t row0 = blk * 32 + 8 * g;
-            if (row0 >= a.n_out) break;
-#pragma unroll
-            for (int cb = 0; cb < NBT; ++cb)
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-                    stg[(4 * half + q) * SLD + cb * 32 + (lane & 31)] = acc[cb][4 * g + q] + bias[cb];
-            const int elems = static_cast<int>(min(static_cast<int64_t>(8), a.n_out - row0)) * a.cout;
-            for (int c = lane; c * EPC < elems; c += 64) {
-                const int e0 = c * EPC;
-                int rr = e0 / a.cout, cc = e0 - rr * a.cout;
-                float v[EPC];
-#pragma unroll
-                for (int i = 0; i < EPC; ++i) {
-                    const bool in = e0 + i < elems;
-                    v[i] = in ? stg[rr * SLD + cc] : 0.0f;
-                    if (a.silu) v[i] = silu(v[i]);
-                    if (a.residual && in) {
-                        const int64_t roff = ((row0 + rr) >> a.residual_shift) * a.cout + cc;
-                        v[i] += a.y_bf16 ? bf16_to_f32(static_cast<const uint16_t *>(a.residual)[roff])
-                                         : static_cast<const float *>(a.residual)[roff];
-                    }
-                    if (++cc == a.cout) {
-                        cc = 0;
-                        ++rr;
-                    }
-                }
-                const int64_t off = row0 * a.cout + e0;
-                if (e0 + EPC <= elems) {
-                    if (a.y_bf16) {
-                        uint32_t w[EPC / 2];
-#pragma unroll
-                        for (int i = 0; i < EPC / 2; ++i)
-                            w[i] = static_cast<uint32_t>(f32_to_bf16(v[2 * i])) |
-                                   (static_cast<uint32_t>(f32_to_bf16(v[2 * i + 1])) << 16);
-                        if constexpr (EPC == 8)
-                            *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.y) + off) = make_uint4(w[0], w[1], w[2], w[3]);
-                        else
-                            *reinterpret_cast<uint2 *>(static_cast<uint16_t *>(a.y) + off) = make_uint2(w[0], w[1]);
-                    } else {
-                        if constexpr (EPC == 4)
-                            *reinterpret_cast<float4 *>(static_cast<float *>(a.y) + off) = make_float4(v[0], v[1], v[2], v[3]);
-                        else
-#pragma unroll
-                            for (int i = 0; i < EPC; ++i) static_cast<float *>(a.y)[off + i] = v[i];
-                    }
+        for (int j = 0; j < 16; ++j) {
+            const int r = 8 * (j >> 2) + 4 * half + (j & 3);
+            if (!col_ok || r >= rows) continue;
+            float v = acc[j] + bias;
+            if (a.silu) v = silu(v);
+            if (a.residual) {
+                const int64_t roff = ((row0 + r) >> a.residual_shift) * cout + col;
+                v += a.y_bf16 ? bf16_to_f32(static_cast<const uint16_t *>(a.residual)[roff])
+                              : static_cast<const float *>(a.residual)[roff];
+            }
+            tl[r * cout + col] = v;
+        }
+        __syncthreads();
+        // The block's rows are one span of rows * cout elements starting at
+        // row0 * cout (16-byte aligned: 32 * cout elements per block).
+        const int elems = rows * cout;
+        if (a.y_bf16) {
+            uint16_t *y = static_cast<uint16_t *>(a.y) + row0 * cout;
+            for (int i = tid; i * 8 < elems; i += 64 * NBT) {
+                if (i * 8 + 8 <= elems) {
+                    const float4 p = *reinterpret_cast<const float4 *>(tl + i * 8);
+                    const float4 q = *reinterpret_cast<const float4 *>(tl + i * 8 + 4);
+                    *reinterpret_cast<uint4 *>(y + i * 8) = make_uint4(
+                        f32_to_bf16(p.x) | (static_cast<uint32_t>(f32_to_bf16(p.y)) << 16),
+                        f32_to_bf16(p.z) | (static_cast<uint32_t>(f32_to_bf16(p.w)) << 16),
+                        f32_to_bf16(q.x) | (static_cast<uint32_t>(f32_to_bf16(q.y)) << 16),
+                        f32_to_bf16(q.z) | (static_cast<uint32_t>(f32_to_bf16(q.w)) << 16));
                 } else {
-#pragma unroll
-                    for (int i = 0; i < EPC; ++i) {
-                        if (e0 + i >= elems) break;
-                        if (a.y_bf16) static_cast<uint16_t *>(a.y)[off + i] = f32_to_bf16(v[i]);
-                        else static_cast<float *>(a.y)[off + i] = v[i];
-                    }
+                    for (int e = i * 8; e < elems; ++e) y[e] = f32_to_bf16(tl[e]);
+                }
+            }
+        } else {
+            float *y = static_cast<float *>(a.y) + row0 * cout;
+            for (int i = tid; i * 4 < elems; i += 64 * NBT) {
+                if (i * 4 + 4 <= elems) {
+                    const u32x4 v = *reinterpret_cast<const u32x4 *>(tl + i * 4);
+                    __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(y + i * 4));
+                } else {
+                    for (int e = i * 4; e < elems; ++e) y[e] = tl[e];
                 }
             }
         }
+    }
+}
+
+// Cin = 16 * ksx for ksx in {2, 4, 6, 8}; nbt column blocks in 1..4.
+template <int NBT>
+KernelFn pick_linear_split_ks(int ksx) {
+    switch (ksx) {
+    case 2: return linear_split_kernel<NBT, 2>;
+    case 4: return linear_split_kernel<NBT, 4>;
+    case 6: return linear_split_kernel<NBT, 6>;
+    case 8: return linear_split_kernel<NBT, 8>;
+    default: return nullptr;
     }
 }
 

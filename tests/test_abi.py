@@ -125,7 +125,7 @@ def test_conv_plan_names_the_launched_kernel(s3dx, monkeypatch):
     # BF16 rows into FP32 layers: the head reads them in its kernel; a
     # 27-offset layer widens them first.  Other combinations are refused.
     head = s3dx.SparseConv(96, 101, 1, s3dx.F32).set_input_dtype(s3dx.BF16)
-    assert head.plan(8 * n, 8 * n).startswith("in=bf16 linear cols=128")
+    assert head.plan(8 * n, 8 * n).startswith("in=bf16 linear cols=128 ksteps=6 terms=3")
     assert s3dx.SparseConv(64, 64, 27, s3dx.F32).set_input_dtype(s3dx.BF16).plan(n, n).startswith("in=bf16 pre=widen mfma")
     with pytest.raises(s3dx.S3dxError, match="input dtype"):
         s3dx.SparseConv(64, 64, 27, s3dx.BF16).set_input_dtype(s3dx.F32)

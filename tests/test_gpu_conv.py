@@ -397,18 +397,27 @@ def test_centre_column_not_identity(s3dx, O, W, dtype):
 
 
 @pytest.mark.parametrize("cin,cout,kvol,n,plan", [
-    (96, 101, 1, 300001, "in=bf16 linear"),   # the mesh head's shape, > 2 passes of the persistent grid
-    (128, 96, 1, 4099, "in=bf16 linear"),
+    (96, 101, 1, 300001, "in=bf16 linear cols=128 ksteps=6 terms=3"),  # the mesh head, > 2 grid passes
+    (128, 96, 1, 4099, "in=bf16 linear cols=96 ksteps=8 terms=3"),
+    (32, 20, 1, 777, "in=bf16 linear cols=32 ksteps=2 terms=3"),
     (64, 64, 27, None, "in=bf16 pre=widen mfma"),
+    (192, 96, 1, 5000, "in=bf16 pre=widen mfma"),
 ])
 def test_bf16_rows_into_fp32_layer(s3dx, O, W, cin, cout, kvol, n, plan):
-    # BF16 rows feeding an FP32 layer: bit-identical to widening them first
-    # (exact) and running the same FP32 layer on FP32 rows.
+    # BF16 rows feeding an FP32 layer.  Widened plans are bit-identical to
+    # widening the rows first (exact) and running the same FP32 layer.  The
+    # three-term plans multiply on BF16 MFMAs: every product is exact and
+    # the sums are FP32, so they stay within 1e-6 (rel-L2) of a float64
+    # reference, like the FP32 kernel; dropping the smallest weight term
+    # alone gives ~1e-5.  The weights span 2^-20 .. 2^20 so that every term
+    # carries bits.
     coords = W.shells_union(2)[:3000] if kvol == 27 else None
     n = coords.shape[0] if kvol == 27 else n
     kmap = O.kmap_subm3(coords, n) if kvol == 27 else None
     xb = W.f32_to_bf16_bits(W.normal_f32(41, 1, (n, cin)))
     w = W.conv_weight(41, 2, cin, cout, kvol=kvol)
+    if kvol == 1:
+        w = (w * np.exp2(np.random.default_rng(43).integers(-20, 21, w.shape))).astype(np.float32)
     b = W.normal_f32(41, 3, (cout,))
     conv_b = s3dx.SparseConv(cin, cout, kvol, s3dx.F32).set_weights(w, s3dx.WEIGHT_SLAT, b).set_input_dtype(s3dx.BF16)
     got_plan = conv_b.plan(n, n)
@@ -420,4 +429,39 @@ def test_bf16_rows_into_fp32_layer(s3dx, O, W, cin, cout, kvol, n, plan):
     y2 = s3dx.DeviceArray((n, cout), np.float32)
     conv_b.run(s3dx.DeviceArray.from_host(xb), n, dk, n, y1, s3dx.F32)
     conv_f.run(s3dx.DeviceArray.from_host(W.bf16_bits_to_f32(xb)), n, dk, n, y2, s3dx.F32)
-    assert np.array_equal(y1.download(), y2.download())
+    g1, g2 = y1.download(), y2.download()
+    if "terms=3" not in plan:
+        assert np.array_equal(g1, g2)
+        return
+    ref = W.bf16_bits_to_f32(xb).astype(np.float64) @ w.reshape(cout, cin).astype(np.float64).T + b
+    e1, e2 = rel_l2(g1, ref), rel_l2(g2, ref)
+    print(f"  rel-L2 vs float64: three-term {e1:.3g}, FP32 kernel {e2:.3g}", flush=True)
+    assert e1 <= 1e-6 and e2 <= 1e-6
+
+
+@pytest.mark.parametrize("y_dtype", [0, 1])
+@pytest.mark.parametrize("cin,cout,p", [(64, 96, 1001), (128, 128, 333), (32, 101, 77)])
+def test_bf16_rows_three_term_epilogue(s3dx, W, y_dtype, cin, cout, p):
+    # The three-term kernel's epilogue: parent rows (row i reads x[i >> 3]),
+    # SiLU, a per-parent residual, FP32 or BF16 output, and a last block
+    # shorter than 32 rows (8 * p rows).  Reference: float64.
+    n = 8 * p
+    xb = W.f32_to_bf16_bits(W.normal_f32(47, 1, (p, cin)))
+    w = W.conv_weight(47, 2, cin, cout, kvol=1)
+    b = W.normal_f32(47, 3, (cout,))
+    res = W.normal_f32(47, 4, (p, cout))
+    if y_dtype == s3dx.BF16:
+        res = W.round_bf16(res)
+    conv = (s3dx.SparseConv(cin, cout, 1, s3dx.F32).set_weights(w, s3dx.WEIGHT_SLAT, b)
+            .set_input_dtype(s3dx.BF16).set_gather_parent(True).set_silu(True).set_residual_parent(True))
+    plan = conv.plan(p, n)
+    print(f"three-term epilogue cin={cin} cout={cout} p={p} y_dtype={y_dtype}: {plan}", flush=True)
+    assert "terms=3" in plan and "parent-rows" in plan, plan
+    y = s3dx.DeviceArray((n, cout), np.uint16 if y_dtype == s3dx.BF16 else np.float32)
+    dr = s3dx.DeviceArray.from_host(W.f32_to_bf16_bits(res) if y_dtype == s3dx.BF16 else res)
+    conv.run(s3dx.DeviceArray.from_host(xb), p, None, n, y, y_dtype, dr)
+    got = from_dev(s3dx, y, y_dtype)
+    h = W.bf16_bits_to_f32(xb).astype(np.float64) @ w.reshape(cout, cin).astype(np.float64).T + b
+    h = h / (1.0 + np.exp(-h)) + res
+    ref = np.repeat(h, 8, axis=0)
+    assert rel_l2(got, ref) <= (1e-6 if y_dtype == s3dx.F32 else 4e-3)
