@@ -440,7 +440,7 @@ def test_bf16_rows_into_fp32_layer(s3dx, O, W, cin, cout, kvol, n, plan):
 
 
 @pytest.mark.parametrize("y_dtype", [0, 1])
-@pytest.mark.parametrize("cin,cout,p", [(64, 96, 1001), (128, 128, 333), (32, 101, 77)])
+@pytest.mark.parametrize("cin,cout,p", [(64, 96, 1001), (128, 128, 333), (32, 101, 77), (64, 64, 5)])
 def test_bf16_rows_three_term_epilogue(s3dx, W, y_dtype, cin, cout, p):
     # The three-term kernel's epilogue: parent rows (row i reads x[i >> 3]),
     # SiLU, a per-parent residual, FP32 or BF16 output, and a last block
