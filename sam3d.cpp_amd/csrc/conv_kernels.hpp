@@ -1123,6 +1123,10 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_splitk_kernel(ConvA
         else load_b(nx, b1);
         next_task(cur, left, nx);  // task 2
         lds_barrier();
+        // The task loop at raised wave priority: where the other workgroup on
+        // the CU is in its prologue, reduction or epilogue, this one's MFMA
+        // stream issues first (same-box A/B: -1.4% BF16, -0.6% FP32).
+        __builtin_amdgcn_s_setprio(1);
         if (odd) {
             read_frags(buf0, fy);
             body(fy, fx, b1, buf1, ra, nx, cur, left);
@@ -1137,6 +1141,7 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_splitk_kernel(ConvA
             body(fy, fx, b1, buf0, ra, nx, cur, left);
         }
         lds_barrier();  // the last fragment reads finish before the tile reuses LDS
+        __builtin_amdgcn_s_setprio(0);
     }
 
     // ---- reduce the 4 partial tiles through LDS, in two phases ----
