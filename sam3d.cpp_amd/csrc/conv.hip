@@ -329,7 +329,7 @@ const Tiling *choose_tiling(int64_t n_out, int nb, int ntiles, bool bf, int kc, 
     for (const Tiling &t : kTilings) {
         if (!usable(t)) continue;
         int rank;
-        if (t.id == 17 || t.id == 18) continue;   // 64-row tiles: chosen by plan_launch
+        if (t.id >= 17) continue;                 // 64-row tiles: chosen by plan_launch
         if (t.splitk) rank = t.id >= 15 ? 0 : 1;  // 128-channel tasks (chunks joined) first
         else if (t.wn == 1 && t.nbw == 4) rank = blocks(t) >= 192 ? 2 : 10;  // 32x128 wave tiles
         else if (t.mbw == 2) rank = blocks(t) >= 256 ? 3 : 20;
@@ -517,6 +517,15 @@ LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bo
                         if (t.id == id) p.tl = &t;
                     p.kc = kc;
                 }
+            }
+            // Joined-chunk 96-column tasks (15) over more 128-row tiles than
+            // one pass over the CUs: the same kernel with 64-row tiles, two
+            // workgroups per CU (19).
+            if (p.tl->id == 15 && forced == 0 && !std::getenv("S3DX_CONV_TILING")) {
+                const int64_t tiles = (n_out + 127) / 128 * (blocks / p.nb);
+                if (tiles > device_cus() && tiling_kernel(19, bf, p.kc, p.xf))
+                    for (const Tiling &t : kTilings)
+                        if (t.id == 19) p.tl = &t;
             }
             // Few row tiles (small voxel sets): split-K runs one workgroup
             // per CU, so narrower column tiles that still fit in one pass

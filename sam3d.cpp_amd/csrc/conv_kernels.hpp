@@ -54,6 +54,7 @@ inline constexpr Tiling kTilings[] = {
     {5, 1, 4, 2, 0}, {6, 2, 1, 2, 0}, {7, 2, 3, 1, 0}, {8, 2, 2, 2, 0}, {9, 2, 3, 2, 0},
     {10, 1, 4, 1, 0}, {11, 4, 4, 1, 1}, {12, 4, 2, 1, 1}, {13, 4, 3, 1, 1}, {14, 4, 1, 1, 1},
     {15, 4, 3, 1, 1}, {16, 4, 4, 1, 1}, {17, 2, 4, 1, 1}, {18, 2, 4, 1, 1},
+    {19, 2, 3, 1, 1},
 };
 
 // MFMA kernel for tiling `id`, kc channels per task, xf 64-bit gathers;
@@ -1245,6 +1246,9 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_splitk_kernel(ConvA
 //   0: 1,1,1,1  1: 1,1,2,1  2: 1,3,1,1  3: 1,2,2,1  4: 1,3,2,1  5: 1,4,2,1
 //   6: 2,1,2,1  7: 2,3,1,1  8: 2,2,2,1  9: 2,3,2,1  10: 1,4,1,2
 //   11-14: split-K, 128 rows x 128 / 64 / 96 / 32 columns
+//   15, 16: split-K, 128 rows x 96 / 128 columns, 128-channel tasks joined
+//           from 32- or 64-channel chunks; 19: 15 with 64 rows
+//   17, 18: split-K, 64 rows x 128 columns, 128- / 64-channel tasks
 // 1x1 layers (kvol 1, no map): y[r] = W x[r >> row_shift] + bias, then SiLU
 // and the residual.  Persistent workgroups: the packed weights (every k-step
 // of all NBT column blocks) are copied to LDS once; each wave then takes
@@ -1568,6 +1572,12 @@ KernelFn pick_tiling(int id) {
         } else {
             return nullptr;
         }
+    }
+    case 19: {  // 15 with 64-row tiles, two workgroups per CU (16's 128 columns would spill)
+        if constexpr (sizeof(T) == 2 && XF == 0 && (KC == 32 || KC == 64))
+            return conv_splitk_kernel<T, 3, 128, XF, 128 / KC, 2>;
+        else
+            return nullptr;
     }
     case 17: case 18: {  // 64-row tiles, two workgroups per CU (18: half-width tasks)
         if constexpr (sizeof(T) == 2 && XF == 0 && KC == 128)

@@ -114,8 +114,10 @@ def test_conv_plan_names_the_launched_kernel(s3dx, monkeypatch):
     assert f64.plan(n, n).startswith("mfma tiling=12 split-k rows=128 cols=64 kc=64")
     # 96 bf16 channels: four 32-channel chunks make each 128-channel task.
     assert s3dx.SparseConv(96, 96, 27, s3dx.BF16).plan(n, n).startswith("mfma tiling=15 split-k rows=128 cols=96 kc=32")
-    # 192 output columns without LayerNorm: two 96-column split-K tiles.
-    assert s3dx.SparseConv(192, 192, 27, s3dx.BF16).plan(n, n).endswith("ln=none grid=221x2")
+    # 192 output columns without LayerNorm: two 96-column split-K tiles; with
+    # more 128-row tiles than CUs (221 x 2) they become 64-row tiles, two per CU.
+    assert s3dx.SparseConv(192, 192, 27, s3dx.BF16).plan(n, n) == \
+        "mfma tiling=19 split-k rows=64 cols=96 kc=64 xf=0 ln=none grid=442x2"
     assert "cols=192" in s3dx.SparseConv(192, 192, 27, s3dx.BF16).set_layernorm(True, 1e-6).plan(n, n)
     # Cout not a multiple of 32: the generic kernel.
     assert s3dx.SparseConv(16, 40, 27, s3dx.F32).plan(100, 100) == "generic rows=64 cols=64 ln=none grid=2x1"

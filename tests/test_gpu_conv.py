@@ -316,6 +316,7 @@ def test_row_block_tilings(s3dx, O, W, monkeypatch, dtype, cin, cout, tiling):
     (96, 96, "15", 27), (192, 96, "15", 27), (96, 128, "16", 27), (192, 128, "16", 27),
     (160, 96, "15", 27), (224, 128, "16", 27),  # 5 and 7 chunks: the last task is part empty
     (96, 96, "15", 1), (160, 128, "16", 1),     # one task holding an empty sub-task
+    (96, 96, "19", 27), (192, 96, "19", 27), (160, 96, "19", 27),  # 15 with 64-row tiles
 ])
 def test_subtask_tilings(s3dx, O, W, monkeypatch, cin, cout, tiling, kvol):
     # Split-K tasks of 128 channels made of 32- or 64-channel chunks (bf16),
