@@ -35,6 +35,8 @@ def test_layernorm_rows(s3dx, O, W, c):
     (20000, 96, 32, 300.0, 0.05),  # |mean| >> std: the shifted sums keep the variance
     (700, 36, 4, 1.0, 1.0),        # rows not whole 16-byte pieces: per-element loads
     (3, 64, 32, 0.0, 1.0),         # fewer rows than blocks
+    (2000, 1024, 2, 1.0, 1.0),     # 512 channels a group: totals in two chunks of 256
+    (500, 300, 1, 1.0, 1.0),       # 300 channels a group: a partial second chunk
 ])
 def test_groupnorm_stats_and_affine(s3dx, O, W, n, c, groups, mean, std):
     x = W.normal_f32(12, 1, (n, c), std) + W.normal_f32(12, 2, (c,), 2.0) + np.float32(mean)
