@@ -213,6 +213,10 @@ S3DX_API s3dx_status s3dx_downsample_coords(const int32_t *coords, int64_t n, in
  *   v -> LayerNorm over Cout (eps, optional affine), optional modulate
  *        v*scale + v + shift (slat_flow_graph.cpp:55-59) -> optional SiLU
  *        -> optional + residual[i] -> y[i]
+ * All of it in float32, rounded once to y's dtype.  When the output tile
+ * cannot span the row (Cout above 256, or not whole 32-column blocks) the
+ * LayerNorm runs as a second pass over the conv's float32 output, kept in
+ * another buffer the layer owns (n_out * Cout * 4 bytes, same rules).
  * Arithmetic: float32 inputs use FP32 MFMA/VALU; bfloat16 inputs use BF16 MFMA;
  * both accumulate in float32.  Deterministic (no atomics on outputs).
  * ---------------------------------------------------------------------- */
@@ -243,6 +247,17 @@ S3DX_API s3dx_status s3dx_conv_set_layernorm(s3dx_conv *conv, int32_t enable, fl
                                              const float *host_mod_scale,
                                              const float *host_mod_shift, char *error,
                                              uint64_t error_capacity);
+/* Per-forward modulate of the fused LayerNorm, h*scale + h + shift
+ * (slat_flow_graph.cpp:55-59): DEVICE scale/shift [cout] float32, caller-owned,
+ * read when s3dx_conv_run runs.  In the SLat res_block they are the two halves
+ * of emb_layers(silu(t_emb)), recomputed on the device for each of the flow's
+ * forwards (slat_flow_graph.cpp:238-243, 257), so a caller updates the buffers
+ * and runs again without touching the layer.  Takes precedence over host
+ * modulate arrays given to s3dx_conv_set_layernorm; NULL,NULL returns to
+ * those.  Requires the LayerNorm epilogue to be enabled; disabling it clears
+ * this setting. */
+S3DX_API s3dx_status s3dx_conv_set_modulate(s3dx_conv *conv, const float *scale, const float *shift,
+                                            char *error, uint64_t error_capacity);
 S3DX_API s3dx_status s3dx_conv_set_silu(s3dx_conv *conv, int32_t enable, char *error,
                                         uint64_t error_capacity);
 /* Residual at parent resolution (enable 0/1): the residual passed to
@@ -265,8 +280,9 @@ S3DX_API s3dx_status s3dx_conv_set_residual_parent(s3dx_conv *conv, int32_t enab
 S3DX_API s3dx_status s3dx_conv_set_input_dtype(s3dx_conv *conv, int32_t dtype, char *error,
                                                uint64_t error_capacity);
 /* Runs the layer.  x [n_in or n_in parents][cin] in the layer's input dtype; kmap
- * [n_out][kvol] (NULL only for kvol 1); residual [n_out][cout] in y_dtype or
- * NULL; y [n_out][cout] in y_dtype.  Asynchronous on `stream`. */
+ * [n_out][kvol] (NULL only for kvol 1, where output row i reads input row i,
+ * so n_out may not exceed the input rows); residual [n_out][cout] in y_dtype
+ * or NULL; y [n_out][cout] in y_dtype.  Asynchronous on `stream`. */
 S3DX_API s3dx_status s3dx_conv_run(const s3dx_conv *conv, const void *x, int64_t n_in,
                                    const int32_t *kmap, int64_t n_out, const void *residual,
                                    void *y, int32_t y_dtype, s3dx_stream stream, char *error,

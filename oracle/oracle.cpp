@@ -195,10 +195,15 @@ void orc_conv_subm(const float *x, int64_t n_in, int32_t cin, const int32_t *kma
                     const float *wr = layout == 0
                                           ? w + (static_cast<int64_t>(co) * kvol + o) * cin
                                           : w + (static_cast<int64_t>(o) * cout + co) * cin;
-                    double s = 0.0;
-                    for (int ci = 0; ci < cin; ++ci)
-                        s += static_cast<double>(wr[ci]) * static_cast<double>(xr[ci]);
-                    acc[co] += s;
+                    // Four float64 partial sums (independent chains; the order
+                    // is fixed, so results are deterministic).
+                    double s[4] = {0.0, 0.0, 0.0, 0.0};
+                    int ci = 0;
+                    for (; ci + 4 <= cin; ci += 4)
+                        for (int u = 0; u < 4; ++u)
+                            s[u] += static_cast<double>(wr[ci + u]) * static_cast<double>(xr[ci + u]);
+                    for (; ci < cin; ++ci) s[0] += static_cast<double>(wr[ci]) * static_cast<double>(xr[ci]);
+                    acc[co] += (s[0] + s[1]) + (s[2] + s[3]);
                 }
             }
             for (int co = 0; co < cout; ++co) y[i * cout + co] = static_cast<float>(acc[co]);

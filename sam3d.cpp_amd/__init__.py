@@ -77,6 +77,7 @@ SIGNATURES = {
     "s3dx_conv_set_gather_parent": (_u32, [_vp, _i32, _vp], True),
     "s3dx_conv_set_input_affine_silu": (_u32, [_vp, _vp, _vp], True),
     "s3dx_conv_set_layernorm": (_u32, [_vp, _i32, _f32, _vp, _vp, _vp, _vp], True),
+    "s3dx_conv_set_modulate": (_u32, [_vp, _vp, _vp], True),
     "s3dx_conv_set_silu": (_u32, [_vp, _i32], True),
     "s3dx_conv_set_residual_parent": (_u32, [_vp, _i32], True),
     "s3dx_conv_set_input_dtype": (_u32, [_vp, _i32], True),
@@ -459,6 +460,13 @@ class SparseConv:
         hs = [_host_f32(a) for a in (weight, bias, mod_scale, mod_shift)]
         call("s3dx_conv_set_layernorm", _vp(self.handle), _i32(int(enable)), _f32(eps),
              *[p for _, p in hs])
+        return self
+
+    def set_modulate(self, scale: DeviceArray = None, shift: DeviceArray = None):
+        """Per-run modulate h*scale + h + shift from DEVICE [cout] float32 buffers
+        (the res_block's emb_layers output); read at run time."""
+        call("s3dx_conv_set_modulate", _vp(self.handle), _dptr(scale), _dptr(shift))
+        self._modulate_refs = (scale, shift)
         return self
 
     def set_silu(self, enable: bool = True):

@@ -252,9 +252,7 @@ __global__ void __launch_bounds__(256) conv_generic_kernel(ConvArgs a) {
 void layernorm_rows_launch(const void *x, int32_t x_dtype, int64_t n, int32_t c, float eps,
                            const float *w, const float *b, const float *mod_scale,
                            const float *mod_shift, int32_t silu, void *y, int32_t y_dtype,
-                           hipStream_t stream);
-void add_rows_launch(const void *a, const void *b, int32_t dtype, int64_t n, int32_t c,
-                     int32_t b_shift, void *y, hipStream_t stream);
+                           hipStream_t stream, const void *residual = nullptr, int32_t residual_shift = 0);
 void convert_launch(const void *x, int32_t x_dtype, int64_t count, void *y, int32_t y_dtype,
                     hipStream_t stream);
 
@@ -281,18 +279,24 @@ struct s3dx_conv {
     bool residual_parent = false;  // residual has one row per 8 output rows
     float eps = 1e-6f;
     float *ln_w = nullptr, *ln_b = nullptr, *mod_scale = nullptr, *mod_shift = nullptr;
+    // Per-run modulate (caller-owned device [cout]); replaces mod_scale/shift.
+    const float *dmod_scale = nullptr, *dmod_shift = nullptr;
     bool weights_set = false;
     // Transformed input rows (slot offsets / affine + SiLU applied), grown on
     // demand by s3dx_conv_run; one buffer per layer object.
     mutable void *xin = nullptr;
     mutable int64_t xin_bytes = 0;
+    // FP32 conv output ahead of a LayerNorm that runs as its own pass (the
+    // output tile does not span the row), grown on demand like xin.
+    mutable void *pre_ln = nullptr;
+    mutable int64_t pre_ln_bytes = 0;
 
     bool transforms() const { return slot_offset != nullptr || pre_scale != nullptr; }
 
     ~s3dx_conv() {
         for (void *p : {w, w_split, static_cast<void *>(bias), static_cast<void *>(slot_offset),
                         static_cast<void *>(ln_w), static_cast<void *>(ln_b),
-                        static_cast<void *>(mod_scale), static_cast<void *>(mod_shift), xin})
+                        static_cast<void *>(mod_scale), static_cast<void *>(mod_shift), xin, pre_ln})
             if (p) (void)hipFree(p);
     }
 };
@@ -569,20 +573,25 @@ float *upload_f32(const float *host, size_t count) {
     return static_cast<float *>(d);
 }
 
-// The layer's transformed-input buffer, at least `bytes` long.  Growing it
-// waits for the stream's earlier work, which may still read the old one.
-void *transform_buffer(const s3dx_conv *conv, int64_t bytes, hipStream_t s) {
-    if (bytes > conv->xin_bytes) {
-        if (conv->xin) {
+// A buffer the layer owns, at least `bytes` long.  Growing it waits for the
+// stream's earlier work, which may still read the old one.
+void *layer_buffer(void *&buf, int64_t &have, int64_t bytes, hipStream_t s) {
+    if (bytes > have) {
+        if (buf) {
             hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
-            hip_check(hipFree(conv->xin), "hipFree");
-            conv->xin = nullptr;
-            conv->xin_bytes = 0;
+            hip_check(hipFree(buf), "hipFree");
+            buf = nullptr;
+            have = 0;
         }
-        hip_check(hipMalloc(&conv->xin, static_cast<size_t>(bytes)), "hipMalloc");
-        conv->xin_bytes = bytes;
+        hip_check(hipMalloc(&buf, static_cast<size_t>(bytes)), "hipMalloc");
+        have = bytes;
     }
-    return conv->xin;
+    return buf;
+}
+
+// The layer's transformed-input buffer.
+void *transform_buffer(const s3dx_conv *conv, int64_t bytes, hipStream_t s) {
+    return layer_buffer(conv->xin, conv->xin_bytes, bytes, s);
 }
 
 void replace(float *&slot, float *fresh) {
@@ -777,6 +786,18 @@ S3DX_API s3dx_status s3dx_conv_set_layernorm(s3dx_conv *conv, int32_t enable, fl
         replace(conv->ln_b, enable ? upload_f32(host_bias, c) : nullptr);
         replace(conv->mod_scale, enable ? upload_f32(host_mod_scale, c) : nullptr);
         replace(conv->mod_shift, enable ? upload_f32(host_mod_shift, c) : nullptr);
+        if (!enable) conv->dmod_scale = conv->dmod_shift = nullptr;
+    });
+}
+
+S3DX_API s3dx_status s3dx_conv_set_modulate(s3dx_conv *conv, const float *scale, const float *shift,
+                                            char *error, uint64_t error_capacity) {
+    return boundary(error, error_capacity, [&] {
+        require(conv != nullptr, "conv is NULL");
+        require((scale == nullptr) == (shift == nullptr), "modulate scale and shift must both be set");
+        require(scale == nullptr || conv->ln, "modulate needs the LayerNorm epilogue (s3dx_conv_set_layernorm)");
+        conv->dmod_scale = scale;
+        conv->dmod_shift = shift;
     });
 }
 
@@ -814,6 +835,8 @@ S3DX_API s3dx_status s3dx_conv_plan(const s3dx_conv *conv, int64_t n_in, int64_t
         require(plan != nullptr && plan_capacity > 0, "plan buffer is empty");
         require(n_in > 0 && n_out > 0, "row counts must be positive");
         const Source src = source_of(conv, n_in);
+        require(conv->kvol != 1 || n_out <= src.n_src,
+                "n_out exceeds the input rows (kvol 1 without a map reads row i of x)");
         const bool bf16_rows = conv->in_dtype != conv->dtype;
         const int64_t x_bytes = src.rows * conv->cin * static_cast<int64_t>(dtype_size(conv->in_dtype));
         LaunchPlan p = plan_launch(conv, x_bytes, n_out, true, bf16_rows);
@@ -853,6 +876,8 @@ S3DX_API s3dx_status s3dx_conv_run(const s3dx_conv *conv, const void *x, int64_t
         require(aligned(x, 16) && aligned(y, 4) && aligned(residual, 4), "misaligned buffer");
         const Source src = source_of(conv, n_in);
         require(src.n_src <= INT32_MAX, "input rows exceed INT32_MAX");
+        require(kmap != nullptr || n_out <= src.n_src,
+                "n_out exceeds the input rows (kvol 1 without a map reads row i of x)");
         const hipStream_t s = as_stream(stream);
         const bool bf = conv->dtype == S3DX_BF16;
         const bool bf16_rows = conv->in_dtype != conv->dtype;  // BF16 rows into an FP32 layer
@@ -905,8 +930,8 @@ S3DX_API s3dx_status s3dx_conv_run(const s3dx_conv *conv, const void *x, int64_t
         a.eps = conv->eps;
         a.ln_w = conv->ln_w;
         a.ln_b = conv->ln_b;
-        a.mod_scale = conv->mod_scale;
-        a.mod_shift = conv->mod_shift;
+        a.mod_scale = conv->dmod_scale ? conv->dmod_scale : conv->mod_scale;
+        a.mod_shift = conv->dmod_scale ? conv->dmod_shift : conv->mod_shift;
         // The MFMA kernel reads the map and writes rows with 16-byte accesses.
         const bool aligned16 = aligned(kmap, 16) && aligned(y, 16) && aligned(residual, 16);
         LaunchPlan plan = plan_launch(conv, a.x_bytes, n_out, aligned16, bf16_rows);
@@ -921,30 +946,31 @@ S3DX_API s3dx_status s3dx_conv_run(const s3dx_conv *conv, const void *x, int64_t
             plan = plan_launch(conv, a.x_bytes, n_out, aligned16);
         }
         if (plan.split) a.w = conv->w_split;
+        // A LayerNorm the epilogue cannot fuse runs as its own pass over the
+        // conv's FP32 output (the layer's buffer), then modulate, SiLU and
+        // the residual, rounded once to y_dtype as the fused epilogue does.
+        const bool separate_ln = conv->ln && !(plan.mfma && plan.fused_ln);
+        if (separate_ln) {
+            a.y = layer_buffer(conv->pre_ln, conv->pre_ln_bytes, n_out * conv->cout * 4, s);
+            a.y_bf16 = 0;
+            a.silu = 0;
+            a.residual = nullptr;
+            a.ln = 0;
+        }
         if (plan.mfma) {
             a.ln = plan.fused_ln;
-            if (conv->ln && !plan.fused_ln) {  // LayerNorm as a separate pass
-                a.silu = 0;
-                a.residual = nullptr;
-            }
             hipLaunchKernelGGL(plan.fn, plan.grid, dim3(plan.threads), plan.smem, s, a);
             launch_check(plan.linear ? "conv_linear" : "conv_mfma");
         } else {
             a.ln = 0;
-            if (conv->ln) {
-                a.silu = 0;
-                a.residual = nullptr;
-            }
             if (bf) hipLaunchKernelGGL(conv_generic_kernel<uint16_t>, plan.grid, dim3(256), 0, s, a);
             else hipLaunchKernelGGL(conv_generic_kernel<float>, plan.grid, dim3(256), 0, s, a);
             launch_check("conv_generic");
         }
-        if (conv->ln && !a.ln) {
-            layernorm_rows_launch(y, y_dtype, n_out, conv->cout, conv->eps, conv->ln_w, conv->ln_b,
-                                  conv->mod_scale, conv->mod_shift, conv->silu ? 1 : 0, y, y_dtype, s);
-            if (residual)
-                add_rows_launch(y, residual, y_dtype, n_out, conv->cout, conv->residual_parent ? 3 : 0, y, s);
-        }
+        if (separate_ln)
+            layernorm_rows_launch(conv->pre_ln, S3DX_F32, n_out, conv->cout, conv->eps, conv->ln_w, conv->ln_b,
+                                  a.mod_scale, a.mod_shift, conv->silu ? 1 : 0, y, y_dtype, s, residual,
+                                  conv->residual_parent ? 3 : 0);
     });
 }
 

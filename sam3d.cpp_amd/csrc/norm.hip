@@ -27,10 +27,12 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // One wave per row; two passes over the row (mean, then centred variance).
+// res (in TO, may be NULL): added after the SiLU, row (row >> res_shift).
 template <class TI, class TO>
 __global__ void __launch_bounds__(256)
 layernorm_kernel(const void *x, int64_t n, int32_t c, float eps, const float *w, const float *b,
-                 const float *ms, const float *mh, int32_t do_silu, void *y) {
+                 const float *ms, const float *mh, int32_t do_silu, void *y, const void *res,
+                 int32_t res_shift) {
     const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (row >= n) return;
@@ -50,20 +52,8 @@ layernorm_kernel(const void *x, int64_t n, int32_t c, float eps, const float *w,
         if (b) t += b[k];
         if (ms) t = (t * ms[k] + t) + mh[k];
         if (do_silu) t = silu(t);
+        if (res) t += ld<TO>(res, (row >> res_shift) * c + k);
         st<TO>(y, base + k, t);
-    }
-}
-
-// y[r][ch] = a[r][ch] + b[r >> b_shift][ch].
-template <class T>
-__global__ void __launch_bounds__(256)
-add_kernel(const void *a, const void *b, int64_t n, int32_t c, int32_t b_shift, void *y) {
-    const int64_t count = n * c;
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count;
-         i += stride) {
-        const int64_t r = i / c;
-        st<T>(y, i, ld<T>(a, i) + ld<T>(b, (r >> b_shift) * c + (i - r * c)));
     }
 }
 
@@ -394,19 +384,12 @@ void gn_layout(W &w, int32_t c, GnLayout *l) {
 void layernorm_rows_launch(const void *x, int32_t x_dtype, int64_t n, int32_t c, float eps,
                            const float *w, const float *b, const float *mod_scale,
                            const float *mod_shift, int32_t do_silu, void *y, int32_t y_dtype,
-                           hipStream_t stream) {
+                           hipStream_t stream, const void *residual, int32_t residual_shift) {
     const unsigned blocks = static_cast<unsigned>((n + 3) / 4);
     S3DX_DISPATCH2(x_dtype, y_dtype, layernorm_kernel,
-                   <<<blocks, 256, 0, stream>>>(x, n, c, eps, w, b, mod_scale, mod_shift, do_silu, y));
+                   <<<blocks, 256, 0, stream>>>(x, n, c, eps, w, b, mod_scale, mod_shift, do_silu, y,
+                                                residual, residual_shift));
     launch_check("layernorm");
-}
-
-void add_rows_launch(const void *a, const void *b, int32_t dtype, int64_t n, int32_t c,
-                     int32_t b_shift, void *y, hipStream_t stream) {
-    const int64_t count = n * c;
-    if (dtype == S3DX_BF16) add_kernel<uint16_t><<<grid_for(count), 256, 0, stream>>>(a, b, n, c, b_shift, y);
-    else add_kernel<float><<<grid_for(count), 256, 0, stream>>>(a, b, n, c, b_shift, y);
-    launch_check("add");
 }
 
 void convert_launch(const void *x, int32_t x_dtype, int64_t count, void *y, int32_t y_dtype,
@@ -439,7 +422,7 @@ S3DX_API s3dx_status s3dx_layernorm_rows(const void *x, int32_t x_dtype, int64_t
                 "modulate scale and shift must both be set");
         require(x != y || x_dtype == y_dtype, "in-place LayerNorm needs equal dtypes");
         layernorm_rows_launch(x, x_dtype, n, c, eps, w, b, mod_scale, mod_shift, silu, y, y_dtype,
-                              as_stream(stream));
+                              as_stream(stream), nullptr, 0);
     });
 }
 

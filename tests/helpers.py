@@ -1,6 +1,7 @@
 """Shared test helpers: named voxel sets rebuilt from the workload generators
 and the golden fixtures."""
 import hashlib
+import struct
 
 import numpy as np
 
@@ -29,3 +30,94 @@ def large_sets(W, O, arrays):
     occ = np.unpackbits(arrays["ss_occ.bits"]).reshape(64, 64, 64).astype(np.float32)
     sets["ss_occ_surface"] = O.prune_surface(O.occupancy_coords(occ))
     return sets
+
+
+def check_rel(got, ref, tol, what="") -> float:
+    """Asserts rel-L2(got, ref) <= tol, printing the measured value first."""
+    e = rel_l2(got, ref)
+    print(f"  rel-L2 {e:.3e} (gate {tol:.0e}) {what}", flush=True)
+    assert e <= tol, (what, e, tol)
+    return e
+
+
+def _coordinate_key(b, x, y, z):
+    """session.cpp:122-127 in Python integers: the four fields as uint32,
+    shifted by 48/32/16/0 into one uint64 (z masked to 16 bits), so fields
+    wider than 16 bits overlap their neighbours' bits."""
+    m32 = 0xFFFFFFFF
+    return (((b & m32) << 48) | ((x & m32) << 32) | ((y & m32) << 16) | (z & 0xFFFF)) & 0xFFFFFFFFFFFFFFFF
+
+
+def _wrap32(v):
+    return (v + 2 ** 31) % 2 ** 32 - 2 ** 31
+
+
+def prune_brute_force(coords):
+    """prune_surface_coords (session.cpp:133-163) written independently of the
+    oracle: a Python set of coordinate keys, and a row is kept (in input
+    order) when some cell of its 3x3x3 neighbourhood in its own batch has a
+    key outside the set."""
+    rows = [tuple(int(v) for v in r) for r in coords]
+    occupied = {_coordinate_key(*r) for r in rows}
+    keep = []
+    for b, x, y, z in rows:
+        if any(_coordinate_key(b, _wrap32(x + dx), _wrap32(y + dy), _wrap32(z + dz)) not in occupied
+               for dx in (-1, 0, 1) for dy in (-1, 0, 1) for dz in (-1, 0, 1)):
+            keep.append((b, x, y, z))
+    return np.array(keep, np.int32).reshape(-1, 4)
+
+
+def prune_cases():
+    """Sets the reference's prune is exercised on: two batches with negative
+    coordinates and duplicated rows, a solid cube (only its shell survives),
+    and cells whose coordinate_key aliases another cell's."""
+    rng = np.random.default_rng(5)
+    blobs = rng.integers(-5, 7, size=(2500, 4)).astype(np.int32)
+    blobs[:, 0] = rng.integers(0, 2, size=blobs.shape[0])
+    blobs = np.unique(blobs, axis=0)
+    blobs = np.concatenate([blobs, blobs[::53]], 0)[rng.permutation(blobs.shape[0] + len(blobs[::53]))]
+    g = np.arange(1, 8, dtype=np.int32)
+    x, y, z = np.meshgrid(g, g, g, indexing="ij")
+    cube = np.stack([np.full_like(x, 3), x, y, z], -1).reshape(-1, 4)
+    # A cube at negative coordinates: y's sign bits spill into x's field
+    # (y << 16 as uint64), so its keys alias one another.
+    neg = cube.copy()
+    neg[:, 1:] -= 9
+    # Aliasing: the centre (0,6,6,6) of the block [5,7]^3 lacks its +x
+    # neighbour (0,7,6,6), but (0,6,65542,6) has that key
+    # ((6<<32) | ((65542<<16)) == (7<<32) | (6<<16)), so the reference sees
+    # the neighbour as present and drops the centre.  (0,6,6,65542) shares
+    # the centre's key through the 16-bit z mask.
+    g3 = np.arange(5, 8, dtype=np.int32)
+    x, y, z = np.meshgrid(g3, g3, g3, indexing="ij")
+    block = np.stack([np.zeros_like(x), x, y, z], -1).reshape(-1, 4)
+    block = block[~np.all(block == [0, 7, 6, 6], axis=1)]
+    alias = np.concatenate([block, [[0, 6, 65542, 6], [0, 6, 6, 65542], [0, -1, 7, 2]]], 0).astype(np.int32)
+    return {"blobs_two_batches_duplicates": blobs, "solid_cube": cube, "negative_cube": neg,
+            "key_aliasing": alias}
+
+
+def gguf_bytes(kv, tensors, align=32):
+    """A GGUF v3 file: header, metadata, tensor infos, aligned data."""
+    def s(x):
+        b = x.encode()
+        return struct.pack("<Q", len(b)) + b
+    out = b"GGUF" + struct.pack("<IQQ", 3, len(tensors), len(kv))
+    for k, (vt, v) in kv.items():
+        out += s(k) + struct.pack("<I", vt)
+        if vt == 8:
+            out += s(v)
+        elif vt == 9:
+            out += struct.pack("<IQ", 4, len(v)) + b"".join(struct.pack("<I", e) for e in v)
+        else:
+            out += struct.pack({4: "<I", 6: "<f", 10: "<Q"}[vt], v)
+    blobs, off = [], 0
+    for name, (gtype, arr) in tensors.items():
+        out += s(name) + struct.pack("<I", arr.ndim) + struct.pack(f"<{arr.ndim}Q", *reversed(arr.shape))
+        out += struct.pack("<IQ", gtype, off)
+        blob = arr.tobytes()
+        pad = (-len(blob)) % align
+        blobs.append(blob + b"\0" * pad)
+        off += len(blob) + pad
+    out += b"\0" * ((-len(out)) % align)
+    return out + b"".join(blobs)

@@ -142,3 +142,28 @@ def test_missing_library_fails_loudly(s3dx, monkeypatch, tmp_path):
     monkeypatch.setattr(s3dx, "LIB_PATH", tmp_path / "absent.so")
     with pytest.raises(RuntimeError, match="not built"):
         s3dx.lib()
+
+
+def test_conv_modulate_needs_layernorm(s3dx):
+    # Device modulate pointers are only recorded here (never read without a
+    # run), so fake addresses suffice on a host without a GPU.
+    conv = s3dx.SparseConv(64, 128, 27, s3dx.BF16)
+    with pytest.raises(s3dx.S3dxError, match="LayerNorm"):
+        conv.set_modulate(0x1000, 0x2000)
+    with pytest.raises(s3dx.S3dxError, match="both"):
+        conv.set_layernorm(True, 1e-6).set_modulate(0x1000, None)
+    conv.set_modulate(0x1000, 0x2000)
+    conv.set_modulate(None, None)
+
+
+def test_linear_layer_rejects_rows_past_the_input(s3dx):
+    # kvol 1 without a map: output row i reads input row i (row i >> 3 when
+    # gathering parents), so n_out may not exceed the input rows.
+    conv = s3dx.SparseConv(64, 64, 1, s3dx.BF16)
+    assert "linear" in conv.plan(100, 100)
+    with pytest.raises(s3dx.S3dxError, match="n_out exceeds"):
+        conv.plan(100, 101)
+    conv.set_gather_parent(True)
+    conv.plan(100, 800)
+    with pytest.raises(s3dx.S3dxError, match="n_out exceeds"):
+        conv.plan(100, 801)

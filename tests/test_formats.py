@@ -12,6 +12,8 @@ from pathlib import Path
 import numpy as np
 import pytest
 
+from helpers import gguf_bytes
+
 FIXTURE = Path("/root/reference/tests/objects_runtime/fixtures/ss_occ_f32.samt")
 
 
@@ -54,32 +56,6 @@ def test_samt_int32_type_30_and_malformed(F, tmp_path):
         F.read_samt(tmp_path / "short.samt")
 
 
-def _gguf_bytes(kv, tensors, align=32):
-    """A GGUF v3 file: header, metadata, tensor infos, aligned data."""
-    def s(x):
-        b = x.encode()
-        return struct.pack("<Q", len(b)) + b
-    out = b"GGUF" + struct.pack("<IQQ", 3, len(tensors), len(kv))
-    for k, (vt, v) in kv.items():
-        out += s(k) + struct.pack("<I", vt)
-        if vt == 8:
-            out += s(v)
-        elif vt == 9:
-            out += struct.pack("<IQ", 4, len(v)) + b"".join(struct.pack("<I", e) for e in v)
-        else:
-            out += struct.pack({4: "<I", 6: "<f", 10: "<Q"}[vt], v)
-    blobs, off = [], 0
-    for name, (gtype, arr) in tensors.items():
-        out += s(name) + struct.pack("<I", arr.ndim) + struct.pack(f"<{arr.ndim}Q", *reversed(arr.shape))
-        out += struct.pack("<IQ", gtype, off)
-        blob = arr.tobytes()
-        pad = (-len(blob)) % align
-        blobs.append(blob + b"\0" * pad)
-        off += len(blob) + pad
-    out += b"\0" * ((-len(out)) % align)
-    return out + b"".join(blobs)
-
-
 def test_gguf_round_trip(F, tmp_path):
     rng = np.random.default_rng(3)
     w = rng.normal(size=(40, 27 * 16)).astype(np.float32)
@@ -90,7 +66,7 @@ def test_gguf_round_trip(F, tmp_path):
     kv = {"general.architecture": (8, "sam3d"), "meshdec.resolution": (4, 256),
           "meshdec.mlp_ratio": (6, 4.0), "general.alignment": (4, 32), "list": (9, [1, 2, 3])}
     path = tmp_path / "m.gguf"
-    path.write_bytes(_gguf_bytes(kv, {"slat.conv.weight": (0, w), "meshdec.conv.weight": (1, h),
+    path.write_bytes(gguf_bytes(kv, {"slat.conv.weight": (0, w), "meshdec.conv.weight": (1, h),
                                       "b": (30, bf_bits), "ids": (26, ids)}))
     g = F.GgufFile(path)
     assert g.version == 3 and g.kv["general.architecture"] == "sam3d" and g.kv["list"] == [1, 2, 3]

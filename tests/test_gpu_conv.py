@@ -5,7 +5,7 @@ on the BF16-rounded inputs and weights."""
 import numpy as np
 import pytest
 
-from helpers import rel_l2
+from helpers import check_rel, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -56,7 +56,7 @@ def test_linear_layer_lane_layout(s3dx, W, dtype, cin, cout):
     got = gpu_conv(s3dx, x, None, n, w, s3dx.WEIGHT_SLAT, b, dtype, cout, kvol=1)
     xr, wr = rnd(s3dx, x, dtype), rnd(s3dx, w, dtype)
     ref = xr.astype(np.float64) @ wr[:, 0, :].T.astype(np.float64) + b
-    assert rel_l2(got, ref) <= TOL[dtype] / (10 if dtype == 0 else 1)
+    check_rel(got, ref, TOL[dtype] / (10 if dtype == 0 else 1))
 
 
 @pytest.mark.parametrize("dtype", [0, 1])
@@ -72,7 +72,7 @@ def test_subm_conv_matches_oracle(s3dx, O, W, dtype, cin, cout):
     b = W.normal_f32(4, 3, (cout,), 0.5)
     got = gpu_conv(s3dx, x, kmap, n, w, s3dx.WEIGHT_SLAT, b, dtype, cout)
     ref = O.conv(rnd(s3dx, x, dtype), kmap, n, rnd(s3dx, w, dtype), 0, cout, b)
-    assert rel_l2(got, ref) <= TOL[dtype]
+    check_rel(got, ref, TOL[dtype])
 
 
 def test_config1_fp32_conv(s3dx, O, W):
@@ -84,7 +84,7 @@ def test_config1_fp32_conv(s3dx, O, W):
     b = np.zeros(64, np.float32)
     got = gpu_conv(s3dx, x, kmap, n, w, s3dx.WEIGHT_SLAT, b, s3dx.F32, 64)
     ref = O.conv(x, kmap, n, w, 0, 64, b)
-    assert rel_l2(got, ref) <= 1e-5
+    check_rel(got, ref, 1e-5)
 
 
 @pytest.mark.parametrize("dtype", [0, 1])
@@ -98,7 +98,7 @@ def test_mesh_layout_minus_one_sentinel(s3dx, O, W, dtype):
     b = W.normal_f32(5, 3, (cout,))
     got = gpu_conv(s3dx, x, kmap, n, w, s3dx.WEIGHT_MESH, b, dtype, cout)
     ref = O.conv(rnd(s3dx, x, dtype), kmap, n, rnd(s3dx, w, dtype), 1, cout, b)
-    assert rel_l2(got, ref) <= TOL[dtype]
+    check_rel(got, ref, TOL[dtype])
 
 
 @pytest.mark.parametrize("dtype", [0, 1])
@@ -134,7 +134,7 @@ def test_gather_parent_slot_offset_and_input_affine(s3dx, O, W, dtype, cin, cout
     xc = O.repeat_children(xr) + (np.tile(slot, (p, 1)) if slot_on else 0.0)
     act = O.silu(xc * scale + shift) if affine_on else xc
     ref = O.conv(rnd(s3dx, act, dtype), kmap, n, rnd(s3dx, w, dtype), 1, cout, b)
-    assert rel_l2(got, ref) <= TOL[dtype] * (2 if dtype == 0 else 1)
+    check_rel(got, ref, TOL[dtype])
 
 
 @pytest.mark.parametrize("dtype", [0, 1])
@@ -163,7 +163,7 @@ def test_residual_at_parent_resolution(s3dx, O, W, dtype, cout, ln):
     if ln:
         h = O.silu(O.layernorm(h, 1e-6))
     ref = h + O.repeat_children(rnd(s3dx, res, dtype))
-    assert rel_l2(got, ref) <= TOL[dtype] * (3 if dtype == 0 else 1)
+    check_rel(got, ref, TOL[dtype])
 
 
 @pytest.mark.parametrize("dtype", [0, 1])
@@ -196,7 +196,7 @@ def test_linear_kernel(s3dx, O, W, dtype, cin, cout, n, parent, res_parent, silu
         h = O.silu(h)
     rr = rnd(s3dx, res, dtype)
     ref = h + (O.repeat_children(rr)[:n] if res_parent else rr)
-    assert rel_l2(got, ref) <= TOL[dtype] * (2 if dtype == 0 else 1)
+    check_rel(got, ref, TOL[dtype])
 
 
 def test_transform_buffer_regrows(s3dx, O, W):
@@ -221,7 +221,7 @@ def test_transform_buffer_regrows(s3dx, O, W):
         got = W.bf16_bits_to_f32(h).reshape(h.shape)
         xc = O.repeat_children(rnd(s3dx, xp, dtype)) + np.tile(slot, (p, 1))
         ref = O.conv(rnd(s3dx, xc, dtype), kmap, n, rnd(s3dx, w, dtype), 1, cout, None)
-        assert rel_l2(got, ref) <= TOL[dtype]
+        check_rel(got, ref, TOL[dtype])
 
 
 @pytest.mark.parametrize("dtype", [0, 1])
@@ -247,7 +247,7 @@ def test_layernorm_modulate_silu_residual_epilogue(s3dx, O, W, dtype, cout):
     got = gpu_conv(s3dx, x, kmap, n, w, s3dx.WEIGHT_SLAT, b, dtype, cout, residual=res, setup=setup)
     h = O.conv(rnd(s3dx, x, dtype), kmap, n, rnd(s3dx, w, dtype), 0, cout, b)
     ref = O.silu(O.modulate(O.layernorm(h, 1e-6, lw, lb), ms, mh)) + rnd(s3dx, res, dtype)
-    assert rel_l2(got, ref) <= TOL[dtype] * (3 if dtype == 0 else 1)
+    check_rel(got, ref, TOL[dtype])
 
 
 def test_output_dtype_cross(s3dx, O, W):
@@ -260,10 +260,10 @@ def test_output_dtype_cross(s3dx, O, W):
     b = W.normal_f32(8, 3, (128,))
     ref = O.conv(W.round_bf16(x), kmap, n, W.round_bf16(w), 0, 128, b)
     got = gpu_conv(s3dx, x, kmap, n, w, 0, b, s3dx.BF16, 128, y_dtype=s3dx.F32)
-    assert rel_l2(got, ref) <= 1e-2
+    check_rel(got, ref, 1e-2)
     ref32 = O.conv(x, kmap, n, w, 0, 128, b)
     got2 = gpu_conv(s3dx, x, kmap, n, w, 0, b, s3dx.F32, 128, y_dtype=s3dx.BF16)
-    assert rel_l2(got2, ref32) <= 1e-2
+    check_rel(got2, ref32, 1e-2)
 
 
 def test_deterministic_and_empty_rows(s3dx, O, W):
@@ -309,7 +309,7 @@ def test_row_block_tilings(s3dx, O, W, monkeypatch, dtype, cin, cout, tiling):
     got = gpu_conv(s3dx, x, kmap, n, w, s3dx.WEIGHT_SLAT, b, dtype, cout, residual=res, setup=setup)
     h = O.conv(rnd(s3dx, x, dtype), kmap, n, rnd(s3dx, w, dtype), 0, cout, b)
     ref = O.silu(O.layernorm(h, 1e-6)) + rnd(s3dx, res, dtype)
-    assert rel_l2(got, ref) <= TOL[dtype] * (3 if dtype == 0 else 1)
+    check_rel(got, ref, TOL[dtype])
 
 
 @pytest.mark.parametrize("cin,cout,tiling,kvol", [
@@ -341,7 +341,7 @@ def test_subtask_tilings(s3dx, O, W, monkeypatch, cin, cout, tiling, kvol):
     got = gpu_conv(s3dx, x, kmap, n, w, s3dx.WEIGHT_SLAT, b, dtype, cout, kvol=kvol, residual=res, setup=setup)
     h = O.conv(rnd(s3dx, x, dtype), kmap, n, rnd(s3dx, w, dtype), 0, cout, b, kvol=kvol)
     ref = O.silu(O.layernorm(h, 1e-6)) + rnd(s3dx, res, dtype)
-    assert rel_l2(got, ref) <= TOL[dtype]
+    check_rel(got, ref, TOL[dtype])
 
 
 @pytest.mark.parametrize("cin,cout,kvol,dtype,with_res", [
@@ -370,7 +370,7 @@ def test_padded_cout(s3dx, O, W, cin, cout, kvol, dtype, with_res):
     ref = O.conv(rnd(s3dx, x, dtype), kmap, n, rnd(s3dx, w, dtype), 0, cout, b, kvol=kvol)
     if with_res:
         ref = ref + rnd(s3dx, res, dtype)
-    assert rel_l2(got, ref) <= TOL[dtype]
+    check_rel(got, ref, TOL[dtype])
 
 
 @pytest.mark.gpu
@@ -394,7 +394,7 @@ def test_centre_column_not_identity(s3dx, O, W, dtype):
         print(f"centre test {name} dtype={dtype} n={n}", flush=True)
         got = gpu_conv(s3dx, x, kmap, n, w, s3dx.WEIGHT_SLAT, b, dtype, 128)
         ref = O.conv(rnd(s3dx, x, dtype), kmap, n, rnd(s3dx, w, dtype), 0, 128, b)
-        assert rel_l2(got, ref) <= TOL[dtype], name
+        check_rel(got, ref, TOL[dtype], name)
 
 
 @pytest.mark.parametrize("cin,cout,kvol,n,plan", [
@@ -465,4 +465,4 @@ def test_bf16_rows_three_term_epilogue(s3dx, W, y_dtype, cin, cout, p):
     h = W.bf16_bits_to_f32(xb).astype(np.float64) @ w.reshape(cout, cin).astype(np.float64).T + b
     h = h / (1.0 + np.exp(-h)) + res
     ref = np.repeat(h, 8, axis=0)
-    assert rel_l2(got, ref) <= (1e-6 if y_dtype == s3dx.F32 else 4e-3)
+    check_rel(got, ref, 1e-6 if y_dtype == s3dx.F32 else 4e-3)

@@ -7,6 +7,8 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
+from helpers import prune_brute_force, prune_cases
+
 pytestmark = pytest.mark.gpu
 
 
@@ -106,3 +108,13 @@ def test_coords_from_occupancy_pipeline(s3dx, O, golden):
     want = O.downsample_coords(O.prune_surface(O.occupancy_coords(occ)))
     print(f"pipeline rows={n}", flush=True)
     assert np.array_equal(_rows(coords, n), want)
+
+
+@pytest.mark.parametrize("case", ["blobs_two_batches_duplicates", "solid_cube", "negative_cube", "key_aliasing"])
+def test_prune_surface_brute_force_cases(s3dx, case):
+    # The GPU prune against the independent brute force (coordinate_key
+    # aliasing, negative coordinates, batches and duplicated rows).
+    c = prune_cases()[case]
+    n, surf = s3dx.prune_surface(s3dx.DeviceArray.from_host(c), c.shape[0])
+    print(f"prune {case} n={c.shape[0]} -> {n}", flush=True)
+    assert np.array_equal(_rows(surf, n), prune_brute_force(c))

@@ -3,7 +3,7 @@ down/upsample, conversions) against the oracle."""
 import numpy as np
 import pytest
 
-from helpers import rel_l2
+from helpers import check_rel, rel_l2
 
 pytestmark = pytest.mark.gpu
 
@@ -22,12 +22,12 @@ def test_layernorm_rows(s3dx, O, W, c):
     s3dx.layernorm_rows(dev(s3dx, x), s3dx.F32, n, c, 1e-6, dev(s3dx, w), dev(s3dx, b),
                         dev(s3dx, ms), dev(s3dx, mh), True, y, s3dx.F32)
     ref = O.silu(O.modulate(O.layernorm(x, 1e-6, w, b), ms, mh))
-    assert rel_l2(y.download(), ref) <= 1e-5
+    check_rel(y.download(), ref, 1e-5)
     # bf16 in, bf16 out, in place, no affine
     xb = dev(s3dx, W.f32_to_bf16_bits(x))
     s3dx.layernorm_rows(xb, s3dx.BF16, n, c, 1e-6)
     got = W.bf16_bits_to_f32(xb.download()).reshape(n, c)
-    assert rel_l2(got, O.layernorm(W.round_bf16(x), 1e-6)) <= 1e-2
+    check_rel(got, O.layernorm(W.round_bf16(x), 1e-6), 1e-2)
 
 
 @pytest.mark.parametrize("n,c,groups,mean,std", [
@@ -47,7 +47,7 @@ def test_groupnorm_stats_and_affine(s3dx, O, W, n, c, groups, mean, std):
     y = s3dx.DeviceArray((n, c), np.float32)
     s3dx.affine_rows(dx, s3dx.F32, n, c, scale, shift, True, y, s3dx.F32)
     ref = O.silu(O.groupnorm(x, groups, 1e-5, g, b))
-    assert rel_l2(y.download(), ref) <= 1e-5
+    check_rel(y.download(), ref, 1e-5)
 
 
 @pytest.mark.parametrize("n,c", [(30000, 768), (100000, 96), (999, 40)])
@@ -60,7 +60,7 @@ def test_groupnorm_stats_bf16_input(s3dx, O, W, n, c):
     y = s3dx.DeviceArray((n, c), np.float32)
     s3dx.affine_rows(dx, s3dx.BF16, n, c, scale, shift, False, y, s3dx.F32)
     ref = O.groupnorm(x, 8, 1e-5, g, b)
-    assert rel_l2(y.download(), ref) <= 1e-5
+    check_rel(y.download(), ref, 1e-5)
 
 
 @pytest.mark.parametrize("dtype,c", [(0, 64), (1, 64), (1, 128), (0, 20), (1, 20), (0, 6)])

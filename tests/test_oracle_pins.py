@@ -5,7 +5,7 @@ forms / library routines for what those leave open."""
 import numpy as np
 import pytest
 
-from helpers import SMALL, large_sets, rel_l2, sha
+from helpers import SMALL, large_sets, prune_brute_force, prune_cases, rel_l2, sha
 
 
 # ---- kernel maps, coarse tables, subdivide: reference golden vectors -------
@@ -55,6 +55,30 @@ def test_real_occupancy_counts(O, golden):
     assert sha(coords) == manifest["ss_occ"]["occupied_sha256"]
     assert sha(surface) == manifest["ss_occ"]["surface_sha256"]
     assert (coords.shape[0], surface.shape[0]) == (69537, 67783)
+
+
+@pytest.mark.parametrize("case", ["blobs_two_batches_duplicates", "solid_cube", "negative_cube", "key_aliasing"])
+def test_prune_surface_brute_force(O, case):
+    c = prune_cases()[case]
+    want = prune_brute_force(c)
+    got = O.prune_surface(c)
+    assert np.array_equal(got, want), case
+    if case == "solid_cube":
+        assert got.shape[0] == 7 ** 3 - 5 ** 3
+    if case == "key_aliasing":
+        assert not any(np.array_equal(r, [0, 6, 6, 6]) for r in got)  # its +x neighbour aliases in
+        assert any(np.array_equal(r, [0, 5, 6, 6]) for r in got)
+
+
+def test_prune_surface_fixture_brute_force(O, golden):
+    # The reference's ss_occ_f32.samt occupancy: the oracle's surface set must
+    # equal the brute force, row for row (67,783 of 69,537 occupied cells).
+    arrays, _ = golden
+    occ = np.unpackbits(arrays["ss_occ.bits"]).reshape(64, 64, 64).astype(np.float32)
+    coords = O.occupancy_coords(occ)
+    want = prune_brute_force(coords)
+    assert want.shape[0] == 67783
+    assert np.array_equal(O.prune_surface(coords), want)
 
 
 # ---- downsample_coords (session.cpp:168-233) ---------------------------------
