@@ -110,6 +110,20 @@ S3DX_API s3dx_status s3dx_kmap_subm3(const int32_t *coords, int64_t n, int32_t m
                                      int32_t *kmap, void *workspace, uint64_t workspace_bytes,
                                      s3dx_stream stream, char *error, uint64_t error_capacity);
 
+/* s3dx_kmap_subm3 without a workspace and without any allocation.  No
+ * counterpart in the reference: it is for callers that cannot allocate --
+ * code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc.  The hash table lives in a static device array of the library
+ * (8 MiB + 256 bytes on each GPU it runs on, held until the process ends),
+ * so n is limited to 262144 voxels (S3DX_INVALID_ARGUMENT above that).  Same
+ * kernels and results as s3dx_kmap_subm3; the table is cleared by a kernel
+ * at the start of every call.  All calls on one GPU share that array:
+ * calls that overlap in time on one GPU (different streams, threads) race
+ * and must be serialized by the caller. */
+S3DX_API s3dx_status s3dx_kmap_subm3_static(const int32_t *coords, int64_t n, int32_t missing_value,
+                                            int32_t *kmap, s3dx_stream stream, char *error,
+                                            uint64_t error_capacity);
+
 /* Workspace bytes for s3dx_coarsen2 on n fine voxels (host query). */
 S3DX_API s3dx_status s3dx_coarsen2_workspace_size(int64_t n, uint64_t *bytes, char *error,
                                                   uint64_t error_capacity);

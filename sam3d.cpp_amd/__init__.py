@@ -60,6 +60,7 @@ SIGNATURES = {
     "s3dx_event_elapsed_ms": (_u32, [_vp, _vp, C.POINTER(_f32)], True),
     "s3dx_kmap_workspace_size": (_u32, [_i64, C.POINTER(_u64)], True),
     "s3dx_kmap_subm3": (_u32, [_vp, _i64, _i32, _vp, _vp, _u64, _vp], True),
+    "s3dx_kmap_subm3_static": (_u32, [_vp, _i64, _i32, _vp, _vp], True),
     "s3dx_coarsen2_workspace_size": (_u32, [_i64, C.POINTER(_u64)], True),
     "s3dx_coarsen2": (_u32, [_vp, _i64, _vp, _vp, _vp, _vp, C.POINTER(_i64), _vp, _u64, _vp], True),
     "s3dx_occupancy_workspace_size": (_u32, [_i32, _i32, _i32, C.POINTER(_u64)], True),
@@ -260,6 +261,16 @@ def kmap_subm3(coords: DeviceArray, n: int, missing: int, kmap: DeviceArray = No
         workspace = DeviceArray(kmap_workspace_size(n), np.uint8)
     call("s3dx_kmap_subm3", _dptr(coords), _i64(n), _i32(missing), _dptr(kmap), _dptr(workspace),
          _u64(workspace.nbytes), _sptr(stream))
+    return kmap
+
+
+def kmap_subm3_static(coords: DeviceArray, n: int, missing: int, kmap: DeviceArray = None,
+                      stream=None) -> DeviceArray:
+    """kmap_subm3 with the library's static table: no workspace, no allocation
+    in the library (n <= 262144; calls overlapping on one GPU race)."""
+    if kmap is None:
+        kmap = DeviceArray((n, 27), np.int32)
+    call("s3dx_kmap_subm3_static", _dptr(coords), _i64(n), _i32(missing), _dptr(kmap), _sptr(stream))
     return kmap
 
 

@@ -135,7 +135,7 @@ __device__ __forceinline__ void block_bounds_atomic(int (&v)[2 * M], int32_t *ou
     }
 }
 
-uint64_t hash_capacity(int64_t n) {
+constexpr uint64_t hash_capacity(int64_t n) {
     uint64_t cap = 256;
     while (cap < static_cast<uint64_t>(n) * 8) cap <<= 1;
     return cap;

@@ -10,6 +10,7 @@
 // std::map::emplace's "first occurrence wins" does.
 #include "coord_hash.hpp"
 
+#include <mutex>
 #include <vector>
 
 namespace s3dx {
@@ -249,6 +250,31 @@ void run_kmap(const int4 *coords, int32_t n, int32_t missing, int32_t *kmap, Has
     launch_check("kmap_lookup");
 }
 
+// Allocation-free kernel maps: the hash table lives in `scratch`, one array
+// per device for the life of the process, sized for kStaticKmapMaxVoxels.
+constexpr int64_t kStaticKmapMaxVoxels = int64_t(1) << 18;
+constexpr uint64_t kStaticKmapBytes =
+    (hash_capacity(kStaticKmapMaxVoxels) * 4 + 255) / 256 * 256 + (64 * 4 + 255) / 256 * 256;
+static __device__ __align__(256) unsigned char scratch[kStaticKmapBytes];
+
+// The device address of `scratch` on the current device, looked up once per
+// device (the array's name in host code is only a stand-in).
+void *static_scratch() {
+    constexpr int kMaxDevices = 64;
+    static std::mutex lock;
+    static void *addr[kMaxDevices] = {};
+    int dev = 0;
+    hip_check(hipGetDevice(&dev), "hipGetDevice");
+    require(dev >= 0 && dev < kMaxDevices, "device index out of range");
+    std::lock_guard<std::mutex> g(lock);
+    if (addr[dev] == nullptr) {
+        void *p = nullptr;
+        hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+        addr[dev] = p;
+    }
+    return addr[dev];
+}
+
 void check_coords(const int32_t *coords, int64_t n) {
     require(coords != nullptr, "coords is NULL");
     require(aligned(coords, 16), "coords must be 16-byte aligned");
@@ -352,6 +378,20 @@ S3DX_API s3dx_status s3dx_kmap_subm3(const int32_t *coords, int64_t n, int32_t m
     });
 }
 
+S3DX_API s3dx_status s3dx_kmap_subm3_static(const int32_t *coords, int64_t n, int32_t missing_value,
+                                            int32_t *kmap, s3dx_stream stream, char *error,
+                                            uint64_t error_capacity) {
+    return boundary(error, error_capacity, [&] {
+        check_coords(coords, n);
+        require(kmap != nullptr, "kmap is NULL");
+        require(n <= kStaticKmapMaxVoxels, "voxel count exceeds the static table's maximum (262144)");
+        Carver w(static_scratch(), kStaticKmapBytes);
+        Hash h;
+        kmap_layout(w, n, &h);
+        run_kmap(reinterpret_cast<const int4 *>(coords), static_cast<int32_t>(n), missing_value, kmap, h,
+                 as_stream(stream));
+    });
+}
 
 S3DX_API s3dx_status s3dx_subdivide2_workspace_size(int64_t parent_count, uint64_t *bytes,
                                                     char *error, uint64_t error_capacity) {

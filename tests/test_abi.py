@@ -167,3 +167,10 @@ def test_linear_layer_rejects_rows_past_the_input(s3dx):
     conv.plan(100, 800)
     with pytest.raises(s3dx.S3dxError, match="n_out exceeds"):
         conv.plan(100, 801)
+
+
+def test_static_kmap_rejects_sets_above_its_table(s3dx):
+    # Checked before any device work: the static table holds 262144 voxels.
+    st, msg = _status(s3dx, "s3dx_kmap_subm3_static", C.c_void_p(0x1000), C.c_int64(262145), C.c_int32(-1),
+                      C.c_void_p(0x2000), C.c_void_p(None))
+    assert st == s3dx.INVALID_ARGUMENT and "262144" in msg
