@@ -301,6 +301,31 @@ S3DX_API s3dx_status s3dx_conv_run(const s3dx_conv *conv, const void *x, int64_t
                                    const int32_t *kmap, int64_t n_out, const void *residual,
                                    void *y, int32_t y_dtype, s3dx_stream stream, char *error,
                                    uint64_t error_capacity);
+/* Gather plans.  No counterpart in the reference, whose GGML graph gathers
+ * im2col rows afresh in every forward (slat_flow_graph.cpp:116-130).  A plan
+ * holds, for each 64-row tile of a kernel map, the distinct source rows its
+ * 27 offsets name and the table the halo-staged kernel gathers them by --
+ * work that otherwise opens every such launch.  It depends only on the map
+ * and on how `conv` reads its input (n_in rows, parent rows or transformed
+ * rows), so build it once per map (as the reference builds its tables once
+ * per sample, session.cpp:1563-1566) and pass it to every
+ * s3dx_conv_run_planned over that map by layers set up alike (e.g. both
+ * convs of a res_block).  The caller keeps kmap unchanged while the plan is
+ * in use.  create enqueues the build on `stream` (device memory: 7 KiB per
+ * 64 output rows); free releases it. */
+typedef struct s3dx_gather_plan s3dx_gather_plan;
+S3DX_API s3dx_status s3dx_gather_plan_create(const s3dx_conv *conv, int64_t n_in, const int32_t *kmap,
+                                             int64_t n_out, s3dx_stream stream, s3dx_gather_plan **out,
+                                             char *error, uint64_t error_capacity);
+S3DX_API void s3dx_gather_plan_free(s3dx_gather_plan *plan);
+/* s3dx_conv_run with a gather plan built for the same kmap, n_out and source
+ * rows (S3DX_INVALID_ARGUMENT when the sizes or the source setup differ).
+ * Results are bit-identical to s3dx_conv_run; launches that do not use the
+ * halo kernel ignore the plan. */
+S3DX_API s3dx_status s3dx_conv_run_planned(const s3dx_conv *conv, const s3dx_gather_plan *plan, const void *x,
+                                           int64_t n_in, const int32_t *kmap, int64_t n_out, const void *residual,
+                                           void *y, int32_t y_dtype, s3dx_stream stream, char *error,
+                                           uint64_t error_capacity);
 /* Describes, as one line of text, the kernel variant s3dx_conv_run launches
  * for n_in input and n_out output rows (buffers assumed 16-byte aligned),
  * e.g. "mfma tiling=11 split-k rows=128 cols=128 kc=128 xf=0 ln=fused

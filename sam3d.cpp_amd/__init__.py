@@ -84,6 +84,9 @@ SIGNATURES = {
     "s3dx_conv_set_input_dtype": (_u32, [_vp, _i32], True),
     "s3dx_conv_run": (_u32, [_vp, _vp, _i64, _vp, _i64, _vp, _vp, _i32, _vp], True),
     "s3dx_conv_plan": (_u32, [_vp, _i64, _i64, C.c_char_p, _u64], True),
+    "s3dx_gather_plan_create": (_u32, [_vp, _i64, _vp, _i64, _vp, C.POINTER(_vp)], True),
+    "s3dx_gather_plan_free": (None, [_vp], False),
+    "s3dx_conv_run_planned": (_u32, [_vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _i32, _vp], True),
     "s3dx_layernorm_rows": (_u32, [_vp, _i32, _i64, _i32, _f32, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp], True),
     "s3dx_groupnorm_workspace_size": (_u32, [_i64, _i32, _i32, C.POINTER(_u64)], True),
     "s3dx_groupnorm_stats": (_u32, [_vp, _i32, _i64, _i32, _i32, _f32, _vp, _vp, _vp, _vp, _vp, _u64, _vp], True),
@@ -500,17 +503,44 @@ class SparseConv:
         call("s3dx_conv_plan", _vp(self.handle), _i64(n_in), _i64(n_out), buf, len(buf))
         return buf.value.decode()
 
+    def gather_plan(self, n_in: int, kmap, n_out: int, stream=None) -> "GatherPlan":
+        """The map's gather plan for this layer's source rows (s3dx_gather_plan_create)."""
+        return GatherPlan(self, n_in, kmap, n_out, stream)
+
     def run(self, x: DeviceArray, n_in: int, kmap, n_out: int, y: DeviceArray, y_dtype: int = None,
-            residual: DeviceArray = None, stream=None):
+            residual: DeviceArray = None, stream=None, plan: "GatherPlan" = None):
         yd = self.dtype if y_dtype is None else y_dtype
-        call("s3dx_conv_run", _vp(self.handle), _dptr(x), _i64(n_in), _dptr(kmap), _i64(n_out),
-             _dptr(residual), _dptr(y), _i32(yd), _sptr(stream))
+        if plan is None:
+            call("s3dx_conv_run", _vp(self.handle), _dptr(x), _i64(n_in), _dptr(kmap), _i64(n_out),
+                 _dptr(residual), _dptr(y), _i32(yd), _sptr(stream))
+        else:
+            call("s3dx_conv_run_planned", _vp(self.handle), _vp(plan.handle), _dptr(x), _i64(n_in), _dptr(kmap),
+                 _i64(n_out), _dptr(residual), _dptr(y), _i32(yd), _sptr(stream))
         return y
 
     def __del__(self):
         try:
             if self.handle:
                 lib().s3dx_conv_free(_vp(self.handle))
+        except Exception:
+            pass
+
+
+class GatherPlan:
+    """A kernel map's per-tile gather plan (s3dx_gather_plan): built once per map,
+    passed to every run over that map by layers that read their input alike."""
+
+    def __init__(self, conv: SparseConv, n_in: int, kmap, n_out: int, stream=None):
+        p = _vp()
+        call("s3dx_gather_plan_create", _vp(conv.handle), _i64(n_in), _dptr(kmap), _i64(n_out), _sptr(stream),
+             C.byref(p))
+        self.handle = p.value
+        self._kmap = kmap
+
+    def __del__(self):
+        try:
+            if self.handle:
+                lib().s3dx_gather_plan_free(_vp(self.handle))
         except Exception:
             pass
 

@@ -120,6 +120,15 @@ __host__ __device__ inline uint16_t f32_to_bf16(float f) {
     return static_cast<uint16_t>(u >> 16);
 }
 
+// Two floats as packed bfloat16 (lo in bits 0-15), each rounded to nearest
+// even: one v_cvt_pk_bf16_f32 on gfx950 (f32_to_bf16 is the same rounding,
+// written out for the host and for single elements).
+__device__ inline uint32_t pack_bf16x2(float lo, float hi) {
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const bf16x2_t v = {static_cast<__bf16>(lo), static_cast<__bf16>(hi)};
+    return __builtin_bit_cast(uint32_t, v);
+}
+
 template <class T>
 __device__ inline float load_as_f32(const T *p);
 template <>

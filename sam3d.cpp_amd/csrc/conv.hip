@@ -301,10 +301,23 @@ struct s3dx_conv {
     }
 };
 
+// A kernel map's gather plan (per 64-row tile: the distinct source rows and
+// the slot table the halo kernel stages them by), for the source rows of one
+// layer setup.
+struct s3dx_gather_plan {
+    void *d = nullptr;
+    int64_t n_out = 0, n_src = 0;
+    int32_t shift = 0;
+    ~s3dx_gather_plan() {
+        if (d) (void)hipFree(d);
+    }
+};
+
 namespace s3dx {
 namespace {
 
 KernelFn tiling_kernel(int id, bool bf, int kc, bool xf) {
+    if (id == 20 || id == 21) return bf && kc == 64 && !xf ? pick_halo_bf16(id == 20 ? 128 : 64) : nullptr;
     return bf ? pick_mfma_bf16(id, kc, xf) : pick_mfma_f32(id, kc, xf);
 }
 
@@ -547,6 +560,26 @@ LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bo
                     }
                     p = best;
                 }
+            }
+        }
+        // The halo-staged kernels for BF16 3x3x3 layers whose channels come
+        // in 64-channel chunks and 128-column tiles: a tile stages each
+        // distinct source row once per chunk into LDS and reads every weight
+        // fragment once.  64-row tiles (tiling 21) by default, 128-row tiles
+        // (tiling 20) with S3DX_CONV_HALO=128; S3DX_CONV_TILING=<other id> or
+        // S3DX_CONV_HALO=0 keeps the kernels above (tuning, tests).
+        {
+            const char *te = std::getenv("S3DX_CONV_TILING");
+            const char *he = std::getenv("S3DX_CONV_HALO");
+            const int tid = te ? std::atoi(te) : 0;
+            const bool allowed = te ? (tid == 20 || tid == 21) : !(he && std::atoi(he) == 0);
+            if (allowed && bf && conv->kvol == kMaxKvol && conv->cin % 64 == 0 && blocks % 4 == 0 && !p.xf &&
+                splitk_ok && (!conv->ln || conv->cout == 128)) {
+                const int want = tid == 20 || tid == 21 ? tid : (he && std::atoi(he) == 128 ? 20 : 21);
+                for (const Tiling &t : kTilings)
+                    if (t.id == want) p.tl = &t;
+                p.nb = 4;
+                p.kc = 64;
             }
         }
         p.fused_ln = conv->ln && p.nb * 32 == conv->cout;
@@ -848,8 +881,9 @@ S3DX_API s3dx_status s3dx_conv_plan(const s3dx_conv *conv, int64_t n_in, int64_t
                           conv->cin / (conv->dtype == S3DX_BF16 || p.split ? 16 : 8),
                           p.split ? " terms=3" : "", conv->ln ? "separate" : "none", p.grid.x);
         else if (p.mfma)
-            std::snprintf(text, sizeof(text), "mfma tiling=%d%s rows=%d cols=%d kc=%d xf=%d ln=%s grid=%ux%u",
-                          p.tl->id, p.tl->splitk ? " split-k" : "", p.tl->rows(), p.tl->cols(), p.kc,
+            std::snprintf(text, sizeof(text), "mfma tiling=%d%s%s rows=%d cols=%d kc=%d xf=%d ln=%s grid=%ux%u",
+                          p.tl->id, p.tl->splitk ? " split-k" : "", p.tl->id >= 20 ? " halo" : "", p.tl->rows(),
+                          p.tl->cols(), p.kc,
                           p.xf ? 1 : 0, conv->ln ? (p.fused_ln ? "fused" : "separate") : "none", p.grid.x,
                           p.grid.y);
         else
@@ -861,11 +895,14 @@ S3DX_API s3dx_status s3dx_conv_plan(const s3dx_conv *conv, int64_t n_in, int64_t
     });
 }
 
-S3DX_API s3dx_status s3dx_conv_run(const s3dx_conv *conv, const void *x, int64_t n_in,
-                                   const int32_t *kmap, int64_t n_out, const void *residual,
-                                   void *y, int32_t y_dtype, s3dx_stream stream, char *error,
-                                   uint64_t error_capacity) {
-    return boundary(error, error_capacity, [&] {
+}  // extern "C"
+
+namespace {
+
+void conv_run_impl(const s3dx_conv *conv, const s3dx_gather_plan *gplan, const void *x, int64_t n_in,
+                   const int32_t *kmap, int64_t n_out, const void *residual, void *y, int32_t y_dtype,
+                   s3dx_stream stream) {
+    {
         require(conv != nullptr, "conv is NULL");
         require(conv->weights_set, "weights not set");
         require(x && y, "NULL feature pointer");
@@ -946,6 +983,15 @@ S3DX_API s3dx_status s3dx_conv_run(const s3dx_conv *conv, const void *x, int64_t
             plan = plan_launch(conv, a.x_bytes, n_out, aligned16);
         }
         if (plan.split) a.w = conv->w_split;
+        if (gplan) {
+            require(gplan->n_out == n_out && gplan->n_src == src.n_src && gplan->shift == src.shift,
+                    "gather plan was built for another map size or source rows");
+            // Only the 64-row halo kernel reads plans; other plans ignore it.
+            if (plan.mfma && plan.tl && plan.tl->id == 21 && !bf16_rows) {
+                a.plan = gplan->d;
+                plan.fn = pick_halo_bf16_planned();
+            }
+        }
         // A LayerNorm the epilogue cannot fuse runs as its own pass over the
         // conv's FP32 output (the layer's buffer), then modulate, SiLU and
         // the residual, rounded once to y_dtype as the fused epilogue does.
@@ -971,6 +1017,55 @@ S3DX_API s3dx_status s3dx_conv_run(const s3dx_conv *conv, const void *x, int64_t
             layernorm_rows_launch(conv->pre_ln, S3DX_F32, n_out, conv->cout, conv->eps, conv->ln_w, conv->ln_b,
                                   a.mod_scale, a.mod_shift, conv->silu ? 1 : 0, y, y_dtype, s, residual,
                                   conv->residual_parent ? 3 : 0);
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+S3DX_API s3dx_status s3dx_conv_run(const s3dx_conv *conv, const void *x, int64_t n_in,
+                                   const int32_t *kmap, int64_t n_out, const void *residual,
+                                   void *y, int32_t y_dtype, s3dx_stream stream, char *error,
+                                   uint64_t error_capacity) {
+    return boundary(error, error_capacity,
+                    [&] { conv_run_impl(conv, nullptr, x, n_in, kmap, n_out, residual, y, y_dtype, stream); });
+}
+
+S3DX_API s3dx_status s3dx_gather_plan_create(const s3dx_conv *conv, int64_t n_in, const int32_t *kmap,
+                                             int64_t n_out, s3dx_stream stream, s3dx_gather_plan **out,
+                                             char *error, uint64_t error_capacity) {
+    return boundary(error, error_capacity, [&] {
+        require(out != nullptr, "out is NULL");
+        *out = nullptr;
+        require(conv != nullptr && kmap != nullptr, "NULL argument");
+        require(conv->kvol == kMaxKvol, "gather plans are for 3x3x3 layers");
+        require(n_in > 0 && n_out > 0 && n_out <= INT32_MAX, "row counts out of range");
+        require(aligned(kmap, 16), "kmap must be 16-byte aligned");
+        const Source src = source_of(conv, n_in);
+        require(src.n_src <= INT32_MAX, "input rows exceed INT32_MAX");
+        const int64_t bytes = (n_out + kGatherPlanRows - 1) / kGatherPlanRows * kGatherPlanRecord;
+        require(bytes < (int64_t(1) << 31), "map too large for a gather plan");
+        auto p = std::make_unique<s3dx_gather_plan>();
+        hip_check(hipMalloc(&p->d, static_cast<size_t>(bytes)), "hipMalloc gather plan");
+        launch_gather_plan_build(kmap, n_out, src.n_src, src.shift, p->d, as_stream(stream));
+        launch_check("gather_plan_build");
+        p->n_out = n_out;
+        p->n_src = src.n_src;
+        p->shift = src.shift;
+        *out = p.release();
+    });
+}
+
+S3DX_API void s3dx_gather_plan_free(s3dx_gather_plan *plan) { delete plan; }
+
+S3DX_API s3dx_status s3dx_conv_run_planned(const s3dx_conv *conv, const s3dx_gather_plan *plan, const void *x,
+                                           int64_t n_in, const int32_t *kmap, int64_t n_out, const void *residual,
+                                           void *y, int32_t y_dtype, s3dx_stream stream, char *error,
+                                           uint64_t error_capacity) {
+    return boundary(error, error_capacity, [&] {
+        require(plan != nullptr, "plan is NULL");
+        conv_run_impl(conv, plan, x, n_in, kmap, n_out, residual, y, y_dtype, stream);
     });
 }
 

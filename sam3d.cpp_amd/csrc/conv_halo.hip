@@ -1,0 +1,597 @@
+// Halo-staged BF16 submanifold conv: one workgroup per 32*MB-row x 128-column
+// output tile, each distinct source row staged in LDS once per 64-channel
+// chunk.  Tiling 20: 128-row tiles, one workgroup per CU; tiling 21: 64-row
+// tiles, two workgroups per CU (one's prologue, halo copies, reduction and
+// epilogue overlap the other's MFMAs).
+//
+// Why: the split-K kernels gather every neighbour row for every offset (27
+// gathers per output row) and stream every weight fragment per workgroup:
+// about 48 KB of vector-memory reads per 16 MFMAs per SIMD, so the CU's
+// vector-memory path, not the MFMA pipes, sets their pace.  Here each distinct
+// source row is read once per chunk (~470 rows for 128 output rows, ~285 for
+// 64, on sphere-shell sets, against 27 gathers per row) and each weight
+// fragment goes straight from memory into the one wave that uses it.
+//
+// Workgroup: 4 waves, split-K.  Wave w owns the whole tile in accumulators
+// (MB x 4 blocks of 32 x 32) and k-step w (16 channels) of each 64-channel
+// chunk, for every present offset.  The task loop has no barrier: A
+// fragments come from the LDS halo (slot from a per-tile table), B fragments
+// from memory two tasks ahead.
+//
+// Prologue (per tile): the map slice is deduplicated with an LDS bitmap over
+// the range of source rows it names; a prefix count gives each distinct row
+// its halo slot (ascending row order), and a [27][rows] table of slots (a zero
+// row for missing neighbours) drives the gathers.  A slice whose rows span
+// more than the bitmap, or name more distinct rows than the halo holds, is
+// gathered from memory instead (same loop, 16-byte MFMA-order loads).
+//
+// Epilogue: the four partial tiles are summed through LDS in a fixed order
+// (deterministic) and finished row-major (bias, LayerNorm, modulate, SiLU,
+// residual) by the shared finish_rows.
+#include "conv_kernels.hpp"
+
+#include <type_traits>
+
+namespace s3dx {
+namespace {
+
+constexpr int kHChunk = 64;              // channels per halo chunk
+constexpr int kHRowBytes = kHChunk * 2;  // 128 bytes per halo row
+
+template <int MB>
+struct HaloSmem {
+    static constexpr int ROWS = 32 * MB;
+    static constexpr int RPH = MB == 4 ? 2 : 1;                  // row blocks reduced per phase
+    static constexpr int CAP = MB == 4 ? 1088 : 511;             // halo rows (slot CAP is the zero row)
+    static constexpr int BITWORDS = MB == 4 ? 1024 : 512;        // bitmap words (32 source rows each)
+    static constexpr int ENTRIES = ROWS * kMaxKvol;
+    static constexpr int STG_LD = 128 + 8;                       // padded FP32 output-tile row
+    static constexpr int HALO_BYTES = (CAP + 1) * kHRowBytes;
+    static constexpr int RED_BYTES = RPH * 4 * 4 * 4096;         // one reduction phase
+    static constexpr int STG_BYTES = ROWS * STG_LD * 4 + 2 * ROWS * 16 * 4;
+    static constexpr int R0A = HALO_BYTES > RED_BYTES ? HALO_BYTES : RED_BYTES;
+    static constexpr int REGION0 = R0A > STG_BYTES ? R0A : STG_BYTES;
+    static constexpr int TABLE_OFF = REGION0;
+    static constexpr int BITMAP_OFF = TABLE_OFF + (ENTRIES * 2 + 15) / 16 * 16;
+    static constexpr int PREFIX_OFF = BITMAP_OFF + BITWORDS * 4;
+    static constexpr int ROWS_OFF = PREFIX_OFF + BITWORDS * 4;
+    static constexpr int MISC_OFF = ROWS_OFF + (CAP * 4 + 15) / 16 * 16;
+    static constexpr int TOTAL = MISC_OFF + 64;
+    static_assert(TOTAL <= (MB == 4 ? 160 * 1024 : 80 * 1024), "LDS budget (two workgroups per CU for MB 2)");
+    // The global-gather mode keeps 32-bit source rows (or -1) in region0,
+    // which that mode does not use as a halo.
+    static_assert(ENTRIES * 4 <= REGION0, "32-bit table fits region0");
+};
+
+// Wave-wide reductions through DPP (each 16-lane row by rotations, then the
+// four rows by readlane); the result is wave-uniform.
+__device__ __forceinline__ int dpp_ror(int x, int n) {
+    switch (n) {
+    case 8: return __builtin_amdgcn_update_dpp(0, x, 0x128, 0xf, 0xf, false);
+    case 4: return __builtin_amdgcn_update_dpp(0, x, 0x124, 0xf, 0xf, false);
+    case 2: return __builtin_amdgcn_update_dpp(0, x, 0x122, 0xf, 0xf, false);
+    default: return __builtin_amdgcn_update_dpp(0, x, 0x121, 0xf, 0xf, false);
+    }
+}
+template <class Op>
+__device__ __forceinline__ int wave_reduce(int x, Op op) {
+    x = op(x, dpp_ror(x, 8));
+    x = op(x, dpp_ror(x, 4));
+    x = op(x, dpp_ror(x, 2));
+    x = op(x, dpp_ror(x, 1));
+    return op(op(__builtin_amdgcn_readlane(x, 0), __builtin_amdgcn_readlane(x, 16)),
+              op(__builtin_amdgcn_readlane(x, 32), __builtin_amdgcn_readlane(x, 48)));
+}
+
+// Exclusive prefix over the workgroup (256 threads) of one value each;
+// returns the prefix, writes the total to *total.  Every thread must call it.
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t *wave_sums, uint32_t *total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    uint32_t incl = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t t = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += t;
+    }
+    if (lane == 63) wave_sums[wave] = incl;
+    __syncthreads();
+    uint32_t base = 0;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) base += w < wave ? wave_sums[w] : 0u;
+    *total = wave_sums[0] + wave_sums[1] + wave_sums[2] + wave_sums[3];
+    return base + incl - v;
+}
+
+// Steps 1-4 of a tile's prologue: the tile's map slice deduplicated into LDS
+// -- the [27][ROWS] slot table (or, when the slice cannot be staged, the
+// 32-bit source-row table), the source row of every slot -- and the offset
+// mask.  Every thread of the workgroup must call it; ends with a barrier.
+struct TileDedupe {
+    uint32_t mask, distinct;
+    bool global_a;
+};
+template <int MB>
+__device__ __forceinline__ TileDedupe dedupe_tile(const int32_t *kmap, int64_t n_src, int32_t row_shift, int64_t m0,
+                                                  int tile_rows, uint16_t *table, int32_t *table32,
+                                                  uint32_t *bitmap, uint32_t *prefix, uint32_t *slot_row,
+                                                  int32_t *misc) {
+    using SM = HaloSmem<MB>;
+    constexpr int ROWS = SM::ROWS, CAP = SM::CAP, ENTRIES = SM::ENTRIES;
+    const int tid = threadIdx.x, lane = tid & 63;
+    // ---- 1. this tile's map slice (ROWS * 27 entries; 16-byte aligned,
+    // ROWS * 108 bytes per tile), as source rows (-1: missing)
+    constexpr int V4 = ENTRIES / 4;
+    constexpr int Q = (V4 + 255) / 256;
+    const int count = tile_rows * kMaxKvol;
+    int sj[Q][4];
+    {
+        const int4 *src = reinterpret_cast<const int4 *>(kmap + m0 * kMaxKvol);
+#pragma unroll
+        for (int q = 0; q < Q; ++q) {
+            const int u = tid + q * 256;
+            int4 v = make_int4(-1, -1, -1, -1);
+            if (u < V4) {
+                if (4 * u + 3 < count) {
+                    v = src[u];
+                } else {
+                    if (4 * u < count) v.x = kmap[m0 * kMaxKvol + 4 * u];
+                    if (4 * u + 1 < count) v.y = kmap[m0 * kMaxKvol + 4 * u + 1];
+                    if (4 * u + 2 < count) v.z = kmap[m0 * kMaxKvol + 4 * u + 2];
+                }
+            }
+            const int jv[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const bool valid = u < V4 && 4 * u + k < count && jv[k] >= 0 && jv[k] < n_src;
+                sj[q][k] = valid ? (jv[k] >> row_shift) : -1;
+            }
+        }
+    }
+    // ---- 2. range of named source rows and the offset mask
+    if (tid == 0) {
+        misc[0] = INT32_MAX;
+        misc[1] = INT32_MIN;
+        misc[2] = 0;
+    }
+    {
+        int lo = INT32_MAX, hi = INT32_MIN, m = 0;
+#pragma unroll
+        for (int q = 0; q < Q; ++q)
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (sj[q][k] >= 0) {
+                    lo = min(lo, sj[q][k]);
+                    hi = max(hi, sj[q][k]);
+                    m |= 1 << ((4 * (tid + q * 256) + k) % kMaxKvol);
+                }
+        lo = wave_reduce(lo, [](int x, int y) { return min(x, y); });
+        hi = wave_reduce(hi, [](int x, int y) { return max(x, y); });
+        m = wave_reduce(m, [](int x, int y) { return x | y; });
+        __syncthreads();
+        if (lane == 0) {
+            atomicMin(&misc[0], lo);
+            atomicMax(&misc[1], hi);
+            atomicOr(&misc[2], m);
+        }
+        __syncthreads();
+    }
+    const int rlo = misc[0], rhi = misc[1];
+    const uint32_t mask = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(misc[2]));
+    const int64_t span = rhi >= rlo ? static_cast<int64_t>(rhi) - rlo + 1 : 0;
+    bool global_a = span > static_cast<int64_t>(SM::BITWORDS) * 32;
+    uint32_t distinct = 0;
+    if (!global_a && span > 0) {
+        // ---- 3. bitmap of named rows -> slot = rank among them
+        const int words = static_cast<int>((span + 31) / 32);
+        for (int w = tid; w < words; w += 256) bitmap[w] = 0u;
+        __syncthreads();
+#pragma unroll
+        for (int q = 0; q < Q; ++q)
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (sj[q][k] >= 0) {
+                    const uint32_t r = static_cast<uint32_t>(sj[q][k] - rlo);
+                    atomicOr(&bitmap[r >> 5], 1u << (r & 31));
+                }
+        __syncthreads();
+        constexpr int WPT = SM::BITWORDS / 256;  // words per thread (4 or 2)
+        uint32_t cnt[WPT], mine = 0;
+#pragma unroll
+        for (int k = 0; k < WPT; ++k) {
+            const int w = tid * WPT + k;
+            cnt[k] = w < words ? static_cast<uint32_t>(__popc(bitmap[w])) : 0u;
+            mine += cnt[k];
+        }
+        uint32_t run = block_exclusive_scan(mine, reinterpret_cast<uint32_t *>(misc + 4), &distinct);
+#pragma unroll
+        for (int k = 0; k < WPT; ++k) {
+            const int w = tid * WPT + k;
+            if (w < words) prefix[w] = run;
+            run += cnt[k];
+        }
+        global_a = distinct > static_cast<uint32_t>(CAP);
+        __syncthreads();
+    }
+    // ---- 4. the slot (or, gathering from memory, the row) of every entry,
+    // and the source row of every slot
+#pragma unroll
+    for (int q = 0; q < Q; ++q)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int e = 4 * (tid + q * 256) + k;
+            if (e >= ENTRIES) continue;
+            const int r = e / kMaxKvol, o = e - r * kMaxKvol;
+            if (global_a) {
+                table32[o * ROWS + r] = sj[q][k];
+            } else {
+                uint32_t slot = CAP;
+                if (sj[q][k] >= 0) {
+                    const uint32_t d = static_cast<uint32_t>(sj[q][k] - rlo);
+                    const uint32_t bits = bitmap[d >> 5];
+                    slot = prefix[d >> 5] + static_cast<uint32_t>(__popc(bits & ((1u << (d & 31)) - 1u)));
+                    slot_row[slot] = static_cast<uint32_t>(sj[q][k]);  // writers of one slot agree
+                }
+                table[o * ROWS + r] = static_cast<uint16_t>(slot);
+            }
+        }
+    __syncthreads();
+    return TileDedupe{mask, distinct, global_a};
+}
+
+// Gather plans: one record per 64-row tile of a kernel map, the result of
+// dedupe_tile kept in memory so that every conv over the map skips it:
+//   [0, 16)     mode (0: halo, 1: global gathers), distinct rows, offset mask, 0
+//   [16, ...)   halo: the u16 slot table [27][64], then at kPlanSlots the
+//               source row of each slot; global: the int32 row table [27][64]
+constexpr int kPlanHeader = 16;
+constexpr int kPlanSlots = kPlanHeader + 64 * kMaxKvol * 2;  // 3472
+static_assert(kPlanSlots + HaloSmem<2>::CAP * 4 <= kGatherPlanRecord, "halo record fits");
+static_assert(kPlanHeader + 64 * kMaxKvol * 4 <= kGatherPlanRecord, "global record fits");
+static_assert(kGatherPlanRecord % 1024 == 0, "records copy as whole 1 KiB pieces");
+
+template <int MB, bool PLAN>
+struct HaloLds {
+    // Planned kernels keep region0 and the copied record; unplanned ones the
+    // dedupe buffers of HaloSmem.
+    static constexpr int TOTAL = PLAN ? HaloSmem<MB>::REGION0 + kGatherPlanRecord + 64 : HaloSmem<MB>::TOTAL;
+    static_assert(!PLAN || MB == 2, "plans are for 64-row tiles");
+    static_assert(TOTAL <= (MB == 4 ? 160 * 1024 : 80 * 1024), "LDS budget");
+};
+
+template <int MB, bool PLAN>
+__global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_halo_kernel(ConvArgs a) {
+    using SM = HaloSmem<MB>;
+    constexpr int ROWS = SM::ROWS, CAP = SM::CAP, RPH = SM::RPH;
+    __shared__ __align__(16) char smem[HaloLds<MB, PLAN>::TOTAL];
+    char *halo = smem;
+    char *rec = smem + SM::REGION0;  // the tile's plan record (planned kernels)
+    uint16_t *table = reinterpret_cast<uint16_t *>(PLAN ? rec + kPlanHeader : smem + SM::TABLE_OFF);
+    uint32_t *bitmap = reinterpret_cast<uint32_t *>(smem + SM::BITMAP_OFF);
+    uint32_t *prefix = reinterpret_cast<uint32_t *>(smem + SM::PREFIX_OFF);
+    uint32_t *slot_row = reinterpret_cast<uint32_t *>(PLAN ? rec + kPlanSlots : smem + SM::ROWS_OFF);
+    int32_t *misc = reinterpret_cast<int32_t *>(smem + SM::MISC_OFF);  // [0] lo, [1] hi, [2] mask, [4..7] scan
+    int32_t *table32 = reinterpret_cast<int32_t *>(PLAN ? rec + kPlanHeader : smem);  // global-gather mode
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int half = lane >> 5;
+    const int tile = xcd_tile(blockIdx.x, gridDim.x);
+    const int64_t m0 = static_cast<int64_t>(tile) * ROWS;
+    const int nb0 = blockIdx.y * 4;
+    const int nbtot = a.cout_pad / 32;
+    const int ksteps_total = a.cin / 16;
+    const int chunks = a.cin / kHChunk;
+    const int tile_rows = static_cast<int>(min(static_cast<int64_t>(ROWS), a.n_out - m0));
+    const int32_t xbytes = static_cast<int32_t>(a.x_bytes < INT32_MAX ? a.x_bytes : INT32_MAX);
+    const int64_t w_bytes = static_cast<int64_t>(kMaxKvol) * a.cin * a.cout_pad * 2;
+    const auto w_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(a.w), static_cast<short>(0),
+                                                          static_cast<int32_t>(w_bytes), 0x00020000);
+    const auto x_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(a.x), static_cast<short>(0),
+                                                          xbytes, 0x00020000);
+
+    TileDedupe dd;
+    if constexpr (PLAN) {
+        // The tile's plan record, straight into LDS: 1 KiB per instruction.
+        const int64_t plan_bytes = (a.n_out + 63) / 64 * kGatherPlanRecord;
+        const auto p_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(a.plan), static_cast<short>(0),
+                                                              static_cast<int32_t>(plan_bytes), 0x00020000);
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int i = wave + 4 * k;
+            if (i < kGatherPlanRecord / 1024)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(p_rsrc, (__attribute__((address_space(3))) void *)(rec + i * 1024),
+                                                         16, lane * 16, tile * kGatherPlanRecord + i * 1024, 0, 0);
+        }
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        __syncthreads();
+        const uint32_t *hdr = reinterpret_cast<const uint32_t *>(rec);
+        dd.global_a = __builtin_amdgcn_readfirstlane(hdr[0]) != 0;
+        dd.distinct = __builtin_amdgcn_readfirstlane(hdr[1]);
+        dd.mask = __builtin_amdgcn_readfirstlane(hdr[2]);
+    } else {
+        dd = dedupe_tile<MB>(a.kmap, a.n_src, a.row_shift, m0, tile_rows, table, table32, bitmap, prefix, slot_row,
+                             misc);
+    }
+    const uint32_t mask = dd.mask, distinct = dd.distinct;
+    const bool global_a = dd.global_a;
+    if (!global_a)
+        for (int i = tid; i < kHRowBytes / 16; i += 256)
+            reinterpret_cast<uint4 *>(halo + CAP * kHRowBytes)[i] = make_uint4(0, 0, 0, 0);
+    __syncthreads();
+
+    f32x16 acc[MB][4];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = f32x16{};
+
+    const int ntasks = __popc(mask);
+    // Fragment (k-step ks, column block cb) of the packed weights sits at
+    // byte ((ks * nbtot + cb) * 64 + lane) * 16; wave w keeps column block
+    // (k + w) mod 4 in accumulator column k, so the block it owns in the
+    // final reduction is always accumulator column 0.
+    int32_t bvo[4];
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) bvo[nb] = lane * 16 + ((nb + wave) & 3) * 1024;
+    // Offsets walked by scalar cursors; past the last one a cursor repeats
+    // it (prefetches beyond the end reload it harmlessly).  Offsets are
+    // below 27, so bit 31 is free: the ctz of rest | bit 31 is 31 exactly
+    // when rest is empty (testing rest itself beside rest - 1 would turn
+    // into a vector subtract and a readfirstlane).
+    const int olast = ntasks > 0 ? 31 - __builtin_clz(mask) : 0;
+    auto advance = [&](uint32_t &rest) __attribute__((always_inline)) {
+        const int c = __builtin_ctz(rest | 0x80000000u);
+        rest &= rest - 1u;
+        return c == 31 ? olast : c;
+    };
+    auto mfmas = [&](const uint4 (&af)[MB], const uint4 (&bf)[4]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = mfma_step<uint16_t>(af[mb], bf[nb], acc[mb][nb]);
+    };
+
+    // The chunk loop, for A from the halo (GA false) or from memory (GA
+    // true): one loop nest per mode, so the accumulators stay in place.
+    auto chunk_loop = [&](auto ga) __attribute__((always_inline)) {
+        constexpr bool GA = decltype(ga)::value;
+        for (int c = 0; c < chunks && ntasks > 0; ++c) {
+            const int ks = c * 4 + wave;  // this wave's k-step over the whole Cin
+            if constexpr (!GA) {
+                if (c > 0) __syncthreads();  // every wave is done with chunk c-1
+                // ---- 5. chunk c of every distinct row into its slot,
+                // straight from memory into LDS (no registers): one
+                // instruction fills 8 consecutive slots (1 KiB, lane L -> byte
+                // 16 L), so lane L loads piece (L % 8) ^ (slot % 8) of its
+                // slot's row -- the swizzle that spreads a gather of 32 slots
+                // over the banks.  Eight lanes read each 128-byte row chunk:
+                // whole cache lines.  Four groups per wave per round: their
+                // slot rows are read first, one LDS round trip for four copies.
+                const int groups = (static_cast<int>(distinct) + 7) >> 3;
+                for (int g0 = wave; g0 < groups; g0 += 16) {
+                    uint32_t off[4];
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const int s = (g0 + 4 * k) * 8 + (lane >> 3);
+                        const int p = (lane & 7) ^ (s & 7);
+                        off[k] = s < static_cast<int>(distinct)
+                                     ? (slot_row[min(s, CAP - 1)] * static_cast<uint32_t>(a.cin) + c * kHChunk +
+                                        p * 8) * 2u
+                                     : 0x80000000u;  // past the buffer: zeros
+                    }
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        if (g0 + 4 * k < groups)
+                            __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                                x_rsrc, (__attribute__((address_space(3))) void *)(halo + (g0 + 4 * k) * 1024), 16,
+                                static_cast<int32_t>(off[k]), 0, 0, 0);
+                }
+                // vmcnt(0) (expcnt and lgkmcnt left at their maxima): this
+                // wave's copies have landed; the barrier covers the others.
+                __builtin_amdgcn_s_waitcnt(0x0F70);
+                __syncthreads();
+            }
+            // ---- 6. tasks: the present offsets in ascending order.  Per
+            // task t: A(t+1) is read and the slots of task t+2 looked up
+            // while t's MFMAs run; the weights of task t+R are requested
+            // right after them.  Scheduling fences keep the weight loads in
+            // that order.
+            auto load_b = [&](int o, uint4 (&bf)[4]) __attribute__((always_inline)) {
+                const int32_t sbase = ((o * ksteps_total + ks) * nbtot + nb0) * 1024;
+#pragma unroll
+                for (int nb = 0; nb < 4; ++nb) {
+                    const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, bvo[nb], sbase, 0);
+                    bf[nb] = make_uint4(v.x, v.y, v.z, v.w);
+                }
+            };
+            // The source of row block mb's lane row (mb*32 + lane%32) at
+            // offset o: its halo slot, or (GA) its source row or -1.
+            auto load_idx = [&](int o, int (&ix)[MB]) __attribute__((always_inline)) {
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) {
+                    if constexpr (GA) ix[mb] = table32[o * ROWS + mb * 32 + (lane & 31)];
+                    else ix[mb] = table[o * ROWS + mb * 32 + (lane & 31)];
+                }
+            };
+            // A fragments: channels ks*16 + half*8 .. +8, i.e. chunk piece
+            // 2*wave + half.
+            auto load_a = [&](const int (&ix)[MB], uint4 (&af)[MB]) __attribute__((always_inline)) {
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) {
+                    if constexpr (GA) {
+                        const uint32_t off = ix[mb] >= 0
+                                                 ? (static_cast<uint32_t>(ix[mb]) * static_cast<uint32_t>(a.cin) +
+                                                    static_cast<uint32_t>(ks * 16 + half * 8)) * 2u
+                                                 : 0x80000000u;
+                        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, static_cast<int32_t>(off), 0, 0);
+                        af[mb] = make_uint4(v.x, v.y, v.z, v.w);
+                    } else {
+                        const int p = 2 * wave + half;
+                        af[mb] = *reinterpret_cast<const uint4 *>(halo + ix[mb] * kHRowBytes + ((p ^ (ix[mb] & 7)) << 4));
+                    }
+                }
+            };
+            // Ring of R task sets (B requested R-1 tasks ahead: three for
+            // 64-row tiles, whose tasks are half as long, else two).
+            constexpr int R = MB == 2 ? 4 : 3;
+            uint4 bq[R][4], aq[R][MB];
+            int iq[R][MB];
+            uint32_t rest_i = mask, rest_b = mask;
+            // (issued in the loop's order, so the wait counts at the loop
+            // head match the steady state)
+#pragma unroll
+            for (int k = 0; k < R; ++k) {
+                load_b(advance(rest_b), bq[k]);
+                sched_fence();
+            }
+            load_idx(advance(rest_i), iq[0]);
+            load_idx(advance(rest_i), iq[1]);
+            load_a(iq[0], aq[0]);
+            sched_fence();
+            // body of task t held in set K (t = K mod R)
+            auto body = [&](auto kc) __attribute__((always_inline)) {
+                constexpr int K = decltype(kc)::value, K1 = (K + 1) % R, K2 = (K + 2) % R;
+                // The LDS reads for the next tasks go between this task's
+                // MFMAs (the scheduler interleaves them); the weight loads
+                // stay after the last MFMA that reads their registers.
+                load_a(iq[K1], aq[K1]);
+                load_idx(advance(rest_i), iq[K2]);
+                mfmas(aq[K], bq[K]);
+                sched_fence();
+                load_b(advance(rest_b), bq[K]);
+                sched_fence();
+            };
+            int t = 0;
+            for (; t + R <= ntasks; t += R) {
+                body(std::integral_constant<int, 0>{});
+                body(std::integral_constant<int, 1>{});
+                body(std::integral_constant<int, 2>{});
+                if constexpr (R == 4) body(std::integral_constant<int, 3>{});
+            }
+            // Fewer than R tasks left: set k holds task t+k's weights; the
+            // A of task t is in set 0 and the slots of task t+1 in set 1.
+            const int left = ntasks - t;
+            if (left >= 1) mfmas(aq[0], bq[0]);
+            if (left >= 2) {
+                load_a(iq[1], aq[1]);
+                mfmas(aq[1], bq[1]);
+            }
+            if constexpr (R == 4) {
+                if (left >= 3) {
+                    load_idx(advance(rest_i), iq[2]);
+                    load_a(iq[2], aq[2]);
+                    mfmas(aq[2], bq[2]);
+                }
+            }
+        }
+    };
+    if (global_a) chunk_loop(std::true_type{});
+    else chunk_loop(std::false_type{});
+    __syncthreads();  // the halo region becomes the reduction slots
+
+    // ---- 7. reduce the 4 partial tiles in two phases of RPH row blocks;
+    // pair (h, c) = (row block RPH*p + h, column block c) is summed by wave c,
+    // the other waves handing their partials over as float4 [4][lane] slots.
+    float4 *red = reinterpret_cast<float4 *>(smem);
+    auto slot_of = [&](int h, int c, int writer) __attribute__((always_inline)) {
+        return red + ((h * 4 + c) * 4 + writer) * (4 * 64);
+    };
+    float fin[2][RPH][16];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+        if (p) __syncthreads();
+#pragma unroll
+        for (int h = 0; h < RPH; ++h)
+#pragma unroll
+            for (int k = 1; k < 4; ++k) {
+                const int c = (k + wave) & 3;
+                float4 *slot = slot_of(h, c, wave);
+#pragma unroll
+                for (int g = 0; g < 4; ++g)
+                    slot[g * 64 + lane] = make_float4(acc[RPH * p + h][k][4 * g], acc[RPH * p + h][k][4 * g + 1],
+                                                      acc[RPH * p + h][k][4 * g + 2], acc[RPH * p + h][k][4 * g + 3]);
+            }
+        __syncthreads();
+#pragma unroll
+        for (int h = 0; h < RPH; ++h)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                float4 sum = make_float4(acc[RPH * p + h][0][4 * g], acc[RPH * p + h][0][4 * g + 1],
+                                         acc[RPH * p + h][0][4 * g + 2], acc[RPH * p + h][0][4 * g + 3]);
+#pragma unroll
+                for (int s2 = 1; s2 < 4; ++s2) {
+                    const float4 v = slot_of(h, wave, (wave + s2) & 3)[g * 64 + lane];
+                    sum.x += v.x;
+                    sum.y += v.y;
+                    sum.z += v.z;
+                    sum.w += v.w;
+                }
+                fin[p][h][4 * g] = sum.x;
+                fin[p][h][4 * g + 1] = sum.y;
+                fin[p][h][4 * g + 2] = sum.z;
+                fin[p][h][4 * g + 3] = sum.w;
+            }
+    }
+    __syncthreads();
+    float *stg = reinterpret_cast<float *>(smem);
+    float *part = stg + ROWS * SM::STG_LD;
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int h = 0; h < RPH; ++h) {
+            const int col = wave * 32 + (lane & 31);
+            const int rb = (RPH * p + h) * 32 + 4 * half;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) stg[(rb + 8 * (r >> 2) + (r & 3)) * SM::STG_LD + col] = fin[p][h][r];
+        }
+    uint4 res[RowMap<16, ROWS>::PASSES][2];
+    load_residual<16, ROWS>(a, m0, nb0, tile_rows, tid, res);
+    __syncthreads();
+    finish_rows<16, ROWS, SM::STG_LD>(a, stg, part, m0, nb0, tile_rows, tid, res);
+}
+
+// One workgroup per 64-row tile: dedupe_tile, then the record to memory.
+__global__ void __launch_bounds__(256) gather_plan_build_kernel(const int32_t *kmap, int64_t n_out, int64_t n_src,
+                                                                int32_t row_shift, char *plan) {
+    using SM = HaloSmem<2>;
+    __shared__ __align__(16) int32_t table32[64 * kMaxKvol];
+    __shared__ __align__(16) uint16_t table[64 * kMaxKvol];
+    __shared__ __align__(16) uint32_t bitmap[SM::BITWORDS];
+    __shared__ __align__(16) uint32_t prefix[SM::BITWORDS];
+    __shared__ __align__(16) uint32_t slot_row[SM::CAP];
+    __shared__ __align__(16) int32_t misc[16];
+    const int tile = blockIdx.x, tid = threadIdx.x;
+    const int64_t m0 = static_cast<int64_t>(tile) * 64;
+    const int tile_rows = static_cast<int>(min(static_cast<int64_t>(64), n_out - m0));
+    const TileDedupe dd = dedupe_tile<2>(kmap, n_src, row_shift, m0, tile_rows, table, table32, bitmap, prefix,
+                                         slot_row, misc);
+    char *rec = plan + static_cast<int64_t>(tile) * kGatherPlanRecord;
+    if (tid == 0)
+        *reinterpret_cast<uint4 *>(rec) = make_uint4(dd.global_a ? 1u : 0u, dd.distinct, dd.mask, 0u);
+    if (dd.global_a) {
+        for (int i = tid; i < 64 * kMaxKvol / 4; i += 256)
+            reinterpret_cast<uint4 *>(rec + kPlanHeader)[i] = reinterpret_cast<const uint4 *>(table32)[i];
+    } else {
+        for (int i = tid; i < 64 * kMaxKvol * 2 / 16; i += 256)
+            reinterpret_cast<uint4 *>(rec + kPlanHeader)[i] = reinterpret_cast<const uint4 *>(table)[i];
+        for (int i = tid; i < static_cast<int>(dd.distinct); i += 256)
+            reinterpret_cast<uint32_t *>(rec + kPlanSlots)[i] = slot_row[i];
+    }
+}
+
+}  // namespace
+
+KernelFn pick_halo_bf16(int rows) {
+    return rows == 128 ? conv_halo_kernel<4, false> : rows == 64 ? conv_halo_kernel<2, false> : nullptr;
+}
+
+KernelFn pick_halo_bf16_planned() { return conv_halo_kernel<2, true>; }
+
+void launch_gather_plan_build(const int32_t *kmap, int64_t n_out, int64_t n_src, int32_t row_shift, void *plan,
+                              hipStream_t stream) {
+    const unsigned tiles = static_cast<unsigned>((n_out + 63) / 64);
+    hipLaunchKernelGGL(gather_plan_build_kernel, dim3(tiles), dim3(256), 0, stream, kmap, n_out, n_src, row_shift,
+                       static_cast<char *>(plan));
+}
+
+}  // namespace s3dx

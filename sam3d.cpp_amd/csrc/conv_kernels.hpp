@@ -33,12 +33,14 @@ struct ConvArgs {
     const float *mod_scale;
     const float *mod_shift;
     int32_t silu;
+    const void *plan;  // per-tile gather plan records (halo kernel), or nullptr
 };
 
 using KernelFn = void (*)(ConvArgs);
 
 // Workgroup tilings of the MFMA kernel: 4 waves in WM x WN (WM = 4/WN), each
 // wave MBW x NBW blocks of 32x32 outputs.
+// Tilings 20, 21: the halo-staged kernel (conv_halo.hip), 128- and 64-row split-K tiles.
 // Split-K tilings (splitk = 1): 128 rows x 32*nbw columns, each wave owning
 // the whole tile for a quarter of the k-steps.  Ids 15 and 16 (BF16, 32- or
 // 64-channel chunks) build each 128-channel task from 4 or 2 chunks.  Ids 17
@@ -54,7 +56,7 @@ inline constexpr Tiling kTilings[] = {
     {5, 1, 4, 2, 0}, {6, 2, 1, 2, 0}, {7, 2, 3, 1, 0}, {8, 2, 2, 2, 0}, {9, 2, 3, 2, 0},
     {10, 1, 4, 1, 0}, {11, 4, 4, 1, 1}, {12, 4, 2, 1, 1}, {13, 4, 3, 1, 1}, {14, 4, 1, 1, 1},
     {15, 4, 3, 1, 1}, {16, 4, 4, 1, 1}, {17, 2, 4, 1, 1}, {18, 2, 4, 1, 1},
-    {19, 2, 3, 1, 1},
+    {19, 2, 3, 1, 1}, {20, 4, 4, 1, 1}, {21, 2, 4, 1, 1},
 };
 
 // MFMA kernel for tiling `id`, kc channels per task, xf 64-bit gathers;
@@ -64,6 +66,18 @@ KernelFn pick_mfma_f32(int id, int kc, bool xf);
 // 1x1-layer kernel for nbt 32-column blocks (1, 2, 3, 4, 6, 8), else nullptr.
 KernelFn pick_linear_bf16(int nbt);
 KernelFn pick_linear_f32(int nbt);
+// The halo-staged BF16 kernel for `rows`-row x 128-column tiles (tiling 20:
+// 128 rows, 21: 64 rows; 64-channel halo chunks; Cin a multiple of 64, Cout
+// padded to whole 128-column tiles, kvol 27, inputs and weights below
+// 2 GiB), else nullptr.
+KernelFn pick_halo_bf16(int rows);
+// The 64-row halo kernel reading a precomputed gather plan (a.plan), the
+// plan builder (one workgroup per 64-row tile), and a plan record's bytes.
+KernelFn pick_halo_bf16_planned();
+void launch_gather_plan_build(const int32_t *kmap, int64_t n_out, int64_t n_src, int32_t row_shift, void *plan,
+                              hipStream_t stream);
+constexpr int kGatherPlanRows = 64;
+constexpr int kGatherPlanRecord = 7168;
 // The FP32 1x1-layer kernel reading BF16 rows, else nullptr.
 KernelFn pick_linear_f32_bf16_rows(int nbt);
 // The same on BF16 MFMAs with three-term split weights (Cin = 16 * ksx,
@@ -418,8 +432,7 @@ __device__ __forceinline__ void finish_rows(const ConvArgs &a, const float *stg,
             uint32_t o4[4];
 #pragma unroll
             for (int k = 0; k < 4; ++k)
-                o4[k] = static_cast<uint32_t>(f32_to_bf16(v[2 * k])) |
-                        (static_cast<uint32_t>(f32_to_bf16(v[2 * k + 1])) << 16);
+                o4[k] = pack_bf16x2(v[2 * k], v[2 * k + 1]);
             // Streaming stores: the rows are read by the next kernel, likely
             // on another XCD, so they need not sit dirty in this XCD's L2
             // (whose write-back at kernel end is on the critical path).
@@ -1309,8 +1322,7 @@ __device__ __forceinline__ void linear_store_block(const ConvArgs &a, const f32x
                     uint32_t w[EPC / 2];
 #pragma unroll
                     for (int i = 0; i < EPC / 2; ++i)
-                        w[i] = static_cast<uint32_t>(f32_to_bf16(v[2 * i])) |
-                               (static_cast<uint32_t>(f32_to_bf16(v[2 * i + 1])) << 16);
+                        w[i] = pack_bf16x2(v[2 * i], v[2 * i + 1]);
                     if constexpr (EPC == 8)
                         *reinterpret_cast<uint4 *>(static_cast<uint16_t *>(a.y) + off) = make_uint4(w[0], w[1], w[2], w[3]);
                     else
@@ -1488,10 +1500,8 @@ linear_split_kernel(ConvArgs a) {
                     const float4 p = *reinterpret_cast<const float4 *>(tl + i * 8);
                     const float4 q = *reinterpret_cast<const float4 *>(tl + i * 8 + 4);
                     *reinterpret_cast<uint4 *>(y + i * 8) = make_uint4(
-                        f32_to_bf16(p.x) | (static_cast<uint32_t>(f32_to_bf16(p.y)) << 16),
-                        f32_to_bf16(p.z) | (static_cast<uint32_t>(f32_to_bf16(p.w)) << 16),
-                        f32_to_bf16(q.x) | (static_cast<uint32_t>(f32_to_bf16(q.y)) << 16),
-                        f32_to_bf16(q.z) | (static_cast<uint32_t>(f32_to_bf16(q.w)) << 16));
+                        pack_bf16x2(p.x, p.y), pack_bf16x2(p.z, p.w), pack_bf16x2(q.x, q.y),
+                        pack_bf16x2(q.z, q.w));
                 } else {
                     for (int e = i * 8; e < elems; ++e) y[e] = f32_to_bf16(tl[e]);
                 }

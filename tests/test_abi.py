@@ -104,12 +104,24 @@ def test_conv_create_validation(s3dx):
 def test_conv_plan_names_the_launched_kernel(s3dx, monkeypatch):
     # Host-only query: which kernel variant s3dx_conv_run would launch.
     monkeypatch.delenv("S3DX_CONV_TILING", raising=False)
+    monkeypatch.delenv("S3DX_CONV_HALO", raising=False)
     n = 28265  # 64^3 eight-shell union, seed 0
     c128 = s3dx.SparseConv(128, 128, 27, s3dx.BF16)
-    # one pass of 128-row tiles on 256 CUs: 64-row tiles, two per CU, 64-channel tasks
+    # BF16 3x3x3 with 64-channel chunks and 128 columns: the halo-staged
+    # kernel on 64-row tiles (442 > 256 CUs), 128-row tiles on request.
+    assert c128.plan(n, n) == "mfma tiling=21 split-k halo rows=64 cols=128 kc=64 xf=0 ln=none grid=442x1"
+    monkeypatch.setenv("S3DX_CONV_HALO", "128")
+    assert c128.plan(n, n) == "mfma tiling=20 split-k halo rows=128 cols=128 kc=64 xf=0 ln=none grid=221x1"
+    # Without it: one pass of 128-row tiles on 256 CUs: 64-row tiles, two per CU, 64-channel tasks
+    monkeypatch.setenv("S3DX_CONV_HALO", "0")
     assert c128.plan(n, n) == "mfma tiling=18 split-k rows=64 cols=128 kc=64 xf=0 ln=none grid=442x1"
+    monkeypatch.delenv("S3DX_CONV_HALO")
     c128.set_layernorm(True, 1e-6)
     assert "ln=fused" in c128.plan(n, n)
+    # A fused LayerNorm over 256 columns is not the halo kernel's epilogue.
+    assert "halo" not in s3dx.SparseConv(128, 256, 27, s3dx.BF16).set_layernorm(True, 1e-6).plan(n, n)
+    assert "halo" in s3dx.SparseConv(1024, 1024, 27, s3dx.BF16).plan(5086, 5086)
+    assert "halo" not in s3dx.SparseConv(128, 128, 27, s3dx.F32).plan(n, n)
     f64 = s3dx.SparseConv(64, 64, 27, s3dx.F32)
     assert f64.plan(n, n).startswith("mfma tiling=12 split-k rows=128 cols=64 kc=64")
     # 96 bf16 channels: four 32-channel chunks make each 128-channel task.

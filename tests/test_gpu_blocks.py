@@ -190,11 +190,13 @@ def test_config2_block_full_size(s3dx, O, W, dtype):
     conv1 = (s3dx.SparseConv(c, c, 27, dtype).set_weights(w1, s3dx.WEIGHT_SLAT, b)
              .set_layernorm(True, 1e-6).set_silu(True))
     conv2 = s3dx.SparseConv(c, c, 27, dtype).set_weights(w2, s3dx.WEIGHT_SLAT, b)
-    kc = 64 if dtype == 1 else 32
+    # BF16: the halo-staged 64-row kernel; FP32: 64-row split-K tiles.
+    head = "mfma tiling=21 split-k halo rows=64 cols=128 kc=64" if dtype == 1 else \
+        "mfma tiling=18 split-k rows=64 cols=128 kc=32"
     for cv in (conv1, conv2):
         plan = cv.plan(n, n)
         print(f"config 2 dtype={dtype}: {plan}", flush=True)
-        assert plan.startswith(f"mfma tiling=18 split-k rows=64 cols=128 kc={kc}") and plan.endswith("grid=442x1"), plan
+        assert plan.startswith(head) and plan.endswith("grid=442x1"), plan
     xd, dk = _dev(s3dx, W, x, dtype), s3dx.DeviceArray.from_host(kmap)
     h, y = _buf(s3dx, n, c, dtype), _buf(s3dx, n, c, dtype)
     conv1.run(xd, n, dk, n, h, dtype)
@@ -219,7 +221,7 @@ def test_config3_full_size(s3dx, O, W):
     conv = s3dx.SparseConv(c, c, 27, s3dx.BF16).set_weights(W.conv_weight(0, 301, c, c), s3dx.WEIGHT_SLAT, None)
     plan = conv.plan(nc, nc)
     print(f"config 3: {plan}", flush=True)
-    assert plan.startswith("mfma tiling=17 split-k rows=64 cols=128 kc=128") and plan.endswith("grid=80x8"), plan
+    assert plan.startswith("mfma tiling=21 split-k halo rows=64 cols=128 kc=64") and plan.endswith("grid=80x8"), plan
     x = W.round_bf16(W.normal_f32(0, 300, (nc, c)))
     y = _buf(s3dx, nc, c, s3dx.BF16)
     conv.run(_dev(s3dx, W, x, s3dx.BF16), nc, s3dx.DeviceArray.from_host(kmap), nc, y, s3dx.BF16)

@@ -1,0 +1,162 @@
+"""The halo-staged BF16 conv kernels and per-map gather plans.
+
+A halo tile stages each distinct source row of its 64 (or 128) output rows
+once per 64-channel chunk into LDS; a tile whose rows reach more distinct
+source rows than its LDS holds reads them from memory instead (global mode).
+A gather plan (s3dx_gather_plan_create) precomputes each 64-row tile's
+distinct rows and slot table once per map; s3dx_conv_run_planned then skips
+that step.  A planned run must equal the unplanned run bit for bit (same
+kernel body, same summation order), on tiles of either mode and on the tail
+tile, and both meet the BF16 gate (rel-L2 1e-2) against the float64 oracle.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from helpers import check_rel
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf(s3dx, W, a):
+    return s3dx.DeviceArray.from_host(W.f32_to_bf16_bits(np.ascontiguousarray(a, np.float32)))
+
+
+def _host(W, d):
+    h = d.download()
+    return W.bf16_bits_to_f32(h).reshape(h.shape)
+
+
+def _dense_cube(side, shuffle_from=None, seed=0):
+    """A dense side^3 cube, batch 0, x-major; rows [shuffle_from:] shuffled,
+    so their tiles reach ~27 distinct source rows per output row."""
+    g = np.stack(np.meshgrid(*(np.arange(side),) * 3, indexing="ij"), -1).reshape(-1, 3)
+    c = np.concatenate([np.zeros((len(g), 1), np.int64), g], 1).astype(np.int32)
+    if shuffle_from is not None:
+        rng = np.random.default_rng(seed)
+        tail = c[shuffle_from:].copy()
+        rng.shuffle(tail)
+        c[shuffle_from:] = tail
+    return np.ascontiguousarray(c)
+
+
+def _layer(s3dx, W, cin, cout, seed, ln):
+    conv = (s3dx.SparseConv(cin, cout, 27, s3dx.BF16)
+            .set_weights(W.conv_weight(seed, 2, cin, cout), s3dx.WEIGHT_SLAT, W.normal_f32(seed, 3, (cout,), 0.1)))
+    if ln:
+        conv.set_layernorm(True, 1e-6).set_silu(True)
+    return conv
+
+
+def _oracle(O, W, x, kmap, n, cin, cout, seed, ln, res=None):
+    h = O.conv(x, kmap, n, W.round_bf16(W.conv_weight(seed, 2, cin, cout)), 0, cout, W.normal_f32(seed, 3, (cout,), 0.1))
+    if ln:
+        h = O.silu(O.layernorm(h, 1e-6))
+    return h + res if res is not None else h
+
+
+CASES = {
+    # name: (coords builder, cin, cout, LayerNorm+SiLU+residual)
+    "shells_union_28265": (lambda W: W.shells_union(0), 128, 128, True),
+    "shells_union_3000_cin256": (lambda W: W.shells_union(1)[:3000], 256, 128, False),
+    "shuffled_cube_13824": (lambda W: _dense_cube(24, 0), 128, 128, True),          # every tile global
+    "half_shuffled_cube_13824": (lambda W: _dense_cube(24, 6912), 128, 128, False),  # both modes
+    "tiny_37": (lambda W: W.shells_union(2)[:37], 128, 128, True),                   # one partial tile
+}
+
+
+@pytest.mark.parametrize("case", list(CASES))
+def test_planned_run_equals_unplanned(s3dx, O, W, monkeypatch, case):
+    monkeypatch.delenv("S3DX_CONV_TILING", raising=False)
+    monkeypatch.delenv("S3DX_CONV_HALO", raising=False)
+    build, cin, cout, ln = CASES[case]
+    coords = build(W)
+    n = coords.shape[0]
+    kmap = O.kmap_subm3(coords, n)
+    conv = _layer(s3dx, W, cin, cout, 40, ln)
+    plan_text = conv.plan(n, n)
+    print(f"{case} n={n}: {plan_text}", flush=True)
+    assert plan_text.startswith("mfma tiling=21 split-k halo rows=64"), plan_text
+    x = W.round_bf16(W.normal_f32(40, 1, (n, cin)))
+    res = W.round_bf16(W.normal_f32(40, 4, (n, cout))) if ln else None
+    xd, kd = _bf(s3dx, W, x), s3dx.DeviceArray.from_host(kmap)
+    rd = _bf(s3dx, W, res) if ln else None
+    gp = conv.gather_plan(n, kd, n)
+    y0 = s3dx.DeviceArray((n, cout), np.uint16)
+    y1 = s3dx.DeviceArray((n, cout), np.uint16)
+    conv.run(xd, n, kd, n, y0, s3dx.BF16, rd)
+    conv.run(xd, n, kd, n, y1, s3dx.BF16, rd, plan=gp)
+    a, b = y0.download(), y1.download()
+    assert np.array_equal(a, b), f"planned run differs in {(a != b).sum()} of {a.size} values"
+    # The plan serves every layer over the same map and source rows.
+    other = _layer(s3dx, W, cin, cout, 41, False)
+    other.run(xd, n, kd, n, y0, s3dx.BF16)
+    other.run(xd, n, kd, n, y1, s3dx.BF16, plan=gp)
+    assert np.array_equal(y0.download(), y1.download())
+    check_rel(_host(W, y1), _oracle(O, W, x, kmap, n, cin, cout, 41, False), 1e-2, f"{case} (second layer)")
+    conv.run(xd, n, kd, n, y1, s3dx.BF16, rd, plan=gp)
+    check_rel(_host(W, y1), _oracle(O, W, x, kmap, n, cin, cout, 40, ln, res), 1e-2, case)
+
+
+def test_planned_config3_rows(s3dx, O, W):
+    # 1024 -> 1024 on the 5,086 coarse rows: eight column blocks share each
+    # tile's plan record.
+    fine = W.shells_union(0)
+    nc, coarse, _, _, _ = O.coarsen2(fine)
+    coarse = np.ascontiguousarray(coarse[:nc])
+    kmap = O.kmap_subm3(coarse, nc)
+    c = 1024
+    conv = s3dx.SparseConv(c, c, 27, s3dx.BF16).set_weights(W.conv_weight(0, 301, c, c), s3dx.WEIGHT_SLAT, None)
+    xd, kd = _bf(s3dx, W, W.round_bf16(W.normal_f32(0, 300, (nc, c)))), s3dx.DeviceArray.from_host(kmap)
+    gp = conv.gather_plan(nc, kd, nc)
+    y0, y1 = s3dx.DeviceArray((nc, c), np.uint16), s3dx.DeviceArray((nc, c), np.uint16)
+    conv.run(xd, nc, kd, nc, y0, s3dx.BF16)
+    conv.run(xd, nc, kd, nc, y1, s3dx.BF16, plan=gp)
+    assert np.array_equal(y0.download(), y1.download())
+
+
+@pytest.mark.parametrize("tiling", ["20", "21"])
+@pytest.mark.parametrize("shuffle_from", [None, 0, 6912])
+def test_halo_tilings_on_dense_and_shuffled_rows(s3dx, O, W, monkeypatch, tiling, shuffle_from):
+    # Both tile heights on LDS-staged, global and mixed tiles (no plan).
+    monkeypatch.setenv("S3DX_CONV_TILING", tiling)
+    coords = _dense_cube(24, shuffle_from, seed=3)
+    n = coords.shape[0]
+    kmap = O.kmap_subm3(coords, n)
+    conv = _layer(s3dx, W, 128, 128, 42, True)
+    plan_text = conv.plan(n, n)
+    print(f"tiling {tiling} shuffle_from={shuffle_from}: {plan_text}", flush=True)
+    assert plan_text.startswith(f"mfma tiling={tiling} split-k halo"), plan_text
+    x = W.round_bf16(W.normal_f32(42, 1, (n, 128)))
+    res = W.round_bf16(W.normal_f32(42, 4, (n, 128)))
+    y = s3dx.DeviceArray((n, 128), np.uint16)
+    conv.run(_bf(s3dx, W, x), n, s3dx.DeviceArray.from_host(kmap), n, y, s3dx.BF16, _bf(s3dx, W, res))
+    check_rel(_host(W, y), _oracle(O, W, x, kmap, n, 128, 128, 42, True, res), 1e-2)
+
+
+def test_plan_rejects_another_map_size(s3dx, O, W, monkeypatch):
+    monkeypatch.delenv("S3DX_CONV_TILING", raising=False)
+    monkeypatch.delenv("S3DX_CONV_HALO", raising=False)
+    coords = W.shells_union(0)[:2000]
+    n = coords.shape[0]
+    kd = s3dx.DeviceArray.from_host(O.kmap_subm3(coords, n))
+    conv = _layer(s3dx, W, 128, 128, 43, False)
+    gp = conv.gather_plan(n, kd, n)
+    xd = _bf(s3dx, W, W.normal_f32(43, 1, (n, 128)))
+    y = s3dx.DeviceArray((n, 128), np.uint16)
+    with pytest.raises(s3dx.S3dxError) as e:
+        conv.run(xd, n, kd, n - 1, y, s3dx.BF16, plan=gp)
+    assert e.value.status == s3dx.INVALID_ARGUMENT and "gather plan" in str(e.value)
+    # A layer reading parent rows (x >> 3) has other source rows.
+    parent = _layer(s3dx, W, 128, 128, 43, False).set_gather_parent(True)
+    with pytest.raises(s3dx.S3dxError) as e:
+        parent.run(xd, n, kd, n, y, s3dx.BF16, plan=gp)
+    assert e.value.status == s3dx.INVALID_ARGUMENT
+    # A layer that runs another kernel ignores the plan.
+    f32 = s3dx.SparseConv(128, 128, 27, s3dx.F32).set_weights(W.conv_weight(43, 2, 128, 128), s3dx.WEIGHT_SLAT, None)
+    xf = s3dx.DeviceArray.from_host(W.normal_f32(43, 5, (n, 128)))
+    yf0, yf1 = s3dx.DeviceArray((n, 128), np.float32), s3dx.DeviceArray((n, 128), np.float32)
+    f32.run(xf, n, kd, n, yf0, s3dx.F32)
+    f32.run(xf, n, kd, n, yf1, s3dx.F32, plan=gp)
+    assert np.array_equal(yf0.download(), yf1.download())
