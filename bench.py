@@ -2,8 +2,9 @@
 """Sparse-voxel conv benchmark: effective TFLOP/s + kernel-map Mvox/s.
 
 Workload (one step): on a seeded 64^3 union of 8 sphere shells (~28k voxels,
-int32 coords resident in HBM), build the 27-offset kernel map on the GPU, then
-run one SparseResBlock at C=128:
+int32 coords resident in HBM), build the 27-offset kernel map and its gather
+plan (per 64-row tile: the distinct source rows) on the GPU, then run one
+SparseResBlock at C=128:
     conv3x3x3 -> LayerNorm -> SiLU -> conv3x3x3 -> + x
 in BF16 with FP32 accumulation (LayerNorm/SiLU fused into the first conv's
 epilogue, the residual into the second's).  The same block in FP32 is
@@ -13,7 +14,10 @@ value        = effective conv TFLOP/s = 2 * (2*Cin*Cout*P) / (conv1 + conv2
                kernel time), P = present (voxel, offset) pairs of the map,
                kernel times from HIP events around each launch on its stream
 kmap_mvox_s  = voxels / (device time of the kernel-map build)
-ms_per_step  = wall clock per step (kernel map + block, host launches included)
+gather_plan_ms = device time of the plan rebuild (reported beside the conv
+               time, and in value_incl_gather_plan)
+ms_per_step  = wall clock per step (kernel map + plan + block, host launches
+               included)
 
 The CPU baseline (rank 0, N=1 only) times the oracle's restatement of the
 reference CPU path on the same inputs: im2col gather + FP32 GEMM (the GGML CPU
@@ -81,14 +85,14 @@ class Block:
                       .set_layernorm(True, 1e-6).set_silu(True))
         self.conv2 = s3dx.SparseConv(c, c, 27, dtype).set_weights(w2, s3dx.WEIGHT_SLAT, b)
 
-    def run(self, kmap, ev=None):
+    def run(self, kmap, ev=None, plan=None):
         s = self.stream
         if ev:
             ev[0].record(s)
-        self.conv1.run(self.x, self.n, kmap, self.n, self.h, self.dtype, None, s)
+        self.conv1.run(self.x, self.n, kmap, self.n, self.h, self.dtype, None, s, plan=plan)
         if ev:
             ev[1].record(s)
-        self.conv2.run(self.h, self.n, kmap, self.n, self.y, self.dtype, self.x, s)
+        self.conv2.run(self.h, self.n, kmap, self.n, self.y, self.dtype, self.x, s, plan=plan)
         if ev:
             ev[2].record(s)
 
@@ -127,12 +131,19 @@ def extras(s3dx, W, stream, seed):
     out = {}
     bf, f32 = s3dx.BF16, s3dx.F32
 
-    def conv_entry(name, conv, x, n_in, kmap, n_out, y, ydt, pairs, cin, cout, peak, residual=None):
-        us = _event_us(s3dx, stream, lambda: conv.run(x, n_in, kmap, n_out, y, ydt, residual, stream))
+    def conv_entry(name, conv, x, n_in, kmap, n_out, y, ydt, pairs, cin, cout, peak, residual=None,
+                   planned=False):
+        gp, plan_us = None, None
+        if planned:  # the map's gather plan, built once per map (timed apart)
+            gp = conv.gather_plan(n_in, kmap, n_out, stream)
+            plan_us = _event_us(s3dx, stream, lambda: gp.rebuild(conv, n_in, kmap, n_out, stream))
+        us = _event_us(s3dx, stream, lambda: conv.run(x, n_in, kmap, n_out, y, ydt, residual, stream, plan=gp))
         flops = 2.0 * cin * cout * pairs
         out[name] = {"us": us, "tflops": flops / us / 1e6, "peak_tflops": peak,
                      "frac": flops / us / 1e6 / peak, "rows": n_out, "pairs": pairs,
                      "plan": conv.plan(n_in, n_out)}
+        if planned:
+            out[name]["gather_plan_us"] = plan_us
 
     # config 1: one FP32 64 -> 64 conv on the 20-radius shell (10,366 voxels)
     c1 = W.shell_64()
@@ -165,7 +176,22 @@ def extras(s3dx, W, stream, seed):
     conv = s3dx.SparseConv(1024, 1024, 27, bf).set_weights(W.conv_weight(seed, 301, 1024, 1024), s3dx.WEIGHT_SLAT, None)
     x = s3dx.DeviceArray.from_host(W.f32_to_bf16_bits(W.normal_f32(seed, 300, (nc, 1024))), stream)
     y = s3dx.DeviceArray((nc, 1024), np.uint16)
-    conv_entry("config3_bf16_conv_1024", conv, x, nc, k3, nc, y, bf, p3, 1024, 1024, PEAK_BF16_TFLOPS)
+    conv_entry("config3_bf16_conv_1024", conv, x, nc, k3, nc, y, bf, p3, 1024, 1024, PEAK_BF16_TFLOPS,
+               planned=True)
+
+    # The SLat flow's largest conv, out_blocks.0.conv1 (slat_flow_graph.cpp:441-470):
+    # 2048 -> 128 over the fine set, with the fused LayerNorm + modulate + SiLU.
+    k2 = s3dx.kmap_subm3(d2, n2, n2, stream=stream)
+    p2 = W.kmap_pairs(k2.download(stream), n2)
+    mscale = s3dx.DeviceArray.from_host(W.normal_f32(seed, 322, (128,), 0.1), stream)
+    mshift = s3dx.DeviceArray.from_host(W.normal_f32(seed, 324, (128,), 0.1), stream)
+    conv = (s3dx.SparseConv(2048, 128, 27, bf).set_weights(W.conv_weight(seed, 321, 2048, 128), s3dx.WEIGHT_SLAT,
+                                                            W.normal_f32(seed, 323, (128,), 0.1))
+            .set_layernorm(True, 1e-6).set_modulate(mscale, mshift).set_silu(True))
+    x = s3dx.DeviceArray.from_host(W.f32_to_bf16_bits(W.normal_f32(seed, 320, (n2, 2048))), stream)
+    y = s3dx.DeviceArray((n2, 128), np.uint16)
+    conv_entry("slat_out_block0_conv1_bf16_2048_128", conv, x, n2, k2, n2, y, bf, p2, 2048, 128, PEAK_BF16_TFLOPS,
+               planned=True)
 
     # SLat sparse I/O (slat_flow_graph.cpp:159-190) at C=128 BF16: 2x mean-pool
     # of the fine rows onto the coarse set, then nearest upsample back.
@@ -410,6 +436,9 @@ def main():
     flops = 2.0 * c * c * pairs  # effective FLOPs per conv
 
     bf = Block(s3dx, W, s3dx.BF16, n, c, args.seed, stream)
+    # The map's gather plan (per 64-row tile: distinct source rows + slot
+    # table), rebuilt in place after each map build and shared by both convs.
+    gplan = bf.conv1.gather_plan(n, kmap, n, stream)
 
     def step(ev_k=None, ev_b=None):
         if ev_k:
@@ -417,7 +446,10 @@ def main():
         s3dx.kmap_subm3(dc, n, n, kmap, ws, stream)
         if ev_k:
             ev_k[1].record(stream)
-        bf.run(kmap, ev_b)
+        gplan.rebuild(bf.conv1, n, kmap, n, stream)
+        if ev_k:
+            ev_k[2].record(stream)
+        bf.run(kmap, ev_b, gplan)
 
     if args.profile_only:
         for _ in range(args.steps):
@@ -442,7 +474,7 @@ def main():
     stream.synchronize()
 
     K = args.steps
-    evk = [[s3dx.Event(timing=True), s3dx.Event(timing=True)] for _ in range(K)]
+    evk = [[s3dx.Event(timing=True), s3dx.Event(timing=True), s3dx.Event(timing=True)] for _ in range(K)]
     evb = [[s3dx.Event(timing=True), s3dx.Event(timing=True), s3dx.Event(timing=True)] for _ in range(K)]
     stream.synchronize()
     t0 = time.perf_counter()
@@ -452,6 +484,7 @@ def main():
     wall = time.perf_counter() - t0
 
     kmap_ms = [evk[i][0].elapsed_ms(evk[i][1]) for i in range(K)]
+    gplan_ms = statistics.mean(evk[i][1].elapsed_ms(evk[i][2]) for i in range(K))
     conv1_ms = [evb[i][0].elapsed_ms(evb[i][1]) for i in range(K)]
     conv2_ms = [evb[i][1].elapsed_ms(evb[i][2]) for i in range(K)]
     conv_ms = statistics.mean(conv1_ms + conv2_ms)
@@ -469,10 +502,15 @@ def main():
 
     tflops = 2 * flops / (block_ms * 1e-3) / 1e12
     achieved = flops / (conv_ms * 1e-3) / 1e12
+    # HBM bytes per launch from the committed FETCH_SIZE/WRITE_SIZE passes,
+    # only while they describe the kernel this run launches.
+    kernel = "conv_halo_kernel<2, true>"
     traffic = None
     tfile = ROOT / "profiles" / "conv_bf16_c128_shells64_traffic.json"
     if tfile.exists():
-        traffic = json.loads(tfile.read_text()).get("hbm_bytes_per_launch")
+        t = json.loads(tfile.read_text())
+        if t.get("kernel") == kernel and "tiling=21" in bf.conv1.plan(n, n):
+            traffic = t.get("hbm_bytes_per_launch")
     out = {
         "metric": METRIC,
         "value": tflops,
@@ -495,12 +533,16 @@ def main():
         },
         "kmap_mvox_s": n / (kmap_avg * 1e-3) / 1e6,
         "kmap_ms": kmap_avg,
+        "gather_plan_ms": gplan_ms,
         "block_ms": block_ms,
         "conv_kernel_ms": conv_ms,
+        # The plan is per map (like the kernel map): this step amortizes it
+        # over its two convs only, the SLat flow over every conv of a sample.
+        "value_incl_gather_plan": 2 * flops / ((block_ms + gplan_ms) * 1e-3) / 1e12,
         "roofline": {
             "bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
             "frac": achieved / PEAK_BF16_TFLOPS, "traffic": traffic,
-            "kernel": "conv_splitk_kernel (bf16)",
+            "kernel": kernel,
             "plan": {"conv1": bf.conv1.plan(n, n), "conv2": bf.conv2.plan(n, n)},
         },
         "kmap_roofline": {

@@ -318,6 +318,13 @@ S3DX_API s3dx_status s3dx_gather_plan_create(const s3dx_conv *conv, int64_t n_in
                                              int64_t n_out, s3dx_stream stream, s3dx_gather_plan **out,
                                              char *error, uint64_t error_capacity);
 S3DX_API void s3dx_gather_plan_free(s3dx_gather_plan *plan);
+/* Rebuilds `plan` in place for another map (e.g. the next sample's), with no
+ * allocation: n_out may be at most the n_out the plan was created for
+ * (S3DX_INVALID_ARGUMENT otherwise).  Enqueued on `stream`; runs still
+ * queued on another stream that read the old plan must be ordered before it. */
+S3DX_API s3dx_status s3dx_gather_plan_rebuild(s3dx_gather_plan *plan, const s3dx_conv *conv, int64_t n_in,
+                                              const int32_t *kmap, int64_t n_out, s3dx_stream stream,
+                                              char *error, uint64_t error_capacity);
 /* s3dx_conv_run with a gather plan built for the same kmap, n_out and source
  * rows (S3DX_INVALID_ARGUMENT when the sizes or the source setup differ).
  * Results are bit-identical to s3dx_conv_run; launches that do not use the

@@ -86,6 +86,7 @@ SIGNATURES = {
     "s3dx_conv_plan": (_u32, [_vp, _i64, _i64, C.c_char_p, _u64], True),
     "s3dx_gather_plan_create": (_u32, [_vp, _i64, _vp, _i64, _vp, C.POINTER(_vp)], True),
     "s3dx_gather_plan_free": (None, [_vp], False),
+    "s3dx_gather_plan_rebuild": (_u32, [_vp, _vp, _i64, _vp, _i64, _vp], True),
     "s3dx_conv_run_planned": (_u32, [_vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _i32, _vp], True),
     "s3dx_layernorm_rows": (_u32, [_vp, _i32, _i64, _i32, _f32, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp], True),
     "s3dx_groupnorm_workspace_size": (_u32, [_i64, _i32, _i32, C.POINTER(_u64)], True),
@@ -536,6 +537,14 @@ class GatherPlan:
              C.byref(p))
         self.handle = p.value
         self._kmap = kmap
+
+    def rebuild(self, conv: SparseConv, n_in: int, kmap, n_out: int, stream=None) -> "GatherPlan":
+        """Rebuilds the plan in place for another map of at most the created rows
+        (s3dx_gather_plan_rebuild; no allocation)."""
+        call("s3dx_gather_plan_rebuild", _vp(self.handle), _vp(conv.handle), _i64(n_in), _dptr(kmap), _i64(n_out),
+             _sptr(stream))
+        self._kmap = kmap
+        return self
 
     def __del__(self):
         try:

@@ -306,6 +306,7 @@ struct s3dx_conv {
 // layer setup.
 struct s3dx_gather_plan {
     void *d = nullptr;
+    int64_t capacity = 0;  // output rows the allocation covers
     int64_t n_out = 0, n_src = 0;
     int32_t shift = 0;
     ~s3dx_gather_plan() {
@@ -1032,32 +1033,63 @@ S3DX_API s3dx_status s3dx_conv_run(const s3dx_conv *conv, const void *x, int64_t
                     [&] { conv_run_impl(conv, nullptr, x, n_in, kmap, n_out, residual, y, y_dtype, stream); });
 }
 
+}  // extern "C"
+
+namespace {
+
+// Checks the arguments and enqueues the build of `p` (allocated for at least
+// n_out rows) over `kmap`.
+void gather_plan_build(s3dx_gather_plan *p, const s3dx_conv *conv, int64_t n_in, const int32_t *kmap,
+                       int64_t n_out, s3dx_stream stream) {
+    const Source src = source_of(conv, n_in);
+    require(src.n_src <= INT32_MAX, "input rows exceed INT32_MAX");
+    launch_gather_plan_build(kmap, n_out, src.n_src, src.shift, p->d, as_stream(stream));
+    launch_check("gather_plan_build");
+    p->n_out = n_out;
+    p->n_src = src.n_src;
+    p->shift = src.shift;
+}
+
+void gather_plan_check(const s3dx_conv *conv, int64_t n_in, const int32_t *kmap, int64_t n_out) {
+    require(conv != nullptr && kmap != nullptr, "NULL argument");
+    require(conv->kvol == kMaxKvol, "gather plans are for 3x3x3 layers");
+    require(n_in > 0 && n_out > 0 && n_out <= INT32_MAX, "row counts out of range");
+    require(aligned(kmap, 16), "kmap must be 16-byte aligned");
+}
+
+}  // namespace
+
+extern "C" {
+
 S3DX_API s3dx_status s3dx_gather_plan_create(const s3dx_conv *conv, int64_t n_in, const int32_t *kmap,
                                              int64_t n_out, s3dx_stream stream, s3dx_gather_plan **out,
                                              char *error, uint64_t error_capacity) {
     return boundary(error, error_capacity, [&] {
         require(out != nullptr, "out is NULL");
         *out = nullptr;
-        require(conv != nullptr && kmap != nullptr, "NULL argument");
-        require(conv->kvol == kMaxKvol, "gather plans are for 3x3x3 layers");
-        require(n_in > 0 && n_out > 0 && n_out <= INT32_MAX, "row counts out of range");
-        require(aligned(kmap, 16), "kmap must be 16-byte aligned");
-        const Source src = source_of(conv, n_in);
-        require(src.n_src <= INT32_MAX, "input rows exceed INT32_MAX");
+        gather_plan_check(conv, n_in, kmap, n_out);
         const int64_t bytes = (n_out + kGatherPlanRows - 1) / kGatherPlanRows * kGatherPlanRecord;
         require(bytes < (int64_t(1) << 31), "map too large for a gather plan");
         auto p = std::make_unique<s3dx_gather_plan>();
         hip_check(hipMalloc(&p->d, static_cast<size_t>(bytes)), "hipMalloc gather plan");
-        launch_gather_plan_build(kmap, n_out, src.n_src, src.shift, p->d, as_stream(stream));
-        launch_check("gather_plan_build");
-        p->n_out = n_out;
-        p->n_src = src.n_src;
-        p->shift = src.shift;
+        p->capacity = n_out;
+        gather_plan_build(p.get(), conv, n_in, kmap, n_out, stream);
         *out = p.release();
     });
 }
 
 S3DX_API void s3dx_gather_plan_free(s3dx_gather_plan *plan) { delete plan; }
+
+S3DX_API s3dx_status s3dx_gather_plan_rebuild(s3dx_gather_plan *plan, const s3dx_conv *conv, int64_t n_in,
+                                              const int32_t *kmap, int64_t n_out, s3dx_stream stream,
+                                              char *error, uint64_t error_capacity) {
+    return boundary(error, error_capacity, [&] {
+        require(plan != nullptr, "plan is NULL");
+        gather_plan_check(conv, n_in, kmap, n_out);
+        require(n_out <= plan->capacity, "n_out exceeds the rows the plan was created for");
+        gather_plan_build(plan, conv, n_in, kmap, n_out, stream);
+    });
+}
 
 S3DX_API s3dx_status s3dx_conv_run_planned(const s3dx_conv *conv, const s3dx_gather_plan *plan, const void *x,
                                            int64_t n_in, const int32_t *kmap, int64_t n_out, const void *residual,

@@ -160,3 +160,28 @@ def test_plan_rejects_another_map_size(s3dx, O, W, monkeypatch):
     f32.run(xf, n, kd, n, yf0, s3dx.F32)
     f32.run(xf, n, kd, n, yf1, s3dx.F32, plan=gp)
     assert np.array_equal(yf0.download(), yf1.download())
+
+
+def test_plan_rebuild_in_place(s3dx, O, W, monkeypatch):
+    # A plan created for a larger map serves a smaller one after rebuild (no
+    # allocation); a larger one is refused.
+    monkeypatch.delenv("S3DX_CONV_TILING", raising=False)
+    monkeypatch.delenv("S3DX_CONV_HALO", raising=False)
+    big, small = W.shells_union(0)[:6000], W.shells_union(1)[:4100]
+    conv = _layer(s3dx, W, 128, 128, 44, True)
+    kb = s3dx.DeviceArray.from_host(O.kmap_subm3(big, big.shape[0]))
+    gp = conv.gather_plan(big.shape[0], kb, big.shape[0])
+    n = small.shape[0]
+    kmap = O.kmap_subm3(small, n)
+    ks = s3dx.DeviceArray.from_host(kmap)
+    gp.rebuild(conv, n, ks, n)
+    x = W.round_bf16(W.normal_f32(44, 1, (n, 128)))
+    xd = _bf(s3dx, W, x)
+    y0, y1 = s3dx.DeviceArray((n, 128), np.uint16), s3dx.DeviceArray((n, 128), np.uint16)
+    conv.run(xd, n, ks, n, y0, s3dx.BF16)
+    conv.run(xd, n, ks, n, y1, s3dx.BF16, plan=gp)
+    assert np.array_equal(y0.download(), y1.download())
+    check_rel(_host(W, y1), _oracle(O, W, x, kmap, n, 128, 128, 44, True), 1e-2)
+    with pytest.raises(s3dx.S3dxError) as e:
+        gp.rebuild(conv, 6001, kb, 6001)
+    assert e.value.status == s3dx.INVALID_ARGUMENT
