@@ -105,7 +105,10 @@ S3DX_API s3dx_status s3dx_kmap_workspace_size(int64_t n, uint64_t *bytes, char *
  * row of the FIRST voxel with coordinates coords[i] + delta(o), or
  * missing_value; rows of later duplicates of a coordinate stay entirely
  * missing_value (sparse_ops.cpp:120-141).  Byte-identical to the reference.
- * Requires 0 < n <= INT32_MAX / 27.  Asynchronous on `stream`. */
+ * Requires 0 < n <= INT32_MAX / 27.  Asynchronous on `stream`, two
+ * launches.  The workspace's contents on entry do not matter and need no
+ * clearing: every build tags the words it writes with a fresh per-call tag,
+ * so one workspace serves any sequence of builds on one stream. */
 S3DX_API s3dx_status s3dx_kmap_subm3(const int32_t *coords, int64_t n, int32_t missing_value,
                                      int32_t *kmap, void *workspace, uint64_t workspace_bytes,
                                      s3dx_stream stream, char *error, uint64_t error_capacity);
@@ -113,11 +116,11 @@ S3DX_API s3dx_status s3dx_kmap_subm3(const int32_t *coords, int64_t n, int32_t m
 /* s3dx_kmap_subm3 without a workspace and without any allocation.  No
  * counterpart in the reference: it is for callers that cannot allocate --
  * code under HIP graph capture, tight serving loops, harnesses that forbid
- * hipMalloc.  The hash table lives in a static device array of the library
- * (8 MiB + 256 bytes on each GPU it runs on, held until the process ends),
+ * hipMalloc.  The table lives in a static device array of the library
+ * (18 MiB + 256 bytes on each GPU it runs on, held until the process ends),
  * so n is limited to 262144 voxels (S3DX_INVALID_ARGUMENT above that).  Same
- * kernels and results as s3dx_kmap_subm3; the table is cleared by a kernel
- * at the start of every call.  All calls on one GPU share that array:
+ * kernels and results as s3dx_kmap_subm3 (per-call tags, no clearing
+ * pass).  All calls on one GPU share that array:
  * calls that overlap in time on one GPU (different streams, threads) race
  * and must be serialized by the caller. */
 S3DX_API s3dx_status s3dx_kmap_subm3_static(const int32_t *coords, int64_t n, int32_t missing_value,

@@ -10,29 +10,195 @@
 // std::map::emplace's "first occurrence wins" does.
 #include "coord_hash.hpp"
 
+#include <atomic>
 #include <mutex>
 #include <vector>
 
 namespace s3dx {
 namespace {
 
+// ---- the kernel-map table ----------------------------------------------------
+// Two structures, chosen per coordinate:
+//  - a direct-index window of 64^3 cells for batch 0 and x, y, z in [0, 64)
+//    (the SLat grids: 64^3 fine, 32^3 coarse), one 64-bit word {row, tag} per
+//    cell: a lookup is one 8-byte read, an insert a read and a CAS;
+//  - for every other coordinate, open addressing with linear probing at load
+//    <= 1/4 over 16-byte slots {key lo, key hi, row, tag}.  The key is
+//    (b, x, y, z) packed as four int16 when the coordinate fits (a set with
+//    any other coordinate raises the "wide" flag and its slots are matched
+//    through the input rows instead).
+// The {row, tag} word is claimed with one 64-bit CAS; a second row with the
+// same coordinates lowers it with a 64-bit atomicMin, so every key keeps its
+// smallest row -- std::map::emplace's "first occurrence wins"
+// (sparse_ops.cpp:124-127).
+//
+// A cell or slot belongs to the current build only when its tag equals
+// tag_of(seed, index), and every build draws a new seed: tag_of is a
+// bijection of seed ^ f(index), so nothing written by another build carries
+// the current tag, and the table needs no clearing pass between builds.
+// Memory that never held the table (a fresh workspace) reads as empty except
+// with probability 2^-32 per word; such a hash slot must still match the
+// packed 64-bit key (or, wide, the input row's coordinates) before a lookup
+// returns its row, and a window cell's row is checked against the input
+// rows' coordinates on insert.
+constexpr int kWindow = 64;                                 // cells per axis
+constexpr int64_t kWindowCells = int64_t(kWindow) * kWindow * kWindow;
+
+struct KmapHash {
+    unsigned long long *cells;  // kWindowCells words {row, tag}
+    uint4 *slots;               // mask + 1 slots
+    int32_t *flags;             // [kFlag*] == flag_of(seed, k) when raised in this build
+    uint32_t mask;
+    uint32_t seed;
+};
+
+constexpr int kFlagWide = 2;  // some hashed coordinate does not fit int16
+
+__device__ __host__ __forceinline__ uint32_t mix32(uint32_t h) {
+    h ^= h >> 16;
+    h *= 0x7FEB352Du;
+    h ^= h >> 15;
+    h *= 0x846CA68Bu;
+    h ^= h >> 16;
+    return h;
+}
+__device__ __forceinline__ uint32_t tag_of(uint32_t seed, uint32_t index) {
+    return mix32(seed ^ (index * 0x9E3779B1u));
+}
+__device__ __host__ __forceinline__ int32_t flag_of(uint32_t seed, int k) {
+    return static_cast<int32_t>(mix32(seed + 0x632BE5ABu * static_cast<uint32_t>(k + 1)));
+}
+
+// The window cell of c, or -1.
+__device__ __forceinline__ int32_t window_cell(int4 c) {
+    const uint32_t x = static_cast<uint32_t>(c.y), y = static_cast<uint32_t>(c.z), z = static_cast<uint32_t>(c.w);
+    if (c.x != 0 || (x | y | z) >= static_cast<uint32_t>(kWindow)) return -1;
+    return static_cast<int32_t>((x * kWindow + y) * kWindow + z);
+}
+
+__device__ __forceinline__ bool fits16(int4 c) {
+    auto f = [](int32_t v) { return v >= -32768 && v <= 32767; };
+    return f(c.x) && f(c.y) && f(c.z) && f(c.w);
+}
+__device__ __forceinline__ uint64_t pack16(int4 c) {
+    return (static_cast<uint64_t>(static_cast<uint16_t>(c.x)) << 48) |
+           (static_cast<uint64_t>(static_cast<uint16_t>(c.y)) << 32) |
+           (static_cast<uint64_t>(static_cast<uint16_t>(c.z)) << 16) | static_cast<uint64_t>(static_cast<uint16_t>(c.w));
+}
+
+// Hash path of the insert (coordinates outside the window): claim a slot
+// for row i, or lower the row of the slot already holding its key.
+__device__ __forceinline__ void kmap_hash_insert(const int4 *__restrict__ keys, int32_t n, const KmapHash &h, int32_t i,
+                                         int4 c) {
+    const bool fits = fits16(c);
+    if (!fits) h.flags[kFlagWide] = flag_of(h.seed, kFlagWide);
+    uint32_t pos = key_hash(c) & h.mask;
+    for (uint32_t probe = 0; probe <= h.mask; ++probe) {
+        const uint32_t tag = tag_of(h.seed, pos);
+        auto *word = reinterpret_cast<unsigned long long *>(&h.slots[pos]) + 1;  // {row, tag}
+        const unsigned long long mine = (static_cast<unsigned long long>(tag) << 32) | static_cast<uint32_t>(i);
+        unsigned long long cur = *word;
+        if (static_cast<uint32_t>(cur >> 32) != tag) {
+            const unsigned long long prev = atomicCAS(word, cur, mine);
+            if (prev == cur) {
+                atomicExch(reinterpret_cast<unsigned long long *>(&h.slots[pos]),
+                           static_cast<unsigned long long>(fits ? pack16(c) : 0ull));
+                return;
+            }
+            cur = prev;  // claimed meanwhile, by a row of this build
+        }
+        // The slot's row is of this build (or a stale word's chance match,
+        // whose row fails the comparison): compare coordinates through the
+        // input, since its packed key may not be written yet.
+        const uint32_t r = static_cast<uint32_t>(cur);
+        if (r < static_cast<uint32_t>(n) && same_key(keys[r], c)) {
+            atomicMin(word, mine);
+            h.flags[kFlagDuplicate] = flag_of(h.seed, kFlagDuplicate);
+            return;
+        }
+        pos = (pos + 1) & h.mask;
+    }
+    h.flags[kFlagOverflow] = flag_of(h.seed, kFlagOverflow);
+}
+
+// Thread per voxel: claim the cell (or, outside the window, a slot) for row
+// i, or lower the row of the one already holding its key.
+__global__ void __launch_bounds__(kThreads)
+kmap_insert_kernel(const int4 *__restrict__ keys, int32_t n, KmapHash h) {
+    const int32_t i = blockIdx.x * kThreads + threadIdx.x;
+    if (i >= n) return;
+    const int4 c = keys[i];
+    const int32_t cell = window_cell(c);
+    if (cell < 0) {
+        kmap_hash_insert(keys, n, h, i, c);
+        return;
+    }
+    const uint32_t tag = tag_of(h.seed, static_cast<uint32_t>(cell));
+    unsigned long long *word = h.cells + cell;
+    const unsigned long long mine = (static_cast<unsigned long long>(tag) << 32) | static_cast<uint32_t>(i);
+    unsigned long long cur = *word;  // a stale read only fails the CAS
+    for (;;) {
+        // A current cell holds this key (one cell per key) unless its tag is
+        // a stale word's chance match, whose row names other coordinates.
+        const uint32_t r = static_cast<uint32_t>(cur);
+        if (static_cast<uint32_t>(cur >> 32) == tag && r < static_cast<uint32_t>(n) && same_key(keys[r], c)) {
+            atomicMin(word, mine);
+            h.flags[kFlagDuplicate] = flag_of(h.seed, kFlagDuplicate);
+            return;
+        }
+        const unsigned long long prev = atomicCAS(word, cur, mine);
+        if (prev == cur) return;
+        cur = prev;  // claimed meanwhile by a row of this build (with this key)
+    }
+}
+
+// Hash path of kmap_find (coordinates outside the window).
+__device__ __forceinline__ int32_t kmap_hash_find(const KmapHash &h, const int4 *__restrict__ keys, int32_t n, int4 q,
+                                          bool wide) {
+    if (!wide && !fits16(q)) return -1;
+    const uint64_t kq = pack16(q);
+    uint32_t pos = key_hash(q) & h.mask;
+    for (uint32_t probe = 0; probe <= h.mask; ++probe) {
+        const uint4 s = h.slots[pos];
+        if (s.w != tag_of(h.seed, pos)) return -1;
+        const bool hit = wide ? s.z < static_cast<uint32_t>(n) && same_key(keys[s.z], q)
+                              : ((static_cast<uint64_t>(s.y) << 32) | s.x) == kq;
+        if (hit) return static_cast<int32_t>(s.z);
+        pos = (pos + 1) & h.mask;
+    }
+    return -1;
+}
+
+// Smallest row whose key equals q, or -1 (after kmap_insert_kernel).
+__device__ __forceinline__ int32_t kmap_find(const KmapHash &h, const int4 *__restrict__ keys, int32_t n, int4 q,
+                                             bool wide) {
+    const int32_t cell = window_cell(q);
+    if (cell < 0) return kmap_hash_find(h, keys, n, q, wide);
+    const unsigned long long v = h.cells[cell];
+    return static_cast<uint32_t>(v >> 32) == tag_of(h.seed, static_cast<uint32_t>(cell))
+               ? static_cast<int32_t>(static_cast<uint32_t>(v))
+               : -1;
+}
+
 // One thread per (voxel, offset): kmap[i*27+o] = first row at coords[i]+d(o).
 __global__ void __launch_bounds__(kThreads)
-kmap_lookup_kernel(const int4 *__restrict__ coords, int32_t n, Hash h, int32_t missing,
+kmap_lookup_kernel(const int4 *__restrict__ coords, int32_t n, KmapHash h, int32_t missing,
                    int32_t *__restrict__ kmap) {
     const int32_t g = blockIdx.x * kThreads + threadIdx.x;
     if (g >= n * 27) return;
     const int32_t i = g / 27;
     const int32_t o = g - i * 27;
     const int4 c = coords[i];
+    const bool wide = h.flags[kFlagWide] == flag_of(h.seed, kFlagWide);
+    const bool dup = h.flags[kFlagDuplicate] == flag_of(h.seed, kFlagDuplicate);
     int32_t result = missing;
     // Later duplicates of a coordinate keep an all-missing row
     // (sparse_ops.cpp:129-139 only visits each key's first row).
-    const bool owner = h.flags[kFlagDuplicate] == 0 || hash_find(h, c) == i;
+    const bool owner = !dup || kmap_find(h, coords, n, c, wide) == i;
     int4 q = c;
     if (owner && add_fits(c.y, o / 9 - 1, &q.y) && add_fits(c.z, (o / 3) % 3 - 1, &q.z) &&
         add_fits(c.w, o % 3 - 1, &q.w)) {
-        const int32_t r = hash_find(h, q);
+        const int32_t r = kmap_find(h, coords, n, q, wide);
         if (r >= 0) result = r;
     }
     kmap[g] = result;
@@ -236,25 +402,51 @@ uint64_t dense_cell_cap(int64_t n) {
     return a > b ? a : b;
 }
 
-template <class W>
-void kmap_layout(W &w, int64_t n, Hash *h) {
-    hash_layout(w, n, h);
+constexpr uint64_t kmap_capacity(int64_t n) {
+    uint64_t cap = 256;
+    while (cap < static_cast<uint64_t>(n) * 4) cap <<= 1;
+    return cap;
 }
 
-// Hash insert + lookup, leaving the flags in the workspace.
-void run_kmap(const int4 *coords, int32_t n, int32_t missing, int32_t *kmap, Hash h,
-              hipStream_t stream) {
-    hash_build(coords, n, h, stream);
-    kmap_lookup_kernel<<<blocks_for(static_cast<int64_t>(n) * 27), kThreads, 0, stream>>>(
-        coords, n, h, missing, kmap);
+template <class W>
+void kmap_layout(W &w, int64_t n, KmapHash *h) {
+    const uint64_t cap = kmap_capacity(n);
+    if constexpr (std::is_same_v<W, Carver>) {
+        h->cells = w.template take<unsigned long long>(kWindowCells);
+        h->slots = w.template take<uint4>(cap);
+        h->flags = w.template take<int32_t>(64);
+        h->mask = static_cast<uint32_t>(cap - 1);
+        h->seed = 0;
+    } else {
+        w.template take<unsigned long long>(kWindowCells);
+        w.template take<uint4>(cap);
+        w.template take<int32_t>(64);
+    }
+}
+
+// A new seed for every build in the process (never repeated before 2^32
+// builds), so slots of earlier builds read as empty.
+uint32_t next_seed() {
+    static std::atomic<uint32_t> counter{0x3C6EF372u};
+    return counter.fetch_add(1, std::memory_order_relaxed);
+}
+
+// Insert + lookup (two launches, no clearing pass), leaving the flags of
+// this build (h.seed) in the workspace.
+void run_kmap(const int4 *coords, int32_t n, int32_t missing, int32_t *kmap, KmapHash &h, hipStream_t stream) {
+    h.seed = next_seed();
+    kmap_insert_kernel<<<blocks_for(n), kThreads, 0, stream>>>(coords, n, h);
+    launch_check("kmap_insert");
+    kmap_lookup_kernel<<<blocks_for(static_cast<int64_t>(n) * 27), kThreads, 0, stream>>>(coords, n, h, missing,
+                                                                                           kmap);
     launch_check("kmap_lookup");
 }
 
 // Allocation-free kernel maps: the hash table lives in `scratch`, one array
 // per device for the life of the process, sized for kStaticKmapMaxVoxels.
 constexpr int64_t kStaticKmapMaxVoxels = int64_t(1) << 18;
-constexpr uint64_t kStaticKmapBytes =
-    (hash_capacity(kStaticKmapMaxVoxels) * 4 + 255) / 256 * 256 + (64 * 4 + 255) / 256 * 256;
+constexpr uint64_t kStaticKmapBytes = kWindowCells * 8 + (kmap_capacity(kStaticKmapMaxVoxels) * 16 + 255) / 256 * 256 +
+                                      (64 * 4 + 255) / 256 * 256;
 static __device__ __align__(256) unsigned char scratch[kStaticKmapBytes];
 
 // The device address of `scratch` on the current device, looked up once per
@@ -288,7 +480,7 @@ void check_coords(const int32_t *coords, int64_t n) {
 namespace s3dx {
 namespace {
 struct SubdivideLayout {
-    Hash hash;
+    KmapHash hash;
     int32_t *parent_kmap;
 };
 template <class W>
@@ -297,7 +489,7 @@ void subdivide_layout(W &w, int64_t p, SubdivideLayout *l) {
         kmap_layout(w, p, &l->hash);
         l->parent_kmap = w.template take<int32_t>(static_cast<uint64_t>(p) * 27);
     } else {
-        kmap_layout(w, p, static_cast<Hash *>(nullptr));
+        kmap_layout(w, p, static_cast<KmapHash *>(nullptr));
         w.template take<int32_t>(static_cast<uint64_t>(p) * 27);
     }
 }
@@ -320,7 +512,7 @@ void coarsen_layout(W &w, int64_t n, CoarsenLayout *l) {
     const uint64_t scan_items = cells > un ? cells : un;
     if constexpr (std::is_same_v<W, Carver>) {
         l->ckeys = w.template take<int4>(un);
-        kmap_layout(w, n, &l->hash);
+        hash_layout(w, n, &l->hash);
         l->bbox = w.template take<int32_t>(8);
         l->totals = w.template take<int32_t>(8);
         l->a = w.template take<int32_t>(un);
@@ -336,7 +528,7 @@ void coarsen_layout(W &w, int64_t n, CoarsenLayout *l) {
         l->scan_ws = w.template take<char>(scan_workspace_bytes(static_cast<int64_t>(scan_items)));
     } else {
         w.template take<int4>(un);
-        kmap_layout(w, n, static_cast<Hash *>(nullptr));
+        hash_layout(w, n, static_cast<Hash *>(nullptr));
         w.template take<int32_t>(8);
         w.template take<int32_t>(8);
         for (int k = 0; k < 8; ++k) w.template take<int32_t>(un);
@@ -358,7 +550,7 @@ S3DX_API s3dx_status s3dx_kmap_workspace_size(int64_t n, uint64_t *bytes, char *
         require(bytes != nullptr, "bytes is NULL");
         require(n > 0 && n <= INT32_MAX / 27, "voxel count out of range");
         Sizer s;
-        kmap_layout(s, n, static_cast<Hash *>(nullptr));
+        kmap_layout(s, n, static_cast<KmapHash *>(nullptr));
         *bytes = s.used;
     });
 }
@@ -371,7 +563,7 @@ S3DX_API s3dx_status s3dx_kmap_subm3(const int32_t *coords, int64_t n, int32_t m
         require(kmap != nullptr, "kmap is NULL");
         require(workspace != nullptr, "workspace is NULL");
         Carver w(workspace, workspace_bytes);
-        Hash h;
+        KmapHash h;
         kmap_layout(w, n, &h);
         run_kmap(reinterpret_cast<const int4 *>(coords), static_cast<int32_t>(n), missing_value,
                  kmap, h, as_stream(stream));
@@ -386,7 +578,7 @@ S3DX_API s3dx_status s3dx_kmap_subm3_static(const int32_t *coords, int64_t n, in
         require(kmap != nullptr, "kmap is NULL");
         require(n <= kStaticKmapMaxVoxels, "voxel count exceeds the static table's maximum (262144)");
         Carver w(static_scratch(), kStaticKmapBytes);
-        Hash h;
+        KmapHash h;
         kmap_layout(w, n, &h);
         run_kmap(reinterpret_cast<const int4 *>(coords), static_cast<int32_t>(n), missing_value, kmap, h,
                  as_stream(stream));
@@ -438,8 +630,9 @@ S3DX_API s3dx_status s3dx_subdivide2(const int32_t *parent_coords, int64_t paren
         hip_check(hipMemcpyAsync(flags, l.hash.flags, sizeof(flags), hipMemcpyDeviceToHost, s),
                   "hipMemcpyAsync flags");
         hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
-        require(flags[kFlagDuplicate] == 0, "duplicate parent coordinates");
-        if (flags[kFlagOverflow]) throw std::runtime_error("hash table overflow");
+        require(flags[kFlagDuplicate] != flag_of(l.hash.seed, kFlagDuplicate), "duplicate parent coordinates");
+        if (flags[kFlagOverflow] == flag_of(l.hash.seed, kFlagOverflow))
+            throw std::runtime_error("hash table overflow");
     });
 }
 
