@@ -141,7 +141,7 @@ def extras(s3dx, W, stream, seed):
         flops = 2.0 * cin * cout * pairs
         out[name] = {"us": us, "tflops": flops / us / 1e6, "peak_tflops": peak,
                      "frac": flops / us / 1e6 / peak, "rows": n_out, "pairs": pairs,
-                     "plan": conv.plan(n_in, n_out)}
+                     "plan": conv.plan(n_in, n_out, gp)}
         if planned:
             out[name]["gather_plan_us"] = plan_us
 
@@ -456,7 +456,8 @@ def main():
             step()
         stream.synchronize()
         print(json.dumps({"profile_only_steps": args.steps, "voxels": n, "pairs": pairs,
-                          "plan": {"conv1": bf.conv1.plan(n, n), "conv2": bf.conv2.plan(n, n)}}), flush=True)
+                          "plan": {"conv1": bf.conv1.plan(n, n, gplan), "conv2": bf.conv2.plan(n, n, gplan)}}),
+              flush=True)
         return
     f32 = Block(s3dx, W, s3dx.F32, n, c, args.seed, stream)
 
@@ -504,12 +505,14 @@ def main():
     achieved = flops / (conv_ms * 1e-3) / 1e12
     # HBM bytes per launch from the committed FETCH_SIZE/WRITE_SIZE passes,
     # only while they describe the kernel this run launches.
-    kernel = "conv_halo_kernel<2, true>"
+    planned = {"conv1": bf.conv1.plan(n, n, gplan), "conv2": bf.conv2.plan(n, n, gplan)}
+    kernel = ("conv_halo8_kernel" if "tiling=22" in planned["conv1"] else
+              "conv_halo_kernel<2, true>" if "plan=64" in planned["conv1"] else "unplanned")
     traffic = None
     tfile = ROOT / "profiles" / "conv_bf16_c128_shells64_traffic.json"
     if tfile.exists():
         t = json.loads(tfile.read_text())
-        if t.get("kernel") == kernel and "tiling=21" in bf.conv1.plan(n, n):
+        if t.get("kernel") == kernel:
             traffic = t.get("hbm_bytes_per_launch")
     out = {
         "metric": METRIC,
@@ -543,7 +546,7 @@ def main():
             "bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
             "frac": achieved / PEAK_BF16_TFLOPS, "traffic": traffic,
             "kernel": kernel,
-            "plan": {"conv1": bf.conv1.plan(n, n), "conv2": bf.conv2.plan(n, n)},
+            "plan": planned,
         },
         "kmap_roofline": {
             "bound": "hbm", "achieved": n * KMAP_BYTES_PER_VOXEL / (kmap_avg * 1e-3) / 1e9,

@@ -314,8 +314,11 @@ S3DX_API s3dx_status s3dx_conv_run(const s3dx_conv *conv, const void *x, int64_t
  * per sample, session.cpp:1563-1566) and pass it to every
  * s3dx_conv_run_planned over that map by layers set up alike (e.g. both
  * convs of a res_block).  The caller keeps kmap unchanged while the plan is
- * in use.  create enqueues the build on `stream` (device memory: 7 KiB per
- * 64 output rows); free releases it. */
+ * in use.  create enqueues the build on `stream` and picks the records' tile
+ * height from `conv`: 128 output rows when its halo kernel's 128-row tiles
+ * fill the GPU's compute units in one pass (runs then use an 8-wave kernel
+ * on those tiles; 14 KiB of device memory per 128 rows), else 64 rows (7
+ * KiB per 64 rows); free releases it. */
 typedef struct s3dx_gather_plan s3dx_gather_plan;
 S3DX_API s3dx_status s3dx_gather_plan_create(const s3dx_conv *conv, int64_t n_in, const int32_t *kmap,
                                              int64_t n_out, s3dx_stream stream, s3dx_gather_plan **out,
@@ -343,6 +346,12 @@ S3DX_API s3dx_status s3dx_conv_run_planned(const s3dx_conv *conv, const s3dx_gat
  * (whose conv is a fixed GGML graph); it exists for tests and benchmarks. */
 S3DX_API s3dx_status s3dx_conv_plan(const s3dx_conv *conv, int64_t n_in, int64_t n_out, char *plan,
                                     uint64_t plan_capacity, char *error, uint64_t error_capacity);
+/* The same for s3dx_conv_run_planned with `gather_plan`: the kernel it
+ * launches, with " plan=64" or " plan=128" appended when that kernel reads
+ * the plan.  No counterpart in the reference. */
+S3DX_API s3dx_status s3dx_conv_plan_planned(const s3dx_conv *conv, const s3dx_gather_plan *gather_plan,
+                                            int64_t n_in, int64_t n_out, char *plan, uint64_t plan_capacity,
+                                            char *error, uint64_t error_capacity);
 
 /* ------------------------------------------------------------------------
  * Standalone row ops (graph_builder.cpp:56-62, mesh_decoder_graph.cpp:16-30,

@@ -87,6 +87,7 @@ SIGNATURES = {
     "s3dx_gather_plan_create": (_u32, [_vp, _i64, _vp, _i64, _vp, C.POINTER(_vp)], True),
     "s3dx_gather_plan_free": (None, [_vp], False),
     "s3dx_gather_plan_rebuild": (_u32, [_vp, _vp, _i64, _vp, _i64, _vp], True),
+    "s3dx_conv_plan_planned": (_u32, [_vp, _vp, _i64, _i64, C.c_char_p, _u64], True),
     "s3dx_conv_run_planned": (_u32, [_vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _i32, _vp], True),
     "s3dx_layernorm_rows": (_u32, [_vp, _i32, _i64, _i32, _f32, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp], True),
     "s3dx_groupnorm_workspace_size": (_u32, [_i64, _i32, _i32, C.POINTER(_u64)], True),
@@ -498,10 +499,15 @@ class SparseConv:
         call("s3dx_conv_set_input_dtype", _vp(self.handle), _i32(dtype))
         return self
 
-    def plan(self, n_in: int, n_out: int) -> str:
-        """The kernel variant run() launches for these row counts (host only)."""
+    def plan(self, n_in: int, n_out: int, gather_plan: "GatherPlan" = None) -> str:
+        """The kernel variant run() launches for these row counts (host only);
+        with `gather_plan`, the one run(plan=gather_plan) launches."""
         buf = C.create_string_buffer(256)
-        call("s3dx_conv_plan", _vp(self.handle), _i64(n_in), _i64(n_out), buf, len(buf))
+        if gather_plan is None:
+            call("s3dx_conv_plan", _vp(self.handle), _i64(n_in), _i64(n_out), buf, len(buf))
+        else:
+            call("s3dx_conv_plan_planned", _vp(self.handle), _vp(gather_plan.handle), _i64(n_in), _i64(n_out), buf,
+                 len(buf))
         return buf.value.decode()
 
     def gather_plan(self, n_in: int, kmap, n_out: int, stream=None) -> "GatherPlan":

@@ -306,6 +306,7 @@ struct s3dx_conv {
 // layer setup.
 struct s3dx_gather_plan {
     void *d = nullptr;
+    int rows = 64;         // tile height of the records (64 or 128)
     int64_t capacity = 0;  // output rows the allocation covers
     int64_t n_out = 0, n_src = 0;
     int32_t shift = 0;
@@ -595,6 +596,36 @@ LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bo
     return p;
 }
 
+// A planned launch: the halo kernel of the plan's tile height in place of
+// the unplanned halo kernel (64-row records: tiling 21 only; 128-row records:
+// tilings 20 and 21, on the 8-wave kernel).  Other launches are unchanged.
+void apply_gather_plan(LaunchPlan &p, const s3dx_gather_plan *g, int64_t n_out, bool bf16_rows) {
+    if (bf16_rows || !p.mfma || !p.tl || (p.tl->id != 20 && p.tl->id != 21)) return;
+    if (g->rows == 64 && p.tl->id == 21) {
+        p.fn = pick_halo_bf16_planned(64);
+    } else if (g->rows == 128) {
+        for (const Tiling &t : kTilings)
+            if (t.id == 22) p.tl = &t;
+        p.fn = pick_halo_bf16_planned(128);
+        p.threads = kHalo8Threads;
+        p.grid = dim3(static_cast<unsigned>((n_out + 127) / 128), p.grid.y);
+    }
+}
+
+// Tile height of the gather plan for `conv`: 128-row records when the
+// layer runs a halo kernel and 128-row tiles fill the CUs in one pass (one
+// 8-wave workgroup per CU), else 64.  S3DX_PLAN_ROWS=64|128 forces it.
+int gather_plan_rows(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out) {
+    if (const char *e = std::getenv("S3DX_PLAN_ROWS")) {
+        const int r = std::atoi(e);
+        if (r == 64 || r == 128) return r;
+    }
+    const LaunchPlan p = plan_launch(conv, x_bytes, n_out, true);
+    if (!p.mfma || !p.tl || (p.tl->id != 20 && p.tl->id != 21)) return 64;
+    const int64_t tiles = (n_out + 127) / 128 * static_cast<int64_t>(p.grid.y);
+    return tiles <= device_cus() ? 128 : 64;
+}
+
 float *upload_f32(const float *host, size_t count) {
     if (!host) return nullptr;
     void *d = nullptr;
@@ -862,9 +893,14 @@ S3DX_API s3dx_status s3dx_conv_set_input_dtype(s3dx_conv *conv, int32_t dtype, c
     });
 }
 
-S3DX_API s3dx_status s3dx_conv_plan(const s3dx_conv *conv, int64_t n_in, int64_t n_out, char *plan,
-                                    uint64_t plan_capacity, char *error, uint64_t error_capacity) {
-    return boundary(error, error_capacity, [&] {
+}  // extern "C"
+
+namespace {
+
+// The launch description behind s3dx_conv_plan and s3dx_conv_plan_planned.
+void describe_launch(const s3dx_conv *conv, const s3dx_gather_plan *gplan, int64_t n_in, int64_t n_out, char *plan,
+                     uint64_t plan_capacity) {
+    {
         require(conv != nullptr, "conv is NULL");
         require(plan != nullptr && plan_capacity > 0, "plan buffer is empty");
         require(n_in > 0 && n_out > 0, "row counts must be positive");
@@ -876,6 +912,12 @@ S3DX_API s3dx_status s3dx_conv_plan(const s3dx_conv *conv, int64_t n_in, int64_t
         LaunchPlan p = plan_launch(conv, x_bytes, n_out, true, bf16_rows);
         const bool widen = bf16_rows && !p.linear;
         if (widen) p = plan_launch(conv, src.rows * conv->cin * 4, n_out, true);
+        if (gplan) {
+            require(gplan->n_out == n_out && gplan->n_src == src.n_src && gplan->shift == src.shift,
+                    "gather plan was built for another map size or source rows");
+            apply_gather_plan(p, gplan, n_out, bf16_rows);
+        }
+        const bool planned = gplan && (p.fn == pick_halo_bf16_planned(64) || p.fn == pick_halo_bf16_planned(128));
         char text[256];
         if (p.linear)
             std::snprintf(text, sizeof(text), "linear cols=%d ksteps=%d%s ln=%s grid=%u", p.nb * 32,
@@ -890,9 +932,27 @@ S3DX_API s3dx_status s3dx_conv_plan(const s3dx_conv *conv, int64_t n_in, int64_t
         else
             std::snprintf(text, sizeof(text), "generic rows=%d cols=%d ln=%s grid=%ux%u", kGM, kGN,
                           conv->ln ? "separate" : "none", p.grid.x, p.grid.y);
-        std::snprintf(plan, plan_capacity, "%s%s%s%s", bf16_rows ? (widen ? "in=bf16 pre=widen " : "in=bf16 ") : "",
+        std::snprintf(plan, plan_capacity, "%s%s%s%s%s", bf16_rows ? (widen ? "in=bf16 pre=widen " : "in=bf16 ") : "",
                       src.pre ? (src.children ? "pre=children " : "pre=rows ") : "", src.shift ? "parent-rows " : "",
-                      text);
+                      text, planned ? (gplan->rows == 128 ? " plan=128" : " plan=64") : "");
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+S3DX_API s3dx_status s3dx_conv_plan(const s3dx_conv *conv, int64_t n_in, int64_t n_out, char *plan,
+                                    uint64_t plan_capacity, char *error, uint64_t error_capacity) {
+    return boundary(error, error_capacity, [&] { describe_launch(conv, nullptr, n_in, n_out, plan, plan_capacity); });
+}
+
+S3DX_API s3dx_status s3dx_conv_plan_planned(const s3dx_conv *conv, const s3dx_gather_plan *gather_plan,
+                                            int64_t n_in, int64_t n_out, char *plan, uint64_t plan_capacity,
+                                            char *error, uint64_t error_capacity) {
+    return boundary(error, error_capacity, [&] {
+        require(gather_plan != nullptr, "gather plan is NULL");
+        describe_launch(conv, gather_plan, n_in, n_out, plan, plan_capacity);
     });
 }
 
@@ -987,11 +1047,9 @@ void conv_run_impl(const s3dx_conv *conv, const s3dx_gather_plan *gplan, const v
         if (gplan) {
             require(gplan->n_out == n_out && gplan->n_src == src.n_src && gplan->shift == src.shift,
                     "gather plan was built for another map size or source rows");
-            // Only the 64-row halo kernel reads plans; other plans ignore it.
-            if (plan.mfma && plan.tl && plan.tl->id == 21 && !bf16_rows) {
-                a.plan = gplan->d;
-                plan.fn = pick_halo_bf16_planned();
-            }
+            // Only the halo kernels read plans; other launches ignore it.
+            apply_gather_plan(plan, gplan, n_out, bf16_rows);
+            if (plan.fn == pick_halo_bf16_planned(64) || plan.fn == pick_halo_bf16_planned(128)) a.plan = gplan->d;
         }
         // A LayerNorm the epilogue cannot fuse runs as its own pass over the
         // conv's FP32 output (the layer's buffer), then modulate, SiLU and
@@ -1043,7 +1101,7 @@ void gather_plan_build(s3dx_gather_plan *p, const s3dx_conv *conv, int64_t n_in,
                        int64_t n_out, s3dx_stream stream) {
     const Source src = source_of(conv, n_in);
     require(src.n_src <= INT32_MAX, "input rows exceed INT32_MAX");
-    launch_gather_plan_build(kmap, n_out, src.n_src, src.shift, p->d, as_stream(stream));
+    launch_gather_plan_build(p->rows, kmap, n_out, src.n_src, src.shift, p->d, as_stream(stream));
     launch_check("gather_plan_build");
     p->n_out = n_out;
     p->n_src = src.n_src;
@@ -1068,9 +1126,13 @@ S3DX_API s3dx_status s3dx_gather_plan_create(const s3dx_conv *conv, int64_t n_in
         require(out != nullptr, "out is NULL");
         *out = nullptr;
         gather_plan_check(conv, n_in, kmap, n_out);
-        const int64_t bytes = (n_out + kGatherPlanRows - 1) / kGatherPlanRows * kGatherPlanRecord;
-        require(bytes < (int64_t(1) << 31), "map too large for a gather plan");
+        const Source src = source_of(conv, n_in);
         auto p = std::make_unique<s3dx_gather_plan>();
+        p->rows = gather_plan_rows(conv, src.rows * conv->cin * static_cast<int64_t>(dtype_size(conv->in_dtype)),
+                                   n_out);
+        const int64_t bytes =
+            (n_out + p->rows - 1) / p->rows * (p->rows == 128 ? kGatherPlanRecord128 : kGatherPlanRecord);
+        require(bytes < (int64_t(1) << 31), "map too large for a gather plan");
         hip_check(hipMalloc(&p->d, static_cast<size_t>(bytes)), "hipMalloc gather plan");
         p->capacity = n_out;
         gather_plan_build(p.get(), conv, n_in, kmap, n_out, stream);

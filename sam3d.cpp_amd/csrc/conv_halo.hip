@@ -35,8 +35,18 @@
 namespace s3dx {
 namespace {
 
+// s_waitcnt immediate waiting for vmcnt <= n (expcnt, lgkmcnt left at their maxima).
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
+
 constexpr int kHChunk = 64;              // channels per halo chunk
 constexpr int kHRowBytes = kHChunk * 2;  // 128 bytes per halo row
+
+// 16-byte piece p of halo slot s sits at position p ^ halo_swizzle(s) of
+// the slot's 128-byte row, so eight consecutive slots (the usual neighbours
+// of consecutive output rows) read by one 16-byte LDS access spread over
+// the eight positions.  ((s >> 1) & 7, which also separates 16 consecutive
+// slots, halves the bank-conflict cycles but measured 1.5% slower.)
+__device__ __forceinline__ int halo_swizzle(int s) { return s & 7; }
 
 template <int MB>
 struct HaloSmem {
@@ -249,6 +259,22 @@ static_assert(kPlanSlots + HaloSmem<2>::CAP * 4 <= kGatherPlanRecord, "halo reco
 static_assert(kPlanHeader + 64 * kMaxKvol * 4 <= kGatherPlanRecord, "global record fits");
 static_assert(kGatherPlanRecord % 1024 == 0, "records copy as whole 1 KiB pieces");
 
+// 128-row records (the 8-wave kernel): same layout over 128 rows.
+constexpr int kPlan128Slots = kPlanHeader + 128 * kMaxKvol * 2;  // 6928
+static_assert(kPlan128Slots + HaloSmem<4>::CAP * 4 <= kGatherPlanRecord128, "halo record fits");
+static_assert(kPlanHeader + 128 * kMaxKvol * 4 <= kGatherPlanRecord128, "global record fits");
+static_assert(kGatherPlanRecord128 % 1024 == 0, "records copy as whole 1 KiB pieces");
+// Halo layout of the 8-wave kernel: two buffers of kH8BufRows rows (one per
+// chunk, the next chunk's copied while the current one is in use) with the
+// zero row at slot kH8Double, or, for tiles naming more distinct rows, one
+// buffer with the zero row at kH8Single.
+constexpr int kH8BufRows = 576;
+constexpr int kH8Double = kH8BufRows - 1;        // 575
+constexpr int kH8Single = HaloSmem<4>::CAP;      // 1088
+constexpr int kH8HaloBytes = 2 * kH8BufRows * kHRowBytes;
+static_assert((kH8Single + 1) * kHRowBytes <= kH8HaloBytes, "single buffer fits");
+static_assert(kH8BufRows % 8 == 0, "buffers keep the slot swizzle");
+
 template <int MB, bool PLAN>
 struct HaloLds {
     // Planned kernels keep region0 and the copied record; unplanned ones the
@@ -362,7 +388,7 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_halo_kernel(ConvArg
                 // ---- 5. chunk c of every distinct row into its slot,
                 // straight from memory into LDS (no registers): one
                 // instruction fills 8 consecutive slots (1 KiB, lane L -> byte
-                // 16 L), so lane L loads piece (L % 8) ^ (slot % 8) of its
+                // 16 L), so lane L loads piece (L % 8) ^ halo_swizzle(slot) of its
                 // slot's row -- the swizzle that spreads a gather of 32 slots
                 // over the banks.  Eight lanes read each 128-byte row chunk:
                 // whole cache lines.  Four groups per wave per round: their
@@ -373,7 +399,7 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_halo_kernel(ConvArg
 #pragma unroll
                     for (int k = 0; k < 4; ++k) {
                         const int s = (g0 + 4 * k) * 8 + (lane >> 3);
-                        const int p = (lane & 7) ^ (s & 7);
+                        const int p = (lane & 7) ^ halo_swizzle(s);
                         off[k] = s < static_cast<int>(distinct)
                                      ? (slot_row[min(s, CAP - 1)] * static_cast<uint32_t>(a.cin) + c * kHChunk +
                                         p * 8) * 2u
@@ -427,7 +453,7 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_halo_kernel(ConvArg
                         af[mb] = make_uint4(v.x, v.y, v.z, v.w);
                     } else {
                         const int p = 2 * wave + half;
-                        af[mb] = *reinterpret_cast<const uint4 *>(halo + ix[mb] * kHRowBytes + ((p ^ (ix[mb] & 7)) << 4));
+                        af[mb] = *reinterpret_cast<const uint4 *>(halo + ix[mb] * kHRowBytes + ((p ^ halo_swizzle(ix[mb])) << 4));
                     }
                 }
             };
@@ -550,32 +576,389 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_halo_kernel(ConvArg
     finish_rows<16, ROWS, SM::STG_LD>(a, stg, part, m0, nb0, tile_rows, tid, res);
 }
 
-// One workgroup per 64-row tile: dedupe_tile, then the record to memory.
+// 128-row x 128-column tiles read through 128-row gather-plan records: one
+// workgroup of 8 waves per CU, two waves per SIMD on the same tile.  Wave w
+// holds k-step ks = w % 4 of every 64-channel chunk for column half
+// ch = w / 4 (column blocks 2ch, 2ch+1): 4 x 2 accumulator blocks, two weight
+// fragments and four A fragments per task, so every weight fragment feeds
+// four row blocks (half the weight traffic per MFMA of the 64-row tiles).
+// Tasks run chunk-major, offsets ascending; the weight loads of the next
+// tasks flow on across chunk boundaries.  With two halo buffers (tiles naming
+// at most kH8Double distinct rows) chunk c+1 is copied into the other buffer
+// while chunk c is in use.
+//
+// Every output element is accumulated in the same order as by the 64-row
+// kernel (k-step w's partial: chunks, then offsets, ascending) and the four
+// k-step partials of column block c are summed as ((P_c + P_c+1) + P_c+2) +
+// P_c+3 (indices mod 4), the order of the 64-row kernel's reduction, so the
+// two kernels' results are bit-identical.
+__global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a) {
+    constexpr int ROWS = 128;
+    constexpr int STG_LD = 128 + 8;
+    __shared__ __align__(16) char smem[kH8HaloBytes + kGatherPlanRecord128];
+    char *halo = smem;
+    char *rec = smem + kH8HaloBytes;
+    const uint16_t *table = reinterpret_cast<const uint16_t *>(rec + kPlanHeader);
+    const uint32_t *slot_row = reinterpret_cast<const uint32_t *>(rec + kPlan128Slots);
+    const int32_t *table32 = reinterpret_cast<const int32_t *>(rec + kPlanHeader);
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int ks = wave & 3, ch = wave >> 2;
+    const int half = lane >> 5;
+    const int tile = xcd_tile(blockIdx.x, gridDim.x);
+    const int64_t m0 = static_cast<int64_t>(tile) * ROWS;
+    const int nb0 = blockIdx.y * 4;
+    const int nbtot = a.cout_pad / 32;
+    const int ksteps_total = a.cin / 16;
+    const int chunks = a.cin / kHChunk;
+    const int tile_rows = static_cast<int>(min(static_cast<int64_t>(ROWS), a.n_out - m0));
+    const int32_t xbytes = static_cast<int32_t>(a.x_bytes < INT32_MAX ? a.x_bytes : INT32_MAX);
+    const int64_t w_bytes = static_cast<int64_t>(kMaxKvol) * a.cin * a.cout_pad * 2;
+    const auto w_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(a.w), static_cast<short>(0),
+                                                          static_cast<int32_t>(w_bytes), 0x00020000);
+    const auto x_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(a.x), static_cast<short>(0),
+                                                          xbytes, 0x00020000);
+
+    // ---- 1. the tile's plan record, straight into LDS (1 KiB per instruction)
+    {
+        const int64_t plan_bytes = (a.n_out + ROWS - 1) / ROWS * kGatherPlanRecord128;
+        const auto p_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(a.plan), static_cast<short>(0),
+                                                              static_cast<int32_t>(plan_bytes), 0x00020000);
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+            const int i = wave + 8 * k;
+            if (i < kGatherPlanRecord128 / 1024)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(p_rsrc, (__attribute__((address_space(3))) void *)(rec + i * 1024),
+                                                         16, lane * 16, tile * kGatherPlanRecord128 + i * 1024, 0, 0);
+        }
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        __syncthreads();
+    }
+    const uint32_t *hdr = reinterpret_cast<const uint32_t *>(rec);
+    const bool global_a = __builtin_amdgcn_readfirstlane(hdr[0]) != 0;
+    const uint32_t distinct = __builtin_amdgcn_readfirstlane(hdr[1]);
+    const uint32_t mask = __builtin_amdgcn_readfirstlane(hdr[2]);
+    const bool dbl = !global_a && distinct <= static_cast<uint32_t>(kH8Double);
+    const int zrow = dbl ? kH8Double : kH8Single;
+    if (!global_a && tid < 2 * (kHRowBytes / 16)) {  // the zero row of each buffer in use
+        const int b = tid / (kHRowBytes / 16);
+        if (b == 0 || dbl)
+            reinterpret_cast<uint4 *>(halo + (b * kH8BufRows + zrow) * kHRowBytes)[tid % (kHRowBytes / 16)] =
+                make_uint4(0, 0, 0, 0);
+    }
+
+    // Chunk c of every distinct row into its slot of `buf` (lane L of a
+    // 1 KiB copy fills piece (L % 8) ^ halo_swizzle(slot) of slot 8g + L / 8).
+    auto halo_copy = [&](int c, char *buf) __attribute__((always_inline)) {
+        const int groups = (static_cast<int>(distinct) + 7) >> 3;
+        for (int g0 = wave; g0 < groups; g0 += 32) {
+            uint32_t off[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const int sl = (g0 + 8 * k) * 8 + (lane >> 3);
+                const int p = (lane & 7) ^ halo_swizzle(sl);
+                off[k] = sl < static_cast<int>(distinct)
+                             ? (slot_row[min(sl, kH8Single - 1)] * static_cast<uint32_t>(a.cin) + c * kHChunk + p * 8) * 2u
+                             : 0x80000000u;  // past the buffer: zeros
+            }
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                if (g0 + 8 * k < groups)
+                    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                        x_rsrc, (__attribute__((address_space(3))) void *)(buf + (g0 + 8 * k) * 1024), 16,
+                        static_cast<int32_t>(off[k]), 0, 0, 0);
+        }
+    };
+    auto buf_of = [&](int c) __attribute__((always_inline)) {
+        return halo + (dbl && (c & 1) ? kH8BufRows * kHRowBytes : 0);
+    };
+
+    f32x16 acc[4][2];
+#pragma unroll
+    for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[mb][j] = f32x16{};
+
+    const int ntasks = __popc(mask);
+    const int olast = ntasks > 0 ? 31 - __builtin_clz(mask) : 0;
+    // Offsets walked by scalar cursors, ascending; past the last one a
+    // cursor repeats it (prefetches beyond the end reload it harmlessly).
+    auto advance = [&](uint32_t &rest) __attribute__((always_inline)) {
+        const int o = __builtin_ctz(rest | 0x80000000u);
+        rest &= rest - 1u;
+        return o == 31 ? olast : o;
+    };
+    // Fragment (k-step, column block) of the packed weights sits at byte
+    // ((kstep * nbtot + cb) * 64 + lane) * 16.
+    auto load_b = [&](int c, int o, uint4 (&bf)[2]) __attribute__((always_inline)) {
+        const int32_t sbase = ((o * ksteps_total + c * 4 + ks) * nbtot + nb0 + 2 * ch) * 1024;
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, lane * 16 + j * 1024, sbase, 0);
+            bf[j] = make_uint4(v.x, v.y, v.z, v.w);
+        }
+    };
+    auto mfmas = [&](const uint4 (&af)[4], const uint4 (&bf)[2]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) acc[mb][j] = mfma_step<uint16_t>(af[mb], bf[j], acc[mb][j]);
+    };
+    constexpr int R = 4;  // weight sets in flight (three tasks ahead)
+    uint4 bq[R][2];
+    // The weight cursor runs over (chunk, offset) chunk-major across the
+    // whole loop, so the loads for the next chunk's first tasks go out while
+    // the current chunk ends; past the last task it repeats it (prefetches
+    // beyond the end reload it harmlessly).
+    int cur_c = 0;
+    uint32_t rest_b = mask;
+    auto next_b = [&](uint4 (&bf)[2]) __attribute__((always_inline)) {
+        if (rest_b == 0u) {
+            ++cur_c;
+            rest_b = mask;
+        }
+        const int o = advance(rest_b);
+        load_b(cur_c < chunks ? cur_c : chunks - 1, cur_c < chunks ? o : olast, bf);
+    };
+    // bq[i] <- bq[(i + n) % R]: after a chunk whose task count leaves n
+    // over a multiple of R, the next chunk's task i sits in bq[(n + i) % R].
+    auto rotate_b = [&](int n) __attribute__((always_inline)) {
+        uint4 t[R][2];
+#pragma unroll
+        for (int k = 0; k < R; ++k) t[k][0] = bq[k][0], t[k][1] = bq[k][1];
+#pragma unroll
+        for (int r = 1; r < R; ++r)
+            if (n == r)
+#pragma unroll
+                for (int k = 0; k < R; ++k) bq[k][0] = t[(k + r) % R][0], bq[k][1] = t[(k + r) % R][1];
+    };
+
+    // The chunk loop, for A from the halo (GA false) or from memory (GA
+    // true).  Before chunk c's tasks its halo copy has landed and every wave
+    // is past chunk c-1; with two buffers the copy of chunk c+1 then goes
+    // into the buffer chunk c-1 used.
+    auto chunk_loop = [&](auto ga) __attribute__((always_inline)) {
+        constexpr bool GA = decltype(ga)::value;
+        if (ntasks == 0) return;
+        if constexpr (!GA) halo_copy(0, halo);
+#pragma unroll
+        for (int k = 0; k < R; ++k) {
+            next_b(bq[k]);
+            sched_fence();
+        }
+        for (int c = 0; c < chunks; ++c) {
+            if constexpr (!GA) {
+                if (dbl) {
+                    // The copy of chunk c precedes every weight load of
+                    // chunk c-1's tasks (or, for c = 0, the first R): with
+                    // at least R tasks a chunk, vmcnt(2R) covers it.
+                    if (c == 0 || ntasks >= R) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * R));
+                    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+                    __syncthreads();
+                    if (c + 1 < chunks) halo_copy(c + 1, buf_of(c + 1));
+                } else {
+                    if (c > 0) {
+                        __syncthreads();
+                        halo_copy(c, halo);
+                        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+                    } else {
+                        __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * R));
+                    }
+                    __syncthreads();
+                }
+            }
+            const char *buf = buf_of(c);
+            const int kch = (c * 4 + ks) * 16 + half * 8;  // this lane's first channel of the A fragment
+            auto load_idx = [&](int o, int (&ix)[4]) __attribute__((always_inline)) {
+#pragma unroll
+                for (int mb = 0; mb < 4; ++mb) {
+                    if constexpr (GA) ix[mb] = table32[o * ROWS + mb * 32 + (lane & 31)];
+                    else ix[mb] = table[o * ROWS + mb * 32 + (lane & 31)];
+                }
+            };
+            auto load_a = [&](const int (&ix)[4], uint4 (&af)[4]) __attribute__((always_inline)) {
+#pragma unroll
+                for (int mb = 0; mb < 4; ++mb) {
+                    if constexpr (GA) {
+                        const uint32_t off = ix[mb] >= 0 ? (static_cast<uint32_t>(ix[mb]) * static_cast<uint32_t>(a.cin) +
+                                                            static_cast<uint32_t>(kch)) * 2u
+                                                         : 0x80000000u;
+                        const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, static_cast<int32_t>(off), 0, 0);
+                        af[mb] = make_uint4(v.x, v.y, v.z, v.w);
+                    } else {
+                        const int p = 2 * ks + half;
+                        af[mb] = *reinterpret_cast<const uint4 *>(buf + ix[mb] * kHRowBytes + ((p ^ halo_swizzle(ix[mb])) << 4));
+                    }
+                }
+            };
+            uint4 aq[2][4];
+            int iq[2][4];
+            uint32_t rest_i = mask;
+            load_idx(advance(rest_i), iq[0]);
+            load_idx(advance(rest_i), iq[1]);
+            load_a(iq[0], aq[0]);
+            sched_fence();
+            // task t: A in aq[t & 1], slots of t + 1 in iq[(t + 1) & 1],
+            // weights in bq[t % R]; A(t + 1) is read and the slots of t + 2
+            // looked up while t's MFMAs run, the weights R tasks on
+            // requested right after them.
+            auto body = [&](auto kc) __attribute__((always_inline)) {
+                constexpr int K = decltype(kc)::value, A0 = K & 1, A1 = (K + 1) & 1;
+                load_a(iq[A1], aq[A1]);
+                load_idx(advance(rest_i), iq[A0]);
+                mfmas(aq[A0], bq[K]);
+                sched_fence();
+                next_b(bq[K]);
+                sched_fence();
+            };
+            int t = 0;
+            for (; t + R <= ntasks; t += R) {
+                body(std::integral_constant<int, 0>{});
+                body(std::integral_constant<int, 1>{});
+                body(std::integral_constant<int, 2>{});
+                body(std::integral_constant<int, 3>{});
+            }
+            // Fewer than R tasks left: bq[k] holds task t+k's weights, aq[0]
+            // the A of task t and iq[1] the slots of task t+1; each set used
+            // is refilled with the next weights in the sequence.
+            const int left = ntasks - t;
+            if (left >= 1) {
+                mfmas(aq[0], bq[0]);
+                sched_fence();
+                next_b(bq[0]);
+                sched_fence();
+            }
+            if (left >= 2) {
+                load_a(iq[1], aq[1]);
+                mfmas(aq[1], bq[1]);
+                sched_fence();
+                next_b(bq[1]);
+                sched_fence();
+            }
+            if (left >= 3) {
+                load_idx(advance(rest_i), iq[0]);
+                load_a(iq[0], aq[0]);
+                mfmas(aq[0], bq[2]);
+                sched_fence();
+                next_b(bq[2]);
+                sched_fence();
+            }
+            rotate_b(left);
+        }
+    };
+    if (global_a) chunk_loop(std::true_type{});
+    else chunk_loop(std::false_type{});
+    __syncthreads();  // the halo region becomes the reduction slots
+
+    // ---- 3. reduce the four k-step partials of each 32 x 32 block: wave
+    // (ks, ch) sums row block ks of column blocks 2ch, 2ch+1, one column
+    // block per phase, the others handing theirs over as float4 [4][lane].
+    float4 *red = reinterpret_cast<float4 *>(smem);
+    auto slot_of = [&](int rb, int writer) __attribute__((always_inline)) {
+        return red + ((rb * 2 + ch) * 4 + writer) * (4 * 64);
+    };
+    float fin[2][16];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        if (j) __syncthreads();
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            if (rb == ks) continue;
+            float4 *sl = slot_of(rb, ks);
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                sl[g * 64 + lane] = make_float4(acc[rb][j][4 * g], acc[rb][j][4 * g + 1], acc[rb][j][4 * g + 2],
+                                                acc[rb][j][4 * g + 3]);
+        }
+        __syncthreads();
+        const int cbl = 2 * ch + j;  // column block within the tile
+        // own partial: row block ks (a wave-uniform pick among the four)
+        f32x16 own = acc[0][j];
+#pragma unroll
+        for (int rb = 1; rb < 4; ++rb)
+            if (rb == ks) own = acc[rb][j];
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            float4 term[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int w = (cbl + i) & 3;
+                term[i] = w == ks ? make_float4(own[4 * g], own[4 * g + 1], own[4 * g + 2], own[4 * g + 3])
+                                  : slot_of(ks, w)[g * 64 + lane];
+            }
+            float4 sum = term[0];
+#pragma unroll
+            for (int i = 1; i < 4; ++i) {
+                sum.x += term[i].x;
+                sum.y += term[i].y;
+                sum.z += term[i].z;
+                sum.w += term[i].w;
+            }
+            fin[j][4 * g] = sum.x;
+            fin[j][4 * g + 1] = sum.y;
+            fin[j][4 * g + 2] = sum.z;
+            fin[j][4 * g + 3] = sum.w;
+        }
+    }
+    __syncthreads();
+    float *stg = reinterpret_cast<float *>(smem);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int col = (2 * ch + j) * 32 + (lane & 31);
+        const int rb = ks * 32 + 4 * half;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) stg[(rb + 8 * (r >> 2) + (r & 3)) * STG_LD + col] = fin[j][r];
+    }
+    uint4 res[RowMap<16, ROWS, kHalo8Threads>::PASSES][2];
+    load_residual<16, ROWS, kHalo8Threads>(a, m0, nb0, tile_rows, tid, res);
+    __syncthreads();
+    finish_rows<16, ROWS, STG_LD, kHalo8Threads>(a, stg, stg + ROWS * STG_LD, m0, nb0, tile_rows, tid, res);
+}
+
+// One workgroup per tile (64 or 128 rows): dedupe_tile, then the record to
+// memory.  128-row records name missing neighbours by the zero row of the
+// kernel's halo layout: slot kH8Single when the tile's distinct rows need
+// the single large buffer, else kH8Double (two buffers, one per chunk).
+template <int MB>
 __global__ void __launch_bounds__(256) gather_plan_build_kernel(const int32_t *kmap, int64_t n_out, int64_t n_src,
                                                                 int32_t row_shift, char *plan) {
-    using SM = HaloSmem<2>;
-    __shared__ __align__(16) int32_t table32[64 * kMaxKvol];
-    __shared__ __align__(16) uint16_t table[64 * kMaxKvol];
+    using SM = HaloSmem<MB>;
+    constexpr int ROWS = SM::ROWS;
+    constexpr int REC = MB == 2 ? kGatherPlanRecord : kGatherPlanRecord128;
+    constexpr int SLOTS = MB == 2 ? kPlanSlots : kPlan128Slots;
+    __shared__ __align__(16) int32_t table32[ROWS * kMaxKvol];
+    __shared__ __align__(16) uint16_t table[ROWS * kMaxKvol];
     __shared__ __align__(16) uint32_t bitmap[SM::BITWORDS];
     __shared__ __align__(16) uint32_t prefix[SM::BITWORDS];
     __shared__ __align__(16) uint32_t slot_row[SM::CAP];
     __shared__ __align__(16) int32_t misc[16];
     const int tile = blockIdx.x, tid = threadIdx.x;
-    const int64_t m0 = static_cast<int64_t>(tile) * 64;
-    const int tile_rows = static_cast<int>(min(static_cast<int64_t>(64), n_out - m0));
-    const TileDedupe dd = dedupe_tile<2>(kmap, n_src, row_shift, m0, tile_rows, table, table32, bitmap, prefix,
-                                         slot_row, misc);
-    char *rec = plan + static_cast<int64_t>(tile) * kGatherPlanRecord;
+    const int64_t m0 = static_cast<int64_t>(tile) * ROWS;
+    const int tile_rows = static_cast<int>(min(static_cast<int64_t>(ROWS), n_out - m0));
+    const TileDedupe dd = dedupe_tile<MB>(kmap, n_src, row_shift, m0, tile_rows, table, table32, bitmap, prefix,
+                                          slot_row, misc);
+    char *rec = plan + static_cast<int64_t>(tile) * REC;
     if (tid == 0)
         *reinterpret_cast<uint4 *>(rec) = make_uint4(dd.global_a ? 1u : 0u, dd.distinct, dd.mask, 0u);
     if (dd.global_a) {
-        for (int i = tid; i < 64 * kMaxKvol / 4; i += 256)
+        for (int i = tid; i < ROWS * kMaxKvol / 4; i += 256)
             reinterpret_cast<uint4 *>(rec + kPlanHeader)[i] = reinterpret_cast<const uint4 *>(table32)[i];
     } else {
-        for (int i = tid; i < 64 * kMaxKvol * 2 / 16; i += 256)
-            reinterpret_cast<uint4 *>(rec + kPlanHeader)[i] = reinterpret_cast<const uint4 *>(table)[i];
+        if constexpr (MB == 4) {
+            const uint32_t z = dd.distinct <= static_cast<uint32_t>(kH8Double) ? kH8Double : kH8Single;
+            for (int i = tid; i < ROWS * kMaxKvol / 2; i += 256) {
+                uint32_t v = reinterpret_cast<const uint32_t *>(table)[i];
+                if ((v & 0xFFFFu) == static_cast<uint32_t>(SM::CAP)) v = (v & 0xFFFF0000u) | z;
+                if ((v >> 16) == static_cast<uint32_t>(SM::CAP)) v = (v & 0xFFFFu) | (z << 16);
+                reinterpret_cast<uint32_t *>(rec + kPlanHeader)[i] = v;
+            }
+        } else {
+            for (int i = tid; i < ROWS * kMaxKvol * 2 / 16; i += 256)
+                reinterpret_cast<uint4 *>(rec + kPlanHeader)[i] = reinterpret_cast<const uint4 *>(table)[i];
+        }
         for (int i = tid; i < static_cast<int>(dd.distinct); i += 256)
-            reinterpret_cast<uint32_t *>(rec + kPlanSlots)[i] = slot_row[i];
+            reinterpret_cast<uint32_t *>(rec + SLOTS)[i] = slot_row[i];
     }
 }
 
@@ -585,13 +968,19 @@ KernelFn pick_halo_bf16(int rows) {
     return rows == 128 ? conv_halo_kernel<4, false> : rows == 64 ? conv_halo_kernel<2, false> : nullptr;
 }
 
-KernelFn pick_halo_bf16_planned() { return conv_halo_kernel<2, true>; }
+KernelFn pick_halo_bf16_planned(int rows) {
+    return rows == 64 ? conv_halo_kernel<2, true> : rows == 128 ? conv_halo8_kernel : nullptr;
+}
 
-void launch_gather_plan_build(const int32_t *kmap, int64_t n_out, int64_t n_src, int32_t row_shift, void *plan,
-                              hipStream_t stream) {
-    const unsigned tiles = static_cast<unsigned>((n_out + 63) / 64);
-    hipLaunchKernelGGL(gather_plan_build_kernel, dim3(tiles), dim3(256), 0, stream, kmap, n_out, n_src, row_shift,
-                       static_cast<char *>(plan));
+void launch_gather_plan_build(int rows, const int32_t *kmap, int64_t n_out, int64_t n_src, int32_t row_shift,
+                              void *plan, hipStream_t stream) {
+    const unsigned tiles = static_cast<unsigned>((n_out + rows - 1) / rows);
+    if (rows == 128)
+        hipLaunchKernelGGL(gather_plan_build_kernel<4>, dim3(tiles), dim3(256), 0, stream, kmap, n_out, n_src,
+                           row_shift, static_cast<char *>(plan));
+    else
+        hipLaunchKernelGGL(gather_plan_build_kernel<2>, dim3(tiles), dim3(256), 0, stream, kmap, n_out, n_src,
+                           row_shift, static_cast<char *>(plan));
 }
 
 }  // namespace s3dx

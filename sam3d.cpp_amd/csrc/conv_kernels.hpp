@@ -40,7 +40,8 @@ using KernelFn = void (*)(ConvArgs);
 
 // Workgroup tilings of the MFMA kernel: 4 waves in WM x WN (WM = 4/WN), each
 // wave MBW x NBW blocks of 32x32 outputs.
-// Tilings 20, 21: the halo-staged kernel (conv_halo.hip), 128- and 64-row split-K tiles.
+// Tilings 20, 21: the halo-staged kernel (conv_halo.hip), 128- and 64-row split-K tiles;
+// 22: its 8-wave 128-row variant, launched only with a 128-row gather plan.
 // Split-K tilings (splitk = 1): 128 rows x 32*nbw columns, each wave owning
 // the whole tile for a quarter of the k-steps.  Ids 15 and 16 (BF16, 32- or
 // 64-channel chunks) build each 128-channel task from 4 or 2 chunks.  Ids 17
@@ -56,7 +57,7 @@ inline constexpr Tiling kTilings[] = {
     {5, 1, 4, 2, 0}, {6, 2, 1, 2, 0}, {7, 2, 3, 1, 0}, {8, 2, 2, 2, 0}, {9, 2, 3, 2, 0},
     {10, 1, 4, 1, 0}, {11, 4, 4, 1, 1}, {12, 4, 2, 1, 1}, {13, 4, 3, 1, 1}, {14, 4, 1, 1, 1},
     {15, 4, 3, 1, 1}, {16, 4, 4, 1, 1}, {17, 2, 4, 1, 1}, {18, 2, 4, 1, 1},
-    {19, 2, 3, 1, 1}, {20, 4, 4, 1, 1}, {21, 2, 4, 1, 1},
+    {19, 2, 3, 1, 1}, {20, 4, 4, 1, 1}, {21, 2, 4, 1, 1}, {22, 4, 4, 1, 1},
 };
 
 // MFMA kernel for tiling `id`, kc channels per task, xf 64-bit gathers;
@@ -71,13 +72,16 @@ KernelFn pick_linear_f32(int nbt);
 // padded to whole 128-column tiles, kvol 27, inputs and weights below
 // 2 GiB), else nullptr.
 KernelFn pick_halo_bf16(int rows);
-// The 64-row halo kernel reading a precomputed gather plan (a.plan), the
-// plan builder (one workgroup per 64-row tile), and a plan record's bytes.
-KernelFn pick_halo_bf16_planned();
-void launch_gather_plan_build(const int32_t *kmap, int64_t n_out, int64_t n_src, int32_t row_shift, void *plan,
-                              hipStream_t stream);
-constexpr int kGatherPlanRows = 64;
-constexpr int kGatherPlanRecord = 7168;
+// The halo kernels reading a precomputed gather plan (a.plan): 64-row tiles
+// (4 waves, two workgroups per CU) or 128-row tiles (8 waves, one workgroup
+// per CU, launched with kHalo8Threads threads); the plan builder (one
+// workgroup per tile of `rows` rows); a plan record's bytes.
+KernelFn pick_halo_bf16_planned(int rows);
+constexpr int kHalo8Threads = 512;
+void launch_gather_plan_build(int rows, const int32_t *kmap, int64_t n_out, int64_t n_src, int32_t row_shift,
+                              void *plan, hipStream_t stream);
+constexpr int kGatherPlanRecord = 7168;      // 64-row tiles
+constexpr int kGatherPlanRecord128 = 14336;  // 128-row tiles
 // The FP32 1x1-layer kernel reading BF16 rows, else nullptr.
 KernelFn pick_linear_f32_bf16_rows(int nbt);
 // The same on BF16 MFMAs with three-term split weights (Cin = 16 * ksx,
@@ -198,20 +202,20 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 // Row-major finish of a workgroup's FP32 output tile: TPR threads per row,
-// 8 consecutive columns each, RPP rows per pass over BM rows.
-template <int TPR, int BM>
+// 8 consecutive columns each, RPP rows per pass over BM rows (NTH threads).
+template <int TPR, int BM, int NTH = 256>
 struct RowMap {
-    static constexpr int RPP = 256 / TPR;
+    static constexpr int RPP = NTH / TPR;
     static constexpr int PASSES = (BM + RPP - 1) / RPP;
     static constexpr bool POW2 = (TPR & (TPR - 1)) == 0;  // row groups are aligned lane segments
 };
 
 // Loads the residual values a thread will finish (8 bf16 in [p][0], or 8
 // floats in [p][0..1]); issued early so the latency overlaps other work.
-template <int TPR, int BM>
+template <int TPR, int BM, int NTH = 256>
 __device__ __forceinline__ void load_residual(const ConvArgs &a, int64_t m0, int nb0, int tile_rows, int tid,
-                                              uint4 (&res)[RowMap<TPR, BM>::PASSES][2]) {
-    using RM = RowMap<TPR, BM>;
+                                              uint4 (&res)[RowMap<TPR, BM, NTH>::PASSES][2]) {
+    using RM = RowMap<TPR, BM, NTH>;
     const int cg = tid % TPR, rsub = tid / TPR;
     const int col0 = nb0 * 32 + cg * 8;
 #pragma unroll
@@ -253,11 +257,11 @@ __device__ __forceinline__ void load_residual(const ConvArgs &a, int64_t m0, int
 // (prefetched by load_residual), 16-byte stores.  Row statistics are summed
 // across the row's TPR lanes with shuffles when TPR is a power of two, else
 // through `part` (2*BM*TPR floats of LDS).
-template <int TPR, int BM, int STG_LD>
+template <int TPR, int BM, int STG_LD, int NTH = 256>
 __device__ __forceinline__ void finish_rows(const ConvArgs &a, const float *stg, float *part, int64_t m0,
                                             int nb0, int tile_rows, int tid,
-                                            const uint4 (&res)[RowMap<TPR, BM>::PASSES][2]) {
-    using RM = RowMap<TPR, BM>;
+                                            const uint4 (&res)[RowMap<TPR, BM, NTH>::PASSES][2]) {
+    using RM = RowMap<TPR, BM, NTH>;
     constexpr int RPP = RM::RPP;
     constexpr int PASSES = RM::PASSES;
     const int cg = tid % TPR, rsub = tid / TPR;

@@ -56,8 +56,21 @@ def _oracle(O, W, x, kmap, n, cin, cout, seed, ln, res=None):
     return h + res if res is not None else h
 
 
+def _sparse_points(step, pair):
+    """Points on a lattice of `step` (no neighbours: one present offset per
+    tile), or (pair) z-adjacent pairs (three present offsets)."""
+    g = np.stack(np.meshgrid(*(np.arange(0, 60, step),) * 3, indexing="ij"), -1).reshape(-1, 3)
+    if pair:
+        g = np.concatenate([g, g + np.array([0, 0, 1])])
+        g = g[np.lexsort((g[:, 2], g[:, 1], g[:, 0]))]
+    c = np.concatenate([np.zeros((len(g), 1), np.int64), g], 1).astype(np.int32)
+    return np.ascontiguousarray(c)
+
+
 CASES = {
     # name: (coords builder, cin, cout, LayerNorm+SiLU+residual)
+    "isolated_points_cin256": (lambda W: _sparse_points(3, False), 256, 128, True),  # fewer tasks than in flight
+    "point_pairs_cin256": (lambda W: _sparse_points(4, True), 256, 128, False),
     "shells_union_28265": (lambda W: W.shells_union(0), 128, 128, True),
     "shells_union_3000_cin256": (lambda W: W.shells_union(1)[:3000], 256, 128, False),
     "shuffled_cube_13824": (lambda W: _dense_cube(24, 0), 128, 128, True),          # every tile global
@@ -83,6 +96,10 @@ def test_planned_run_equals_unplanned(s3dx, O, W, monkeypatch, case):
     xd, kd = _bf(s3dx, W, x), s3dx.DeviceArray.from_host(kmap)
     rd = _bf(s3dx, W, res) if ln else None
     gp = conv.gather_plan(n, kd, n)
+    planned = conv.plan(n, n, gp)
+    print(f"  planned: {planned}", flush=True)
+    # one pass of 128-row tiles over the CUs: the 8-wave kernel
+    assert planned.startswith("mfma tiling=22 split-k halo rows=128") and planned.endswith("plan=128"), planned
     y0 = s3dx.DeviceArray((n, cout), np.uint16)
     y1 = s3dx.DeviceArray((n, cout), np.uint16)
     conv.run(xd, n, kd, n, y0, s3dx.BF16, rd)
@@ -110,6 +127,9 @@ def test_planned_config3_rows(s3dx, O, W):
     conv = s3dx.SparseConv(c, c, 27, s3dx.BF16).set_weights(W.conv_weight(0, 301, c, c), s3dx.WEIGHT_SLAT, None)
     xd, kd = _bf(s3dx, W, W.round_bf16(W.normal_f32(0, 300, (nc, c)))), s3dx.DeviceArray.from_host(kmap)
     gp = conv.gather_plan(nc, kd, nc)
+    planned = conv.plan(nc, nc, gp)
+    # 40 x 8 128-row tiles would need two passes over 256 CUs: 64-row records
+    assert planned.startswith("mfma tiling=21 split-k halo rows=64") and planned.endswith("grid=80x8 plan=64"), planned
     y0, y1 = s3dx.DeviceArray((nc, c), np.uint16), s3dx.DeviceArray((nc, c), np.uint16)
     conv.run(xd, nc, kd, nc, y0, s3dx.BF16)
     conv.run(xd, nc, kd, nc, y1, s3dx.BF16, plan=gp)
@@ -185,3 +205,26 @@ def test_plan_rebuild_in_place(s3dx, O, W, monkeypatch):
     with pytest.raises(s3dx.S3dxError) as e:
         gp.rebuild(conv, 6001, kb, 6001)
     assert e.value.status == s3dx.INVALID_ARGUMENT
+
+
+@pytest.mark.parametrize("rows", ["64", "128"])
+def test_plan_tile_heights_agree(s3dx, O, W, monkeypatch, rows):
+    # Both planned kernels (64-row records, 4 waves; 128-row records, 8
+    # waves) on the config-2 block, bit-identical to the unplanned run.
+    monkeypatch.delenv("S3DX_CONV_TILING", raising=False)
+    monkeypatch.delenv("S3DX_CONV_HALO", raising=False)
+    monkeypatch.setenv("S3DX_PLAN_ROWS", rows)
+    coords = W.shells_union(0)
+    n = coords.shape[0]
+    kd = s3dx.DeviceArray.from_host(O.kmap_subm3(coords, n))
+    conv = _layer(s3dx, W, 128, 128, 45, True)
+    gp = conv.gather_plan(n, kd, n)
+    planned = conv.plan(n, n, gp)
+    print(f"rows {rows}: {planned}", flush=True)
+    assert planned.endswith(f"plan={rows}") and f"rows={rows}" in planned, planned
+    xd = _bf(s3dx, W, W.normal_f32(45, 1, (n, 128)))
+    res = _bf(s3dx, W, W.normal_f32(45, 4, (n, 128)))
+    y0, y1 = s3dx.DeviceArray((n, 128), np.uint16), s3dx.DeviceArray((n, 128), np.uint16)
+    conv.run(xd, n, kd, n, y0, s3dx.BF16, res)
+    conv.run(xd, n, kd, n, y1, s3dx.BF16, res, plan=gp)
+    assert np.array_equal(y0.download(), y1.download())

@@ -151,3 +151,35 @@ def test_coarsen_subdivide_reused_buffers(s3dx, W):
         child2, kmap2 = s3dx.subdivide2(d, m, True)
         assert np.array_equal(child.download()[: 8 * m], child2.download())
         assert np.array_equal(kmap.download()[: 8 * m], kmap2.download())
+
+
+def test_workspace_reuse_and_garbage(s3dx, O, W):
+    # One workspace across builds of different sets -- window cells (batch 0,
+    # [0, 64)^3), hashed coordinates (outside the window, other batches, wide
+    # int32 values) and duplicates -- first as left by earlier builds, then
+    # filled with random bytes: no word of an earlier build or of the bytes
+    # may surface in a later map.
+    rng = np.random.default_rng(5)
+    big = W.shells_union(0)
+    dup = np.concatenate([big[:3000], big[1000:2500]])
+    rng.shuffle(dup)
+    batch1 = big[:5000].copy()
+    batch1[:, 0] = 1
+    wide = big[:2000].copy()
+    wide[::5, 1] += 70000  # beyond int16: matched through the input rows
+    sets = {"shells": big, "shells_every_3rd": big[::3],
+            "shifted_x40": big + np.array([0, 40, 0, 0], np.int32),
+            "shifted_negative": big - np.array([0, 30, 30, 30], np.int32),
+            "two_batches": np.concatenate([big[:5000], batch1]),
+            "duplicates": dup, "wide": wide, "shells_again": big}
+    n_max = max(c.shape[0] for c in sets.values())
+    ws = s3dx.DeviceArray(s3dx.kmap_workspace_size(n_max), np.uint8)
+    for garbage in (False, True):
+        if garbage:
+            ws.upload(rng.integers(0, 256, size=ws.nbytes, dtype=np.uint8))
+        for name, c in sets.items():
+            c = np.ascontiguousarray(c, np.int32)
+            n = c.shape[0]
+            print(f"kmap reuse garbage={garbage} {name} n={n}", flush=True)
+            got = s3dx.kmap_subm3(s3dx.DeviceArray.from_host(c), n, -1, workspace=ws).download()
+            assert np.array_equal(got, O.kmap_subm3(c, -1)), name
