@@ -141,7 +141,8 @@ S3DX_API s3dx_status s3dx_coarsen2_workspace_size(int64_t n, uint64_t *bytes, ch
  *   coarse_inv_count float [n]     (1/(count+1), the scatter-mean quirk)
  *   *nc_out         host int64
  * The coarse kernel map is s3dx_kmap_subm3(coarse_coords, nc, nc, ...)
- * (sparse_ops.cpp:142).  Synchronizes `stream` to return nc. */
+ * (sparse_ops.cpp:142).  Sort-based: O(n log n) for any int32 coordinates
+ * and bounding box.  Synchronizes `stream` once, to return nc. */
 S3DX_API s3dx_status s3dx_coarsen2(const int32_t *coords, int64_t n, int32_t *coarse_coords,
                                    int32_t *fine_to_coarse, int32_t *coarse_children,
                                    float *coarse_inv_count, int64_t *nc_out, void *workspace,

@@ -105,7 +105,7 @@ unsigned blocks_for(int64_t items) { return static_cast<unsigned>((items + kThre
 
 // Grid of a bounds reduction: at most 128 blocks, each thread striding over
 // the items, so the per-block atomics stay few.
-unsigned bounds_blocks(int64_t items) { return blocks_for(items) < 128u ? blocks_for(items) : 128u; }
+inline unsigned bounds_blocks(int64_t items) { return blocks_for(items) < 128u ? blocks_for(items) : 128u; }
 
 // Block-wide min of v[0..M) and max of v[M..2M), committed with one atomic
 // per value per block: a wave butterfly, then the block's waves through LDS.
@@ -156,7 +156,7 @@ void hash_layout(W &w, int64_t n, Hash *h) {
 }
 
 // Clears the table and inserts n keys (first occurrence wins).
-void hash_build(const int4 *keys, int32_t n, Hash &h, hipStream_t stream) {
+inline void hash_build(const int4 *keys, int32_t n, Hash &h, hipStream_t stream) {
     h.keys = keys;
     const uint64_t cap = static_cast<uint64_t>(h.mask) + 1;
     hash_clear_kernel<<<blocks_for(static_cast<int64_t>(cap)), kThreads, 0, stream>>>(h);

@@ -1,5 +1,5 @@
-// Kernel maps on the GPU: the coordinate hash, the 27-offset submanifold
-// neighbour table, the 2x OR-pool (coarse set) and the exact 2x subdivide.
+// Kernel maps on the GPU: the 27-offset submanifold neighbour table and the
+// exact 2x subdivide (the 2x coarsen is in coarsen.hip).
 //
 // Reference semantics (all host C++ in sam3d.cpp):
 //   build_conv            src/objects_runtime/sparse_ops.cpp:117-142
@@ -252,156 +252,6 @@ child_kmap_kernel(const int32_t *__restrict__ parent_kmap, int32_t p, int32_t *_
     kmap[g] = t >= 0 ? t * 8 + cs : -1;
 }
 
-// ---- coarsen ---------------------------------------------------------------
-__global__ void __launch_bounds__(kThreads)
-coarse_keys_kernel(const int4 *__restrict__ coords, int32_t n, int4 *__restrict__ ckeys,
-                   int32_t *bbox) {
-    int v[8] = {INT32_MAX, INT32_MAX, INT32_MAX, INT32_MAX, INT32_MIN, INT32_MIN, INT32_MIN, INT32_MIN};
-    for (int32_t i = blockIdx.x * kThreads + threadIdx.x; i < n; i += gridDim.x * kThreads) {
-        const int4 c = coords[i];
-        // C++ integer division truncates toward zero (sparse_ops.cpp:63-64).
-        const int4 k = make_int4(c.x, c.y / 2, c.z / 2, c.w / 2);
-        ckeys[i] = k;
-        v[0] = min(v[0], k.x); v[1] = min(v[1], k.y); v[2] = min(v[2], k.z); v[3] = min(v[3], k.w);
-        v[4] = max(v[4], k.x); v[5] = max(v[5], k.y); v[6] = max(v[6], k.z); v[7] = max(v[7], k.w);
-    }
-    block_bounds_atomic<4>(v, bbox);
-}
-
-struct DenseGrid {
-    int32_t lo[4];
-    int64_t ext[4];
-};
-
-__device__ __forceinline__ int64_t dense_cell(const DenseGrid &g, int4 k) {
-    return ((static_cast<int64_t>(k.x) - g.lo[0]) * g.ext[1] + (static_cast<int64_t>(k.y) - g.lo[1])) *
-               g.ext[2] * g.ext[3] +
-           (static_cast<int64_t>(k.z) - g.lo[2]) * g.ext[3] + (static_cast<int64_t>(k.w) - g.lo[3]);
-}
-
-// Dense path: every occupied coarse cell is marked; the exclusive scan over
-// the row-major (b, x, y, z) cell index is then the lexicographic rank.
-__global__ void __launch_bounds__(kThreads)
-dense_mark_kernel(const int4 *__restrict__ ckeys, int32_t n, DenseGrid g, int32_t *mark) {
-    const int32_t i = blockIdx.x * kThreads + threadIdx.x;
-    if (i < n) mark[dense_cell(g, ckeys[i])] = 1;
-}
-
-__global__ void __launch_bounds__(kThreads)
-dense_assign_kernel(const int4 *__restrict__ ckeys, int32_t n, DenseGrid g,
-                    const int32_t *__restrict__ rank, int32_t *__restrict__ f2c,
-                    int4 *__restrict__ coarse_coords) {
-    const int32_t i = blockIdx.x * kThreads + threadIdx.x;
-    if (i >= n) return;
-    const int4 k = ckeys[i];
-    const int32_t r = rank[dense_cell(g, k)];
-    f2c[i] = r;
-    coarse_coords[r] = k;  // every writer of row r stores the same key
-}
-
-// General path (bounding box too large for a dense grid): representatives
-// (the smallest fine row of each coarse key) are ranked by counting smaller
-// keys, O(nc^2) comparisons tiled through LDS.
-__global__ void __launch_bounds__(kThreads)
-rep_flag_kernel(const int4 *__restrict__ ckeys, int32_t n, Hash h, int32_t *__restrict__ rep,
-                int32_t *__restrict__ is_rep) {
-    const int32_t i = blockIdx.x * kThreads + threadIdx.x;
-    if (i >= n) return;
-    const int32_t r = hash_find(h, ckeys[i]);
-    rep[i] = r;
-    is_rep[i] = r == i ? 1 : 0;
-}
-
-__global__ void __launch_bounds__(kThreads)
-rep_compact_kernel(const int32_t *__restrict__ is_rep, const int32_t *__restrict__ pos, int32_t n,
-                   int32_t *__restrict__ reps) {
-    const int32_t i = blockIdx.x * kThreads + threadIdx.x;
-    if (i < n && is_rep[i]) reps[pos[i]] = i;
-}
-
-__device__ __forceinline__ bool key_less(int4 a, int4 b) {
-    if (a.x != b.x) return a.x < b.x;
-    if (a.y != b.y) return a.y < b.y;
-    if (a.z != b.z) return a.z < b.z;
-    return a.w < b.w;
-}
-
-__global__ void __launch_bounds__(kThreads)
-rank_count_kernel(const int4 *__restrict__ ckeys, const int32_t *__restrict__ reps, int32_t nc,
-                  int32_t *__restrict__ rank_of) {
-    __shared__ int4 tile[kThreads];
-    const int32_t u = blockIdx.x * kThreads + threadIdx.x;
-    const int4 mine = u < nc ? ckeys[reps[u]] : make_int4(0, 0, 0, 0);
-    int32_t rank = 0;
-    for (int32_t t0 = 0; t0 < nc; t0 += kThreads) {
-        const int32_t v = t0 + threadIdx.x;
-        __syncthreads();
-        if (v < nc) tile[threadIdx.x] = ckeys[reps[v]];
-        __syncthreads();
-        const int32_t m = min(kThreads, nc - t0);
-        for (int32_t j = 0; j < m; ++j) rank += key_less(tile[j], mine) ? 1 : 0;
-    }
-    if (u < nc) rank_of[u] = rank;
-}
-
-__global__ void __launch_bounds__(kThreads)
-general_assign_kernel(const int4 *__restrict__ ckeys, int32_t n, const int32_t *__restrict__ rep,
-                      const int32_t *__restrict__ pos, const int32_t *__restrict__ rank_of,
-                      int32_t *__restrict__ f2c, int4 *__restrict__ coarse_coords) {
-    const int32_t i = blockIdx.x * kThreads + threadIdx.x;
-    if (i >= n) return;
-    const int32_t r = rank_of[pos[rep[i]]];
-    f2c[i] = r;
-    if (rep[i] == i) coarse_coords[r] = ckeys[i];
-}
-
-// Children lists: counts -> offsets -> bucketed fine rows -> the 8 smallest
-// per coarse row in ascending order (sparse_ops.cpp:82-104).
-__global__ void __launch_bounds__(kThreads)
-child_count_kernel(const int32_t *__restrict__ f2c, int32_t n, int32_t *counts) {
-    const int32_t i = blockIdx.x * kThreads + threadIdx.x;
-    if (i < n) atomicAdd(&counts[f2c[i]], 1);
-}
-
-__global__ void __launch_bounds__(kThreads)
-child_bucket_kernel(const int32_t *__restrict__ f2c, int32_t n, const int32_t *__restrict__ start,
-                    int32_t *fill, int32_t *__restrict__ bucket) {
-    const int32_t i = blockIdx.x * kThreads + threadIdx.x;
-    if (i >= n) return;
-    const int32_t c = f2c[i];
-    bucket[start[c] + atomicAdd(&fill[c], 1)] = i;
-}
-
-__global__ void __launch_bounds__(kThreads)
-child_select_kernel(const int32_t *__restrict__ bucket, const int32_t *__restrict__ start,
-                    const int32_t *__restrict__ counts, int32_t nc, int32_t n,
-                    int32_t *__restrict__ children, float *__restrict__ inv_count) {
-    const int32_t c = blockIdx.x * kThreads + threadIdx.x;
-    if (c >= nc) return;
-    const int32_t s = start[c], k = counts[c];
-    int32_t prev = -1;
-    for (int j = 0; j < 8; ++j) {
-        // j-th smallest: the smallest entry greater than the previous pick
-        // (entries are distinct fine rows).
-        int32_t best = INT32_MAX;
-        for (int32_t t = 0; t < k; ++t) {
-            const int32_t v = bucket[s + t];
-            if (v > prev && v < best) best = v;
-        }
-        const bool have = j < k;
-        children[static_cast<int64_t>(c) * 8 + j] = have ? best : n;
-        if (have) prev = best;
-    }
-    inv_count[c] = 1.0f / static_cast<float>(k + 1);
-}
-
-// Dense coarse grids up to this many cells use the scan path.
-uint64_t dense_cell_cap(int64_t n) {
-    const uint64_t a = uint64_t(1) << 21;
-    const uint64_t b = static_cast<uint64_t>(n) * 64;
-    return a > b ? a : b;
-}
-
 constexpr uint64_t kmap_capacity(int64_t n) {
     uint64_t cap = 256;
     while (cap < static_cast<uint64_t>(n) * 4) cap <<= 1;
@@ -491,50 +341,6 @@ void subdivide_layout(W &w, int64_t p, SubdivideLayout *l) {
     } else {
         kmap_layout(w, p, static_cast<KmapHash *>(nullptr));
         w.template take<int32_t>(static_cast<uint64_t>(p) * 27);
-    }
-}
-}  // namespace
-namespace {
-struct CoarsenLayout {
-    int4 *ckeys;
-    Hash hash;
-    int32_t *bbox;
-    int32_t *totals;
-    int32_t *a, *b, *c, *d;  // n-sized scratch
-    int32_t *counts, *start, *fill, *bucket;
-    int32_t *dense_mark, *dense_rank;
-    void *scan_ws;
-};
-template <class W>
-void coarsen_layout(W &w, int64_t n, CoarsenLayout *l) {
-    const uint64_t un = static_cast<uint64_t>(n);
-    const uint64_t cells = dense_cell_cap(n);
-    const uint64_t scan_items = cells > un ? cells : un;
-    if constexpr (std::is_same_v<W, Carver>) {
-        l->ckeys = w.template take<int4>(un);
-        hash_layout(w, n, &l->hash);
-        l->bbox = w.template take<int32_t>(8);
-        l->totals = w.template take<int32_t>(8);
-        l->a = w.template take<int32_t>(un);
-        l->b = w.template take<int32_t>(un);
-        l->c = w.template take<int32_t>(un);
-        l->d = w.template take<int32_t>(un);
-        l->counts = w.template take<int32_t>(un);
-        l->start = w.template take<int32_t>(un);
-        l->fill = w.template take<int32_t>(un);
-        l->bucket = w.template take<int32_t>(un);
-        l->dense_mark = w.template take<int32_t>(cells);
-        l->dense_rank = w.template take<int32_t>(cells);
-        l->scan_ws = w.template take<char>(scan_workspace_bytes(static_cast<int64_t>(scan_items)));
-    } else {
-        w.template take<int4>(un);
-        hash_layout(w, n, static_cast<Hash *>(nullptr));
-        w.template take<int32_t>(8);
-        w.template take<int32_t>(8);
-        for (int k = 0; k < 8; ++k) w.template take<int32_t>(un);
-        w.template take<int32_t>(cells);
-        w.template take<int32_t>(cells);
-        w.template take<char>(scan_workspace_bytes(static_cast<int64_t>(scan_items)));
     }
 }
 }  // namespace
@@ -636,108 +442,5 @@ S3DX_API s3dx_status s3dx_subdivide2(const int32_t *parent_coords, int64_t paren
     });
 }
 
-
-S3DX_API s3dx_status s3dx_coarsen2_workspace_size(int64_t n, uint64_t *bytes, char *error,
-                                                  uint64_t error_capacity) {
-    return boundary(error, error_capacity, [&] {
-        require(bytes != nullptr, "bytes is NULL");
-        require(n > 0 && n <= INT32_MAX / 27, "voxel count out of range");
-        Sizer s;
-        coarsen_layout(s, n, nullptr);
-        *bytes = s.used;
-    });
-}
-
-S3DX_API s3dx_status s3dx_coarsen2(const int32_t *coords, int64_t n, int32_t *coarse_coords,
-                                   int32_t *fine_to_coarse, int32_t *coarse_children,
-                                   float *coarse_inv_count, int64_t *nc_out, void *workspace,
-                                   uint64_t workspace_bytes, s3dx_stream stream, char *error,
-                                   uint64_t error_capacity) {
-    return boundary(error, error_capacity, [&] {
-        check_coords(coords, n);
-        require(coarse_coords && fine_to_coarse && coarse_children && coarse_inv_count && nc_out,
-                "NULL output");
-        require(aligned(coarse_coords, 16), "coarse_coords must be 16-byte aligned");
-        require(workspace != nullptr, "workspace is NULL");
-        const hipStream_t s = as_stream(stream);
-        const int32_t ni = static_cast<int32_t>(n);
-        Carver w(workspace, workspace_bytes);
-        CoarsenLayout l;
-        coarsen_layout(w, n, &l);
-        const int4 *c4 = reinterpret_cast<const int4 *>(coords);
-        int4 *cc4 = reinterpret_cast<int4 *>(coarse_coords);
-
-        // 1. coarse keys + their bounding box.
-        fill_u32(reinterpret_cast<uint32_t *>(l.bbox), 4, static_cast<uint32_t>(INT32_MAX), s);
-        fill_u32(reinterpret_cast<uint32_t *>(l.bbox) + 4, 4, static_cast<uint32_t>(INT32_MIN), s);
-        coarse_keys_kernel<<<bounds_blocks(ni), kThreads, 0, s>>>(c4, ni, l.ckeys, l.bbox);
-        launch_check("coarse_keys");
-        int32_t bbox[8];
-        hip_check(hipMemcpyAsync(bbox, l.bbox, sizeof(bbox), hipMemcpyDeviceToHost, s),
-                  "hipMemcpyAsync bbox");
-        hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
-
-        DenseGrid g;
-        bool dense = true;
-        uint64_t cells = 1;
-        for (int a = 0; a < 4; ++a) {
-            g.lo[a] = bbox[a];
-            g.ext[a] = static_cast<int64_t>(bbox[4 + a]) - bbox[a] + 1;
-            const uint64_t e = static_cast<uint64_t>(g.ext[a]);
-            if (cells > dense_cell_cap(n) / e) dense = false;
-            else cells *= e;
-        }
-        dense = dense && cells <= dense_cell_cap(n);
-
-        int32_t nc = 0;
-        if (dense) {
-            // 2a. mark occupied cells, scan -> lexicographic rank.
-            fill_u32(reinterpret_cast<uint32_t *>(l.dense_mark), cells, 0, s);
-            dense_mark_kernel<<<blocks_for(ni), kThreads, 0, s>>>(l.ckeys, ni, g, l.dense_mark);
-            launch_check("dense_mark");
-            exclusive_scan_i32(l.dense_mark, l.dense_rank, static_cast<int64_t>(cells), l.totals,
-                               l.scan_ws, s);
-            dense_assign_kernel<<<blocks_for(ni), kThreads, 0, s>>>(l.ckeys, ni, g, l.dense_rank,
-                                                                    fine_to_coarse, cc4);
-            launch_check("dense_assign");
-        } else {
-            // 2b. dedupe through the hash, rank representatives by counting.
-            hash_build(l.ckeys, ni, l.hash, s);
-            int32_t *rep = l.a, *is_rep = l.b, *pos = l.c, *rank_of = l.d;
-            rep_flag_kernel<<<blocks_for(ni), kThreads, 0, s>>>(l.ckeys, ni, l.hash, rep, is_rep);
-            launch_check("rep_flag");
-            exclusive_scan_i32(is_rep, pos, ni, l.totals, l.scan_ws, s);
-            int32_t *reps = l.bucket;  // free until the children pass
-            rep_compact_kernel<<<blocks_for(ni), kThreads, 0, s>>>(is_rep, pos, ni, reps);
-            launch_check("rep_compact");
-            hip_check(hipMemcpyAsync(&nc, l.totals, sizeof(nc), hipMemcpyDeviceToHost, s),
-                      "hipMemcpyAsync nc");
-            hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
-            rank_count_kernel<<<blocks_for(nc), kThreads, 0, s>>>(l.ckeys, reps, nc, rank_of);
-            launch_check("rank_count");
-            general_assign_kernel<<<blocks_for(ni), kThreads, 0, s>>>(l.ckeys, ni, rep, pos, rank_of,
-                                                                      fine_to_coarse, cc4);
-            launch_check("general_assign");
-        }
-        hip_check(hipMemcpyAsync(&nc, l.totals, sizeof(nc), hipMemcpyDeviceToHost, s),
-                  "hipMemcpyAsync nc");
-        hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
-        require(nc > 0 && nc <= ni, "coarse row count out of range");
-
-        // 3. children (8 smallest fine rows per coarse row) and 1/(count+1).
-        fill_u32(reinterpret_cast<uint32_t *>(l.counts), static_cast<uint64_t>(nc), 0, s);
-        fill_u32(reinterpret_cast<uint32_t *>(l.fill), static_cast<uint64_t>(nc), 0, s);
-        child_count_kernel<<<blocks_for(ni), kThreads, 0, s>>>(fine_to_coarse, ni, l.counts);
-        launch_check("child_count");
-        exclusive_scan_i32(l.counts, l.start, nc, l.totals + 1, l.scan_ws, s);
-        child_bucket_kernel<<<blocks_for(ni), kThreads, 0, s>>>(fine_to_coarse, ni, l.start, l.fill,
-                                                                l.bucket);
-        launch_check("child_bucket");
-        child_select_kernel<<<blocks_for(nc), kThreads, 0, s>>>(l.bucket, l.start, l.counts, nc, ni,
-                                                                coarse_children, coarse_inv_count);
-        launch_check("child_select");
-        *nc_out = nc;
-    });
-}
 
 }  // extern "C"

@@ -78,11 +78,12 @@ def test_random_sets_with_duplicates_and_batches(s3dx, O):
         assert np.array_equal(inv.download()[:nc], oinv)
 
 
-def test_coarsen_general_path_wide_bbox(s3dx, O):
-    # Coordinates spread over ~2^30: the dense rank grid cannot hold the box,
-    # so the counting-rank path runs.
+@pytest.mark.parametrize("n", [3000, 200000])
+def test_coarsen_wide_bbox(s3dx, O, n):
+    # Coordinates spread over ~2^30 (negative ones too, two batches, half the
+    # rows repeated): the sort-based coarsen orders any int32 keys, in
+    # O(n log n) -- 200k rows of 100k distinct wide keys in one call.
     rng = np.random.default_rng(77)
-    n = 3000
     c = rng.integers(-2**30, 2**30, size=(n, 4)).astype(np.int32)
     c[:, 0] = rng.integers(0, 2, size=n)
     c[n // 2:] = c[: n - n // 2]  # duplicates
@@ -93,7 +94,9 @@ def test_coarsen_general_path_wide_bbox(s3dx, O):
     assert np.array_equal(cc.download()[:nc], occ)
     assert np.array_equal(f2c.download(), of2c)
     assert np.array_equal(ch.download()[: 8 * nc], och)
-    assert np.array_equal(gpu_kmap(s3dx, c, n), O.kmap_subm3(c, n))
+    assert np.array_equal(inv.download()[:nc].view(np.uint32), oinv.view(np.uint32))
+    if n <= 3000:
+        assert np.array_equal(gpu_kmap(s3dx, c, n), O.kmap_subm3(c, n))
 
 
 def test_subdivide_rejects_duplicates(s3dx):
