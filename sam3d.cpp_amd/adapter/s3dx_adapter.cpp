@@ -103,9 +103,11 @@ __attribute__((visibility("default"))) s3dx_status s3dx_adapter_res_block(
         s3d::SlatResBlock block(cin, cout, false, n1w, n1b, w1, b1, w2, b2, ws, bs, st.s);
         s3d::DeviceBuffer dx(uint64_t(n) * cin * 4), dy(uint64_t(n) * cout * 4), tmp;
         dx.upload(x, uint64_t(n) * cin * 4, st.s);
+        // Odd forwards run with the fine map's gather plan: same results.
+        s3d::GatherPlan plan(block.conv1, n, t.conv_fine.get<int32_t>(), st.s);
         for (int f = 0; f < forwards; ++f) {
             block.forward(dx.get(), n, t.conv_fine.get<int32_t>(), scale + uint64_t(f) * cout,
-                          shift + uint64_t(f) * cout, dy.get(), tmp, st.s);
+                          shift + uint64_t(f) * cout, dy.get(), tmp, st.s, f % 2 ? plan.get() : nullptr);
             dy.download(y + uint64_t(f) * n * cout, uint64_t(n) * cout * 4, st.s);
         }
         return S3DX_OK;

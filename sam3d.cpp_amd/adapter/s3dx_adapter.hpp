@@ -141,10 +141,16 @@ public:
     ~SparseConvLayer() { s3dx_conv_free(c_); }
     s3dx_conv *get() const { return c_; }
     explicit operator bool() const { return c_ != nullptr; }
+    // With a gather plan of kmap (GatherPlan below) the halo kernels skip
+    // their per-tile dedupe; results are the same bits either way.
     void run(const void *x, int64_t n_in, const int32_t *kmap, int64_t n_out, const void *residual, void *y,
-             int32_t y_dtype, s3dx_stream s) const {
+             int32_t y_dtype, s3dx_stream s, const s3dx_gather_plan *plan = nullptr) const {
         char err[512];
-        s3dx_check(s3dx_conv_run(c_, x, n_in, kmap, n_out, residual, y, y_dtype, s, err, sizeof err), err);
+        if (plan)
+            s3dx_check(s3dx_conv_run_planned(c_, plan, x, n_in, kmap, n_out, residual, y, y_dtype, s, err,
+                                             sizeof err), err);
+        else
+            s3dx_check(s3dx_conv_run(c_, x, n_in, kmap, n_out, residual, y, y_dtype, s, err, sizeof err), err);
     }
     std::string plan(int64_t n_in, int64_t n_out) const {
         char buf[256], err[256];
@@ -154,6 +160,39 @@ public:
 
 private:
     s3dx_conv *c_ = nullptr;
+};
+
+// A kernel map's gather plan (s3dx_gather_plan): built once per map -- as
+// SlatTables are, once per sample -- and shared by every conv over that map
+// whose source rows are the map's rows (all SLat convs).  rebuild() refills
+// it for the next sample's map without allocating (at most the rows it was
+// built for).
+class GatherPlan {
+public:
+    GatherPlan() = default;
+    GatherPlan(const SparseConvLayer &layer, int64_t n, const int32_t *kmap, s3dx_stream s) {
+        char err[512];
+        s3dx_check(s3dx_gather_plan_create(layer.get(), n, kmap, n, s, &p_, err, sizeof err), err);
+    }
+    GatherPlan(const GatherPlan &) = delete;
+    GatherPlan &operator=(const GatherPlan &) = delete;
+    GatherPlan(GatherPlan &&o) noexcept : p_(std::exchange(o.p_, nullptr)) {}
+    GatherPlan &operator=(GatherPlan &&o) noexcept {
+        if (this != &o) {
+            s3dx_gather_plan_free(p_);
+            p_ = std::exchange(o.p_, nullptr);
+        }
+        return *this;
+    }
+    ~GatherPlan() { s3dx_gather_plan_free(p_); }
+    void rebuild(const SparseConvLayer &layer, int64_t n, const int32_t *kmap, s3dx_stream s) {
+        char err[512];
+        s3dx_check(s3dx_gather_plan_rebuild(p_, layer.get(), n, kmap, n, s, err, sizeof err), err);
+    }
+    const s3dx_gather_plan *get() const { return p_; }
+
+private:
+    s3dx_gather_plan *p_ = nullptr;
 };
 
 // At weight load: SLat weights are [Cout][27][Cin] (gguf_schema.py:326-334),
@@ -201,11 +240,12 @@ struct SlatResBlock {
         else if (cin != cout) throw s3dx_failure(S3DX_INVALID_ARGUMENT, "s3d: res_block skip needs a Linear");
     }
 
-    // One forward on n rows of x (device, the layers' dtype) over kmap.
-    // scale/shift: host [cout], this forward's emb_layers halves.  The
-    // temporaries come from `tmp` (3 * n * max(cin, cout) elements).
+    // One forward on n rows of x (device, the layers' dtype) over kmap (and
+    // its gather plan, or NULL).  scale/shift: host [cout], this forward's
+    // emb_layers halves.  The temporaries come from `tmp` (3 * n * max(cin,
+    // cout) elements).
     void forward(const void *x, int64_t n, const int32_t *kmap, const float *scale, const float *shift, void *y,
-                 DeviceBuffer &tmp, s3dx_stream s) {
+                 DeviceBuffer &tmp, s3dx_stream s, const s3dx_gather_plan *plan = nullptr) {
         char err[512];
         const int32_t dt = bf16 ? S3DX_BF16 : S3DX_F32;
         const uint64_t es = bf16 ? 2 : 4, wide = uint64_t(cin > cout ? cin : cout);
@@ -215,13 +255,13 @@ struct SlatResBlock {
         mod_shift.upload(shift, uint64_t(cout) * 4, s);
         s3dx_check(s3dx_layernorm_rows(x, dt, n, cin, 1e-6f, norm1_w.get<float>(), norm1_b.get<float>(), nullptr,
                                        nullptr, 1, h, dt, s, err, sizeof err), err);
-        conv1.run(h, n, kmap, n, nullptr, y1, dt, s);
+        conv1.run(h, n, kmap, n, nullptr, y1, dt, s, plan);
         const void *res = x;
         if (skip) {
             skip.run(x, n, nullptr, n, nullptr, sk, dt, s);
             res = sk;
         }
-        conv2.run(y1, n, kmap, n, res, y, dt, s);
+        conv2.run(y1, n, kmap, n, res, y, dt, s, plan);
     }
 };
 
