@@ -38,6 +38,15 @@ namespace {
 // s_waitcnt immediate waiting for vmcnt <= n (expcnt, lgkmcnt left at their maxima).
 constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x0F70; }
 
+// f(integral_constant<int, I>) for I = B..E-1, unrolled at compile time.
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+    if constexpr (B < E) {
+        f(std::integral_constant<int, B>{});
+        static_for<B + 1, E>(f);
+    }
+}
+
 constexpr int kHChunk = 64;              // channels per halo chunk
 constexpr int kHRowBytes = kHChunk * 2;  // 128 bytes per halo row
 
@@ -47,6 +56,11 @@ constexpr int kHRowBytes = kHChunk * 2;  // 128 bytes per halo row
 // the eight positions.  ((s >> 1) & 7, which also separates 16 consecutive
 // slots, halves the bank-conflict cycles but measured 1.5% slower.)
 __device__ __forceinline__ int halo_swizzle(int s) { return s & 7; }
+// Byte offset of slot s's row with its swizzle folded in: piece p of the
+// slot sits at halo_offset(s) ^ (p << 4) (the row offset has bits 4-6 clear).
+__device__ __forceinline__ uint32_t halo_offset(uint32_t s) {
+    return s * kHRowBytes | static_cast<uint32_t>(halo_swizzle(static_cast<int>(s))) << 4;
+}
 
 template <int MB>
 struct HaloSmem {
@@ -259,8 +273,11 @@ static_assert(kPlanSlots + HaloSmem<2>::CAP * 4 <= kGatherPlanRecord, "halo reco
 static_assert(kPlanHeader + 64 * kMaxKvol * 4 <= kGatherPlanRecord, "global record fits");
 static_assert(kGatherPlanRecord % 1024 == 0, "records copy as whole 1 KiB pieces");
 
-// 128-row records (the 8-wave kernel): same layout over 128 rows.
-constexpr int kPlan128Slots = kPlanHeader + 128 * kMaxKvol * 2;  // 6928
+// 128-row records (the 8-wave kernel): the same header; halo tiles hold the
+// u32 table [27][128] of halo byte offsets (halo_offset of each slot), then
+// at kPlan128Slots the source row of each slot; global tiles the int32 row
+// table [27][128].
+constexpr int kPlan128Slots = kPlanHeader + 128 * kMaxKvol * 4;  // 13840
 static_assert(kPlan128Slots + HaloSmem<4>::CAP * 4 <= kGatherPlanRecord128, "halo record fits");
 static_assert(kPlanHeader + 128 * kMaxKvol * 4 <= kGatherPlanRecord128, "global record fits");
 static_assert(kGatherPlanRecord128 % 1024 == 0, "records copy as whole 1 KiB pieces");
@@ -268,8 +285,8 @@ static_assert(kGatherPlanRecord128 % 1024 == 0, "records copy as whole 1 KiB pie
 // chunk, the next chunk's copied while the current one is in use) with the
 // zero row at slot kH8Double, or, for tiles naming more distinct rows, one
 // buffer with the zero row at kH8Single.
-constexpr int kH8BufRows = 576;
-constexpr int kH8Double = kH8BufRows - 1;        // 575
+constexpr int kH8BufRows = 568;
+constexpr int kH8Double = kH8BufRows - 1;        // 567
 constexpr int kH8Single = HaloSmem<4>::CAP;      // 1088
 constexpr int kH8HaloBytes = 2 * kH8BufRows * kHRowBytes;
 static_assert((kH8Single + 1) * kHRowBytes <= kH8HaloBytes, "single buffer fits");
@@ -598,9 +615,9 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
     __shared__ __align__(16) char smem[kH8HaloBytes + kGatherPlanRecord128];
     char *halo = smem;
     char *rec = smem + kH8HaloBytes;
-    const uint16_t *table = reinterpret_cast<const uint16_t *>(rec + kPlanHeader);
-    const uint32_t *slot_row = reinterpret_cast<const uint32_t *>(rec + kPlan128Slots);
+    // [27][128] u32: halo byte offsets, or source rows for global gathers
     const int32_t *table32 = reinterpret_cast<const int32_t *>(rec + kPlanHeader);
+    const uint32_t *slot_row = reinterpret_cast<const uint32_t *>(rec + kPlan128Slots);
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -626,7 +643,7 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
         const auto p_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(a.plan), static_cast<short>(0),
                                                               static_cast<int32_t>(plan_bytes), 0x00020000);
 #pragma unroll
-        for (int k = 0; k < 2; ++k) {
+        for (int k = 0; k < (kGatherPlanRecord128 / 1024 + 7) / 8; ++k) {
             const int i = wave + 8 * k;
             if (i < kGatherPlanRecord128 / 1024)
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(p_rsrc, (__attribute__((address_space(3))) void *)(rec + i * 1024),
@@ -650,7 +667,15 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
 
     // Chunk c of every distinct row into its slot of `buf` (lane L of a
     // 1 KiB copy fills piece (L % 8) ^ halo_swizzle(slot) of slot 8g + L / 8).
-    auto halo_copy = [&](int c, char *buf) __attribute__((always_inline)) {
+    // The copies run from within the chunk bodies below, whose pointer
+    // arguments are __restrict__: that tells the compiler that a copy into
+    // one buffer does not alias the reads of the other, so it waits for the
+    // copy only where the code says so (else it drains vmcnt before every
+    // LDS read that follows a copy, and the next chunk's copy stops
+    // overlapping the current chunk's MFMAs).
+    auto halo_copy = [&](int c, char *buf, const uint32_t *slot_row, const char *xg) __attribute__((always_inline)) {
+        const auto x_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(xg), static_cast<short>(0), xbytes,
+                                                              0x00020000);
         const int groups = (static_cast<int>(distinct) + 7) >> 3;
         for (int g0 = wave; g0 < groups; g0 += 32) {
             uint32_t off[4];
@@ -690,14 +715,20 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
         return o == 31 ? olast : o;
     };
     // Fragment (k-step, column block) of the packed weights sits at byte
-    // ((kstep * nbtot + cb) * 64 + lane) * 16.
-    auto load_b = [&](int c, int o, uint4 (&bf)[2]) __attribute__((always_inline)) {
-        const int32_t sbase = ((o * ksteps_total + c * 4 + ks) * nbtot + nb0 + 2 * ch) * 1024;
+    // ((kstep * nbtot + cb) * 64 + lane) * 16: for (chunk c, offset o) this
+    // wave's two fragments start at w_first + c * w_chunk + o * w_offset.
+    const int32_t w_offset = ksteps_total * nbtot * 1024;
+    const int32_t w_chunk = 4 * nbtot * 1024;
+    const int32_t w_first = (ks * nbtot + nb0 + 2 * ch) * 1024;
+    auto load_b_at = [&](int32_t sbase, uint4 (&bf)[2]) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, lane * 16 + j * 1024, sbase, 0);
             bf[j] = make_uint4(v.x, v.y, v.z, v.w);
         }
+    };
+    auto load_b = [&](int c, int o, uint4 (&bf)[2]) __attribute__((always_inline)) {
+        load_b_at(w_first + c * w_chunk + o * w_offset, bf);
     };
     auto mfmas = [&](const uint4 (&af)[4], const uint4 (&bf)[2]) __attribute__((always_inline)) {
 #pragma unroll
@@ -705,91 +736,99 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
 #pragma unroll
             for (int j = 0; j < 2; ++j) acc[mb][j] = mfma_step<uint16_t>(af[mb], bf[j], acc[mb][j]);
     };
-    constexpr int R = 4;  // weight sets in flight (three tasks ahead)
-    uint4 bq[R][2];
-    // The weight cursor runs over (chunk, offset) chunk-major across the
-    // whole loop, so the loads for the next chunk's first tasks go out while
-    // the current chunk ends; past the last task it repeats it (prefetches
-    // beyond the end reload it harmlessly).
-    int cur_c = 0;
-    uint32_t rest_b = mask;
-    auto next_b = [&](uint4 (&bf)[2]) __attribute__((always_inline)) {
-        if (rest_b == 0u) {
-            ++cur_c;
-            rest_b = mask;
-        }
-        const int o = advance(rest_b);
-        load_b(cur_c < chunks ? cur_c : chunks - 1, cur_c < chunks ? o : olast, bf);
+    // This lane's 16-byte piece of the A fragment (channels 8p..8p+7 of the
+    // chunk) from the halo rows whose offsets ix holds.
+    const uint32_t p16 = static_cast<uint32_t>(2 * ks + half) << 4;
+    auto load_a_halo = [&](const char *buf, const int (&ix)[4], uint4 (&af)[4]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+            af[mb] = *reinterpret_cast<const uint4 *>(buf + (static_cast<uint32_t>(ix[mb]) ^ p16));
     };
-    // bq[i] <- bq[(i + n) % R]: after a chunk whose task count leaves n
-    // over a multiple of R, the next chunk's task i sits in bq[(n + i) % R].
-    auto rotate_b = [&](int n) __attribute__((always_inline)) {
-        uint4 t[R][2];
-#pragma unroll
-        for (int k = 0; k < R; ++k) t[k][0] = bq[k][0], t[k][1] = bq[k][1];
-#pragma unroll
-        for (int r = 1; r < R; ++r)
-            if (n == r)
-#pragma unroll
-                for (int k = 0; k < R; ++k) bq[k][0] = t[(k + r) % R][0], bq[k][1] = t[(k + r) % R][1];
+    // Before chunk c's tasks its halo copy has landed and every wave is past
+    // chunk c-1; with two buffers the copy of chunk c+1 then goes into the
+    // buffer chunk c-1 used.  NB weight loads were issued after the copy of
+    // chunk c (the first NB of the loop for c = 0, the last NB of chunk c-1's
+    // tasks otherwise), so vmcnt(NB) covers the copy; few_tasks: chunk c-1
+    // issued fewer than NB loads after the copy.
+    auto chunk_sync = [&](int c, auto nb, bool few_tasks, char *cur, char *nxt, const uint32_t *rows,
+                          const char *xg) __attribute__((always_inline)) {
+        constexpr int NB = decltype(nb)::value;
+        if (dbl) {
+            if (c == 0 || !few_tasks) __builtin_amdgcn_s_waitcnt(vmcnt_imm(NB));
+            else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+            __syncthreads();
+            if (c + 1 < chunks) halo_copy(c + 1, nxt, rows, xg);
+        } else {
+            if (c > 0) {
+                __syncthreads();
+                halo_copy(c, cur, rows, xg);
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+            } else {
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(NB));
+            }
+            __syncthreads();
+        }
     };
 
-    // The chunk loop, for A from the halo (GA false) or from memory (GA
-    // true).  Before chunk c's tasks its halo copy has landed and every wave
-    // is past chunk c-1; with two buffers the copy of chunk c+1 then goes
-    // into the buffer chunk c-1 used.
+    // The chunk loop over any offset mask, for A from the halo (GA false) or
+    // from memory (GA true).
     auto chunk_loop = [&](auto ga) __attribute__((always_inline)) {
         constexpr bool GA = decltype(ga)::value;
         if (ntasks == 0) return;
-        if constexpr (!GA) halo_copy(0, halo);
+        constexpr int R = 4;  // weight sets in flight (three tasks ahead)
+        uint4 bq[R][2];
+        // The weight cursor runs over (chunk, offset) chunk-major across the
+        // whole loop, so the loads for the next chunk's first tasks go out while
+        // the current chunk ends; past the last task it repeats it (prefetches
+        // beyond the end reload it harmlessly).
+        int cur_c = 0;
+        uint32_t rest_b = mask;
+        auto next_b = [&](uint4 (&bf)[2]) __attribute__((always_inline)) {
+            if (rest_b == 0u) {
+                ++cur_c;
+                rest_b = mask;
+            }
+            const int o = advance(rest_b);
+            load_b(cur_c < chunks ? cur_c : chunks - 1, cur_c < chunks ? o : olast, bf);
+        };
+        // bq[i] <- bq[(i + n) % R]: after a chunk whose task count leaves n
+        // over a multiple of R, the next chunk's task i sits in bq[(n + i) % R].
+        auto rotate_b = [&](int n) __attribute__((always_inline)) {
+            uint4 t[R][2];
+    #pragma unroll
+            for (int k = 0; k < R; ++k) t[k][0] = bq[k][0], t[k][1] = bq[k][1];
+    #pragma unroll
+            for (int r = 1; r < R; ++r)
+                if (n == r)
+    #pragma unroll
+                    for (int k = 0; k < R; ++k) bq[k][0] = t[(k + r) % R][0], bq[k][1] = t[(k + r) % R][1];
+        };
+        if constexpr (!GA) halo_copy(0, halo, slot_row, static_cast<const char *>(a.x));
 #pragma unroll
         for (int k = 0; k < R; ++k) {
             next_b(bq[k]);
             sched_fence();
         }
-        for (int c = 0; c < chunks; ++c) {
-            if constexpr (!GA) {
-                if (dbl) {
-                    // The copy of chunk c precedes every weight load of
-                    // chunk c-1's tasks (or, for c = 0, the first R): with
-                    // at least R tasks a chunk, vmcnt(2R) covers it.
-                    if (c == 0 || ntasks >= R) __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * R));
-                    else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-                    __syncthreads();
-                    if (c + 1 < chunks) halo_copy(c + 1, buf_of(c + 1));
-                } else {
-                    if (c > 0) {
-                        __syncthreads();
-                        halo_copy(c, halo);
-                        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-                    } else {
-                        __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * R));
-                    }
-                    __syncthreads();
-                }
-            }
-            const char *buf = buf_of(c);
+        auto chunk = [&](int c, char *__restrict__ buf, char *__restrict__ nxt, const int32_t *__restrict__ tbl,
+                         const uint32_t *__restrict__ rows, const char *__restrict__ xg) __attribute__((always_inline)) {
+            if constexpr (!GA) chunk_sync(c, std::integral_constant<int, 2 * R>{}, ntasks < R, buf, nxt, rows, xg);
             const int kch = (c * 4 + ks) * 16 + half * 8;  // this lane's first channel of the A fragment
             auto load_idx = [&](int o, int (&ix)[4]) __attribute__((always_inline)) {
 #pragma unroll
-                for (int mb = 0; mb < 4; ++mb) {
-                    if constexpr (GA) ix[mb] = table32[o * ROWS + mb * 32 + (lane & 31)];
-                    else ix[mb] = table[o * ROWS + mb * 32 + (lane & 31)];
-                }
+                for (int mb = 0; mb < 4; ++mb) ix[mb] = tbl[o * ROWS + mb * 32 + (lane & 31)];
             };
             auto load_a = [&](const int (&ix)[4], uint4 (&af)[4]) __attribute__((always_inline)) {
+                if constexpr (GA) {
 #pragma unroll
-                for (int mb = 0; mb < 4; ++mb) {
-                    if constexpr (GA) {
+                    for (int mb = 0; mb < 4; ++mb) {
                         const uint32_t off = ix[mb] >= 0 ? (static_cast<uint32_t>(ix[mb]) * static_cast<uint32_t>(a.cin) +
                                                             static_cast<uint32_t>(kch)) * 2u
                                                          : 0x80000000u;
                         const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, static_cast<int32_t>(off), 0, 0);
                         af[mb] = make_uint4(v.x, v.y, v.z, v.w);
-                    } else {
-                        const int p = 2 * ks + half;
-                        af[mb] = *reinterpret_cast<const uint4 *>(buf + ix[mb] * kHRowBytes + ((p ^ halo_swizzle(ix[mb])) << 4));
                     }
+                } else {
+                    load_a_halo(buf, ix, af);
                 }
             };
             uint4 aq[2][4];
@@ -845,9 +884,107 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
                 sched_fence();
             }
             rotate_b(left);
+        };
+        for (int c = 0; c < chunks; ++c)
+            chunk(c, buf_of(c), buf_of(c + 1), table32, slot_row, static_cast<const char *>(a.x));
+    };
+
+    // Two-buffer halo tiles whose rows have neighbours at all 27 offsets
+    // (every tile of a closed surface): the same task order with the offsets
+    // known at compile time, so the table reads take immediate addresses and
+    // no cursor runs.  Three weight sets in flight: 27 tasks a chunk leave
+    // task t of every chunk in set t % 3.
+    //
+    // The copy of chunk c+1 goes out one 1 KiB piece per task over chunk
+    // c's first tasks, each right after a weight load:
+    // vmcnt retires loads in issue order, so a wait for weights requested
+    // after a piece also waits for that piece, and spreading the pieces
+    // gives each about RF tasks of MFMAs to land instead of stalling the
+    // chunk's first task on the whole copy.
+    auto full_loop = [&]() __attribute__((always_inline)) {
+        constexpr int RF = 3;
+        // Pieces a wave copies per chunk with two buffers: group
+        // min(wave + 8j, groups - 1) (slots 8g..8g+7) for j < kPieces, so
+        // every wave issues all of them (a clamped piece copies its group
+        // again: the same bytes to the same place).
+        constexpr int kPieces = (kH8Double + 1 + 63) / 64;  // 9
+        static_assert(kPieces <= kMaxKvol - RF, "the pieces go out before the chunk's last weight loads");
+        const int groups = (static_cast<int>(distinct) + 7) >> 3;
+        uint32_t piece_off[kPieces];  // source byte offset of each piece at chunk 0
+        int piece_group[kPieces];
+#pragma unroll
+        for (int j = 0; j < kPieces; ++j) {
+            piece_group[j] = min(wave + 8 * j, groups - 1);
+            const int sl = piece_group[j] * 8 + (lane >> 3);
+            const int p = (lane & 7) ^ halo_swizzle(sl);
+            piece_off[j] = sl < static_cast<int>(distinct)
+                               ? (slot_row[min(sl, kH8Double)] * static_cast<uint32_t>(a.cin) + p * 8) * 2u
+                               : 0x80000000u;  // past the buffer: zeros
+        }
+        // piece j of chunk cc into buffer dst (soffset is outside the range
+        // check: the zero-fill offset stays out of range)
+        auto piece = [&](__amdgpu_buffer_rsrc_t rsrc, int j, int cc, uint32_t off, char *dst) __attribute__((always_inline)) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc,
+                                                     (__attribute__((address_space(3))) void *)(dst + piece_group[j] * 1024),
+                                                     16, static_cast<int32_t>(off), cc * kHRowBytes, 0, 0);
+        };
+        uint4 bf[RF][2];
+        int32_t wb = w_first;  // weights of the next task to request
+        {
+            const auto x_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(a.x), static_cast<short>(0),
+                                                                  xbytes, 0x00020000);
+#pragma unroll
+            for (int j = 0; j < kPieces; ++j) piece(x_rsrc, j, 0, piece_off[j], halo);
+        }
+#pragma unroll
+        for (int k = 0; k < RF; ++k) {
+            load_b_at(wb, bf[k]);
+            wb += w_offset;
+            sched_fence();
+        }
+        // Chunk c's 27 tasks from `buf`, chunk c+1's copy into `nxt` going
+        // out over the first tasks (zero fills, which read nothing, after
+        // the last chunk).
+        auto chunk = [&](int c, const char *__restrict__ buf, char *__restrict__ nxt, const int32_t *__restrict__ tbl,
+                         const char *__restrict__ xg) __attribute__((always_inline)) {
+            const auto x_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(xg), static_cast<short>(0),
+                                                                  xbytes, 0x00020000);
+            const bool last = c + 1 == chunks;
+            auto load_idx = [&](int o, int (&ix)[4]) __attribute__((always_inline)) {
+#pragma unroll
+                for (int mb = 0; mb < 4; ++mb) ix[mb] = tbl[o * ROWS + mb * 32 + (lane & 31)];
+            };
+            // the next chunk's first weights (the last chunk reloads its own)
+            const int32_t w_next = w_first + (last ? c : c + 1) * w_chunk;
+            uint4 aq[2][4];
+            int iq[2][4];
+            load_idx(0, iq[0]);
+            load_idx(1, iq[1]);
+            load_a_halo(buf, iq[0], aq[0]);
+            sched_fence();
+            static_for<0, kMaxKvol>([&](auto tc) __attribute__((always_inline)) {
+                constexpr int t = decltype(tc)::value, A0 = t & 1, A1 = (t + 1) & 1;
+                if constexpr (t + 1 < kMaxKvol) load_a_halo(buf, iq[A1], aq[A1]);
+                if constexpr (t + 2 < kMaxKvol) load_idx(t + 2, iq[A0]);
+                mfmas(aq[A0], bf[t % RF]);
+                sched_fence();
+                if constexpr (t + RF == kMaxKvol) wb = w_next;
+                load_b_at(wb, bf[t % RF]);
+                wb += w_offset;
+                if constexpr (t < kPieces) piece(x_rsrc, t, c + 1, last ? 0x80000000u : piece_off[t], nxt);
+                sched_fence();
+            });
+        };
+        for (int c = 0; c < chunks; ++c) {
+            // chunk c's pieces precede the last 2 RF weight loads, and after
+            // the barrier no wave reads the buffer of chunk c-1
+            __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * RF));
+            __syncthreads();
+            chunk(c, buf_of(c), buf_of(c + 1), table32, static_cast<const char *>(a.x));
         }
     };
     if (global_a) chunk_loop(std::true_type{});
+    else if (dbl && mask == (1u << kMaxKvol) - 1u) full_loop();
     else chunk_loop(std::false_type{});
     __syncthreads();  // the halo region becomes the reduction slots
 
@@ -917,9 +1054,10 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
 }
 
 // One workgroup per tile (64 or 128 rows): dedupe_tile, then the record to
-// memory.  128-row records name missing neighbours by the zero row of the
-// kernel's halo layout: slot kH8Single when the tile's distinct rows need
-// the single large buffer, else kH8Double (two buffers, one per chunk).
+// memory.  128-row records hold halo byte offsets and name missing
+// neighbours by the zero row of the kernel's halo layout: slot kH8Single when
+// the tile's distinct rows need the single large buffer, else kH8Double (two
+// buffers, one per chunk).
 template <int MB>
 __global__ void __launch_bounds__(256) gather_plan_build_kernel(const int32_t *kmap, int64_t n_out, int64_t n_src,
                                                                 int32_t row_shift, char *plan) {
@@ -947,11 +1085,10 @@ __global__ void __launch_bounds__(256) gather_plan_build_kernel(const int32_t *k
     } else {
         if constexpr (MB == 4) {
             const uint32_t z = dd.distinct <= static_cast<uint32_t>(kH8Double) ? kH8Double : kH8Single;
-            for (int i = tid; i < ROWS * kMaxKvol / 2; i += 256) {
-                uint32_t v = reinterpret_cast<const uint32_t *>(table)[i];
-                if ((v & 0xFFFFu) == static_cast<uint32_t>(SM::CAP)) v = (v & 0xFFFF0000u) | z;
-                if ((v >> 16) == static_cast<uint32_t>(SM::CAP)) v = (v & 0xFFFFu) | (z << 16);
-                reinterpret_cast<uint32_t *>(rec + kPlanHeader)[i] = v;
+            for (int i = tid; i < ROWS * kMaxKvol; i += 256) {
+                const uint32_t sl = table[i];
+                reinterpret_cast<uint32_t *>(rec + kPlanHeader)[i] =
+                    halo_offset(sl == static_cast<uint32_t>(SM::CAP) ? z : sl);
             }
         } else {
             for (int i = tid; i < ROWS * kMaxKvol * 2 / 16; i += 256)

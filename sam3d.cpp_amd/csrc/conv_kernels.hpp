@@ -81,7 +81,7 @@ constexpr int kHalo8Threads = 512;
 void launch_gather_plan_build(int rows, const int32_t *kmap, int64_t n_out, int64_t n_src, int32_t row_shift,
                               void *plan, hipStream_t stream);
 constexpr int kGatherPlanRecord = 7168;      // 64-row tiles
-constexpr int kGatherPlanRecord128 = 14336;  // 128-row tiles
+constexpr int kGatherPlanRecord128 = 18432;  // 128-row tiles
 // The FP32 1x1-layer kernel reading BF16 rows, else nullptr.
 KernelFn pick_linear_f32_bf16_rows(int nbt);
 // The same on BF16 MFMAs with three-term split weights (Cin = 16 * ksx,
