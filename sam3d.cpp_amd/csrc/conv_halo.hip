@@ -986,6 +986,9 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
     if (global_a) chunk_loop(std::true_type{});
     else if (dbl && mask == (1u << kMaxKvol) - 1u) full_loop();
     else chunk_loop(std::false_type{});
+    // the epilogue's column parameters, in flight during the reduction
+    RowParams params;
+    load_row_params(a, nb0 * 32 + (tid % 16) * 8, params);
     __syncthreads();  // the halo region becomes the reduction slots
 
     // ---- 3. reduce the four k-step partials of each 32 x 32 block: wave
@@ -1050,7 +1053,7 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
     uint4 res[RowMap<16, ROWS, kHalo8Threads>::PASSES][2];
     load_residual<16, ROWS, kHalo8Threads>(a, m0, nb0, tile_rows, tid, res);
     __syncthreads();
-    finish_rows<16, ROWS, STG_LD, kHalo8Threads>(a, stg, stg + ROWS * STG_LD, m0, nb0, tile_rows, tid, res);
+    finish_rows<16, ROWS, STG_LD, kHalo8Threads>(a, stg, stg + ROWS * STG_LD, m0, nb0, tile_rows, tid, res, params);
 }
 
 // One workgroup per tile (64 or 128 rows): dedupe_tile, then the record to

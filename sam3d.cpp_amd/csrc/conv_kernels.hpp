@@ -257,10 +257,29 @@ __device__ __forceinline__ void load_residual(const ConvArgs &a, int64_t m0, int
 // (prefetched by load_residual), 16-byte stores.  Row statistics are summed
 // across the row's TPR lanes with shuffles when TPR is a power of two, else
 // through `part` (2*BM*TPR floats of LDS).
+// The per-column parameters of a thread's 8 columns from col0: bias,
+// LayerNorm affine, modulation.  Padded columns (col >= cout, zero weights)
+// read none.  Kernels with latency to hide load them early.
+struct RowParams {
+    float bias[8], lw[8], lb[8], ms[8], mh[8];
+};
+__device__ __forceinline__ void load_row_params(const ConvArgs &a, int col0, RowParams &q) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const bool real = col0 + k < a.cout;
+        q.bias[k] = a.bias && real ? a.bias[col0 + k] : 0.0f;
+        q.lw[k] = a.ln_w && real ? a.ln_w[col0 + k] : 1.0f;
+        q.lb[k] = a.ln_b && real ? a.ln_b[col0 + k] : 0.0f;
+        q.ms[k] = a.mod_scale && real ? a.mod_scale[col0 + k] : 0.0f;
+        q.mh[k] = a.mod_shift && real ? a.mod_shift[col0 + k] : 0.0f;
+    }
+}
+
 template <int TPR, int BM, int STG_LD, int NTH = 256>
 __device__ __forceinline__ void finish_rows(const ConvArgs &a, const float *stg, float *part, int64_t m0,
                                             int nb0, int tile_rows, int tid,
-                                            const uint4 (&res)[RowMap<TPR, BM, NTH>::PASSES][2]) {
+                                            const uint4 (&res)[RowMap<TPR, BM, NTH>::PASSES][2],
+                                            const RowParams &q) {
     using RM = RowMap<TPR, BM, NTH>;
     constexpr int RPP = RM::RPP;
     constexpr int PASSES = RM::PASSES;
@@ -268,13 +287,10 @@ __device__ __forceinline__ void finish_rows(const ConvArgs &a, const float *stg,
     const bool active = rsub < RPP;
     const int col0 = nb0 * 32 + cg * 8;  // global column of this thread's 8 values
     const float inv_c = 1.0f / static_cast<float>(a.cout);
-    // Padded columns (col >= cout, zero weights) read no parameters and are
-    // not stored.  Rows of a cout that is not a multiple of 8 are not
-    // 16-byte aligned: element stores.
+    // Padded columns are not stored.  Rows of a cout that is not a multiple
+    // of 8 are not 16-byte aligned: element stores.
     const bool ragged = a.cout % 8 != 0;
-    float bias8[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) bias8[k] = a.bias && col0 + k < a.cout ? a.bias[col0 + k] : 0.0f;
+    const float(&bias8)[8] = q.bias;
 
     auto tile_vals = [&](int rl, float (&v)[8]) __attribute__((always_inline)) {
         const float4 *p = reinterpret_cast<const float4 *>(stg + rl * STG_LD + cg * 8);
@@ -328,15 +344,10 @@ __device__ __forceinline__ void finish_rows(const ConvArgs &a, const float *stg,
         }
     }
 
-    float lw[8], lb[8], ms[8], mh[8];
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const bool real = col0 + k < a.cout;
-        lw[k] = a.ln_w && real ? a.ln_w[col0 + k] : 1.0f;
-        lb[k] = a.ln_b && real ? a.ln_b[col0 + k] : 0.0f;
-        ms[k] = a.mod_scale && real ? a.mod_scale[col0 + k] : 0.0f;
-        mh[k] = a.mod_shift && real ? a.mod_shift[col0 + k] : 0.0f;
-    }
+    const float(&lw)[8] = q.lw;
+    const float(&lb)[8] = q.lb;
+    const float(&ms)[8] = q.ms;
+    const float(&mh)[8] = q.mh;
     // Power-of-two groups: LayerNorm statistics of every pass first, all
     // passes in lockstep so the cross-lane sums overlap (two-pass mean /
     // variance; every lane of a group takes part, whatever its row).
@@ -461,6 +472,15 @@ __device__ __forceinline__ void finish_rows(const ConvArgs &a, const float *stg,
                 reinterpret_cast<u32x4 *>(yp) + 1);
         }
     }
+}
+
+template <int TPR, int BM, int STG_LD, int NTH = 256>
+__device__ __forceinline__ void finish_rows(const ConvArgs &a, const float *stg, float *part, int64_t m0,
+                                            int nb0, int tile_rows, int tid,
+                                            const uint4 (&res)[RowMap<TPR, BM, NTH>::PASSES][2]) {
+    RowParams q;
+    load_row_params(a, nb0 * 32 + (tid % TPR) * 8, q);
+    finish_rows<TPR, BM, STG_LD, NTH>(a, stg, part, m0, nb0, tile_rows, tid, res, q);
 }
 
 // LDS budget of a tiling: two weight buffers, or (after the main loop) the
