@@ -285,10 +285,18 @@ static_assert(kGatherPlanRecord128 % 1024 == 0, "records copy as whole 1 KiB pie
 // chunk, the next chunk's copied while the current one is in use) with the
 // zero row at slot kH8Double, or, for tiles naming more distinct rows, one
 // buffer with the zero row at kH8Single.
-constexpr int kH8BufRows = 568;
-constexpr int kH8Double = kH8BufRows - 1;        // 567
+constexpr int kH8BufRows = 560;
+constexpr int kH8Double = kH8BufRows - 1;        // 559
 constexpr int kH8Single = HaloSmem<4>::CAP;      // 1088
 constexpr int kH8HaloBytes = 2 * kH8BufRows * kHRowBytes;
+// 1 KiB after the halo that nothing reads: the last chunk sends its unneeded
+// copy pieces (zero fills, which read no memory) there.
+constexpr int kH8Dump = kH8HaloBytes;
+constexpr int kH8Bytes = 160 * 1024;  // the kernel's LDS: halo, dump, plan record, padding
+static_assert(kH8Dump + 1024 + kGatherPlanRecord128 <= kH8Bytes, "halo, dump and record fit");
+// The record header's last word, 0 as the plan builder writes it: in LDS,
+// the 8-wave kernel's arrival counter for the four waves of column half 0.
+constexpr int kHalfCounter = 12;
 static_assert((kH8Single + 1) * kHRowBytes <= kH8HaloBytes, "single buffer fits");
 static_assert(kH8BufRows % 8 == 0, "buffers keep the slot swizzle");
 
@@ -611,10 +619,10 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_halo_kernel(ConvArg
 // two kernels' results are bit-identical.
 __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a) {
     constexpr int ROWS = 128;
-    constexpr int STG_LD = 128 + 8;
-    __shared__ __align__(16) char smem[kH8HaloBytes + kGatherPlanRecord128];
+    constexpr int STG_LD = 128;
+    __shared__ __align__(16) char smem[kH8Bytes];
     char *halo = smem;
-    char *rec = smem + kH8HaloBytes;
+    char *rec = smem + kH8Dump + 1024;
     // [27][128] u32: halo byte offsets, or source rows for global gathers
     const int32_t *table32 = reinterpret_cast<const int32_t *>(rec + kPlanHeader);
     const uint32_t *slot_row = reinterpret_cast<const uint32_t *>(rec + kPlan128Slots);
@@ -720,10 +728,12 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
     const int32_t w_offset = ksteps_total * nbtot * 1024;
     const int32_t w_chunk = 4 * nbtot * 1024;
     const int32_t w_first = (ks * nbtot + nb0 + 2 * ch) * 1024;
-    auto load_b_at = [&](int32_t sbase, uint4 (&bf)[2]) __attribute__((always_inline)) {
+    // (voff_extra 0x80000000 puts the loads out of range: zeros, no memory read)
+    auto load_b_at = [&](int32_t sbase, uint4 (&bf)[2], uint32_t voff_extra = 0u) __attribute__((always_inline)) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
-            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, lane * 16 + j * 1024, sbase, 0);
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(
+                w_rsrc, static_cast<int32_t>((static_cast<uint32_t>(lane * 16) | voff_extra) + j * 1024), sbase, 0);
             bf[j] = make_uint4(v.x, v.y, v.z, v.w);
         }
     };
@@ -779,8 +789,7 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
         uint4 bq[R][2];
         // The weight cursor runs over (chunk, offset) chunk-major across the
         // whole loop, so the loads for the next chunk's first tasks go out while
-        // the current chunk ends; past the last task it repeats it (prefetches
-        // beyond the end reload it harmlessly).
+        // the current chunk ends; past the last task it requests nothing.
         int cur_c = 0;
         uint32_t rest_b = mask;
         auto next_b = [&](uint4 (&bf)[2]) __attribute__((always_inline)) {
@@ -789,7 +798,7 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
                 rest_b = mask;
             }
             const int o = advance(rest_b);
-            load_b(cur_c < chunks ? cur_c : chunks - 1, cur_c < chunks ? o : olast, bf);
+            if (cur_c < chunks) load_b(cur_c, o, bf);
         };
         // bq[i] <- bq[(i + n) % R]: after a chunk whose task count leaves n
         // over a multiple of R, the next chunk's task i sits in bq[(n + i) % R].
@@ -923,10 +932,10 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
         }
         // piece j of chunk cc into buffer dst (soffset is outside the range
         // check: the zero-fill offset stays out of range)
-        auto piece = [&](__amdgpu_buffer_rsrc_t rsrc, int j, int cc, uint32_t off, char *dst) __attribute__((always_inline)) {
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc,
-                                                     (__attribute__((address_space(3))) void *)(dst + piece_group[j] * 1024),
-                                                     16, static_cast<int32_t>(off), cc * kHRowBytes, 0, 0);
+        auto piece = [&](__amdgpu_buffer_rsrc_t rsrc, int j, int cc, uint32_t off, char *dst)
+                         __attribute__((always_inline)) {
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void *)(dst), 16,
+                                                     static_cast<int32_t>(off), cc * kHRowBytes, 0, 0);
         };
         uint4 bf[RF][2];
         int32_t wb = w_first;  // weights of the next task to request
@@ -934,7 +943,7 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
             const auto x_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(a.x), static_cast<short>(0),
                                                                   xbytes, 0x00020000);
 #pragma unroll
-            for (int j = 0; j < kPieces; ++j) piece(x_rsrc, j, 0, piece_off[j], halo);
+            for (int j = 0; j < kPieces; ++j) piece(x_rsrc, j, 0, piece_off[j], halo + piece_group[j] * 1024);
         }
 #pragma unroll
         for (int k = 0; k < RF; ++k) {
@@ -942,20 +951,24 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
             wb += w_offset;
             sched_fence();
         }
-        // Chunk c's 27 tasks from `buf`, chunk c+1's copy into `nxt` going
-        // out over the first tasks (zero fills, which read nothing, after
-        // the last chunk).
+        // Chunk c's 27 tasks from `buf`; but for the last chunk, chunk
+        // c+1's copy goes into `nxt` over the first tasks and the first
+        // weights of chunk c+1 are requested over the last ones.  The last
+        // chunk leaves the other buffer untouched (the epilogue uses it).
         auto chunk = [&](int c, const char *__restrict__ buf, char *__restrict__ nxt, const int32_t *__restrict__ tbl,
                          const char *__restrict__ xg) __attribute__((always_inline)) {
+            const bool last = c + 1 == chunks;
             const auto x_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(xg), static_cast<short>(0),
                                                                   xbytes, 0x00020000);
-            const bool last = c + 1 == chunks;
             auto load_idx = [&](int o, int (&ix)[4]) __attribute__((always_inline)) {
 #pragma unroll
                 for (int mb = 0; mb < 4; ++mb) ix[mb] = tbl[o * ROWS + mb * 32 + (lane & 31)];
             };
-            // the next chunk's first weights (the last chunk reloads its own)
-            const int32_t w_next = w_first + (last ? c : c + 1) * w_chunk;
+            const int32_t w_next = w_first + (c + 1) * w_chunk;
+            // The last chunk requests nothing for a next one: its pieces go
+            // to the dump, its last weight loads out of range (zeros, no
+            // memory read), so no wave waits on them after the loop.
+            const uint32_t b_void = last ? 0x80000000u : 0u;
             uint4 aq[2][4];
             int iq[2][4];
             load_idx(0, iq[0]);
@@ -969,9 +982,11 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
                 mfmas(aq[A0], bf[t % RF]);
                 sched_fence();
                 if constexpr (t + RF == kMaxKvol) wb = w_next;
-                load_b_at(wb, bf[t % RF]);
+                load_b_at(wb, bf[t % RF], t + RF < kMaxKvol ? 0u : b_void);
                 wb += w_offset;
-                if constexpr (t < kPieces) piece(x_rsrc, t, c + 1, last ? 0x80000000u : piece_off[t], nxt);
+                if constexpr (t < kPieces)
+                    piece(x_rsrc, t, c + 1, last ? 0x80000000u : piece_off[t],
+                          last ? smem + kH8Dump : nxt + piece_group[t] * 1024);
                 sched_fence();
             });
         };
@@ -989,43 +1004,52 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
     // the epilogue's column parameters, in flight during the reduction
     RowParams params;
     load_row_params(a, nb0 * 32 + (tid % 16) * 8, params);
-    __syncthreads();  // the halo region becomes the reduction slots
 
     // ---- 3. reduce the four k-step partials of each 32 x 32 block: wave
-    // (ks, ch) sums row block ks of column blocks 2ch, 2ch+1, one column
-    // block per phase, the others handing theirs over as float4 [4][lane].
-    float4 *red = reinterpret_cast<float4 *>(smem);
-    auto slot_of = [&](int rb, int writer) __attribute__((always_inline)) {
-        return red + ((rb * 2 + ch) * 4 + writer) * (4 * 64);
-    };
+    // (ks, ch) sums row block ks of column blocks 2ch, 2ch+1, the three
+    // other waves of its column half handing theirs over through LDS as
+    // float4 [4][lane] blocks.  The halves are independent: column half 0
+    // (whose waves the SIMDs favour, so they leave the loop first) reduces
+    // in the halo buffer the last chunk does not use while half 1 still
+    // runs its MFMAs, synchronizing its four waves through an LDS counter;
+    // half 1 then reduces both column blocks at once after the barrier.
+    // With one large halo buffer (nothing free during the loop) both halves
+    // take the second path in turn.
     float fin[2][16];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        if (j) __syncthreads();
+    // Writer w's block of row block rb: rank (w - rb - 1) & 3 among the
+    // three writers, 4 KiB each, [rb][rank] per column block.
+    auto block_of = [&](float4 *base, int rb, int w) __attribute__((always_inline)) {
+        return base + (rb * 3 + ((w - rb - 1) & 3)) * (4 * 64);
+    };
+    auto write_partials = [&](float4 *base, int j) __attribute__((always_inline)) {
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb) {
             if (rb == ks) continue;
-            float4 *sl = slot_of(rb, ks);
+            float4 *sl = block_of(base, rb, ks);
 #pragma unroll
             for (int g = 0; g < 4; ++g)
                 sl[g * 64 + lane] = make_float4(acc[rb][j][4 * g], acc[rb][j][4 * g + 1], acc[rb][j][4 * g + 2],
                                                 acc[rb][j][4 * g + 3]);
         }
-        __syncthreads();
-        const int cbl = 2 * ch + j;  // column block within the tile
-        // own partial: row block ks (a wave-uniform pick among the four)
-        f32x16 own = acc[0][j];
-#pragma unroll
-        for (int rb = 1; rb < 4; ++rb)
-            if (rb == ks) own = acc[rb][j];
+    };
+    // fin[j]: ((P_c + P_c+1) + P_c+2) + P_c+3 for column block c = 2ch + j
+    // (indices mod 4), the order of the 64-row kernel's reduction.  The
+    // code is instantiated per k-step KS (= ks, dispatched by with_ks) so
+    // that the own partial acc[KS][j] is a constant index: a runtime pick
+    // among the four gets folded into a load from a computed address, which
+    // puts all of acc in scratch memory.
+    auto reduce_block = [&](auto kc, const float4 *base, int j) __attribute__((always_inline)) {
+        constexpr int KS = decltype(kc)::value;
+        const int cbl = 2 * ch + j;
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             float4 term[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int w = (cbl + i) & 3;
-                term[i] = w == ks ? make_float4(own[4 * g], own[4 * g + 1], own[4 * g + 2], own[4 * g + 3])
-                                  : slot_of(ks, w)[g * 64 + lane];
+                term[i] = w == KS ? make_float4(acc[KS][j][4 * g], acc[KS][j][4 * g + 1], acc[KS][j][4 * g + 2],
+                                                acc[KS][j][4 * g + 3])
+                                  : block_of(const_cast<float4 *>(base), KS, w)[g * 64 + lane];
             }
             float4 sum = term[0];
 #pragma unroll
@@ -1040,20 +1064,84 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
             fin[j][4 * g + 2] = sum.z;
             fin[j][4 * g + 3] = sum.w;
         }
-    }
-    __syncthreads();
-    float *stg = reinterpret_cast<float *>(smem);
+    };
+    auto with_ks = [&](auto f) __attribute__((always_inline)) {
+        switch (ks) {
+        case 0: f(std::integral_constant<int, 0>{}); break;
+        case 1: f(std::integral_constant<int, 1>{}); break;
+        case 2: f(std::integral_constant<int, 2>{}); break;
+        default: f(std::integral_constant<int, 3>{}); break;
+        }
+    };
+    // The staged output tile, unpadded at the top of LDS (the slots of a
+    // whole-half reduction take the 96 KiB below it): 16-byte group q of row
+    // r sits at q ^ 8 when r & 4, so rows r and r + 4 (written by one
+    // instruction) fall on opposite halves of the banks.
+    constexpr int kSlotBytes = 2 * 4 * 3 * 4096;
+    static_assert(kSlotBytes + ROWS * STG_LD * 4 <= kH8Bytes, "slots and tile fit");
+    float *stg = reinterpret_cast<float *>(smem + kSlotBytes);
+    auto write_stg = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int col = (2 * ch + j) * 32 + (lane & 31);
-        const int rb = ks * 32 + 4 * half;
+        for (int j = 0; j < 2; ++j) {
+            const int col = (2 * ch + j) * 32 + (lane & 31);
+            const int rb = ks * 32 + 4 * half;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) stg[(rb + 8 * (r >> 2) + (r & 3)) * STG_LD + col] = fin[j][r];
+            for (int r = 0; r < 16; ++r) {
+                const int row = rb + 8 * (r >> 2) + (r & 3);
+                stg[row * STG_LD + (col ^ (((row >> 2) & 1) << 5))] = fin[j][r];
+            }
+        }
+    };
+    float4 *slots = reinterpret_cast<float4 *>(smem);
+    if (dbl || global_a) {  // a halo buffer is free during the last chunk
+        if (ch == 0) {
+            float4 *region = reinterpret_cast<float4 *>(global_a ? halo : buf_of(chunks));
+            uint32_t *ctr = reinterpret_cast<uint32_t *>(rec + kHalfCounter);
+            // all four waves of the half have arrived `round` times
+            auto half_sync = [&](uint32_t round) __attribute__((always_inline)) {
+                if (lane == 0) __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+                while (__hip_atomic_load(ctr, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < 4u * round)
+                    __builtin_amdgcn_s_sleep(1);
+            };
+            write_partials(region, 0);
+            half_sync(1);
+            with_ks([&](auto kc) __attribute__((always_inline)) { reduce_block(kc, region, 0); });
+            half_sync(2);  // every wave has read column block 0's partials
+            write_partials(region, 1);
+            half_sync(3);
+            with_ks([&](auto kc) __attribute__((always_inline)) { reduce_block(kc, region, 1); });
+        }
+        __syncthreads();  // the loop and half 0's reduction are over: LDS is free
+        if (ch == 0) {
+            write_stg();
+        } else {
+            write_partials(slots, 0);
+            write_partials(slots + 12 * 256, 1);
+        }
+        __syncthreads();
+        if (ch == 1) {
+            with_ks([&](auto kc) __attribute__((always_inline)) {
+                reduce_block(kc, slots, 0);
+                reduce_block(kc, slots + 12 * 256, 1);
+            });
+            write_stg();
+        }
+    } else {  // both halves at once, one column block per phase
+        __syncthreads();  // the halo region becomes the reduction slots
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            if (j) __syncthreads();  // phase 0's slots have been read
+            write_partials(slots + ch * 12 * 256, j);
+            __syncthreads();
+            with_ks([&](auto kc) __attribute__((always_inline)) { reduce_block(kc, slots + ch * 12 * 256, j); });
+        }
+        write_stg();
     }
+    load_row_mod(a, nb0 * 32 + (tid % 16) * 8, params);
     uint4 res[RowMap<16, ROWS, kHalo8Threads>::PASSES][2];
     load_residual<16, ROWS, kHalo8Threads>(a, m0, nb0, tile_rows, tid, res);
     __syncthreads();
-    finish_rows<16, ROWS, STG_LD, kHalo8Threads>(a, stg, stg + ROWS * STG_LD, m0, nb0, tile_rows, tid, res, params);
+    finish_rows<16, ROWS, STG_LD, kHalo8Threads, true>(a, stg, stg, m0, nb0, tile_rows, tid, res, params);
 }
 
 // One workgroup per tile (64 or 128 rows): dedupe_tile, then the record to

@@ -263,6 +263,7 @@ __device__ __forceinline__ void load_residual(const ConvArgs &a, int64_t m0, int
 struct RowParams {
     float bias[8], lw[8], lb[8], ms[8], mh[8];
 };
+// Bias and LayerNorm affine; the modulation separately (load_row_mod).
 __device__ __forceinline__ void load_row_params(const ConvArgs &a, int col0, RowParams &q) {
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
@@ -270,12 +271,19 @@ __device__ __forceinline__ void load_row_params(const ConvArgs &a, int col0, Row
         q.bias[k] = a.bias && real ? a.bias[col0 + k] : 0.0f;
         q.lw[k] = a.ln_w && real ? a.ln_w[col0 + k] : 1.0f;
         q.lb[k] = a.ln_b && real ? a.ln_b[col0 + k] : 0.0f;
+    }
+}
+__device__ __forceinline__ void load_row_mod(const ConvArgs &a, int col0, RowParams &q) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const bool real = col0 + k < a.cout;
         q.ms[k] = a.mod_scale && real ? a.mod_scale[col0 + k] : 0.0f;
         q.mh[k] = a.mod_shift && real ? a.mod_shift[col0 + k] : 0.0f;
     }
 }
 
-template <int TPR, int BM, int STG_LD, int NTH = 256>
+// SWZ: the tile's 16-byte group q of row r sits at q ^ 8 when r & 4.
+template <int TPR, int BM, int STG_LD, int NTH = 256, bool SWZ = false>
 __device__ __forceinline__ void finish_rows(const ConvArgs &a, const float *stg, float *part, int64_t m0,
                                             int nb0, int tile_rows, int tid,
                                             const uint4 (&res)[RowMap<TPR, BM, NTH>::PASSES][2],
@@ -293,7 +301,8 @@ __device__ __forceinline__ void finish_rows(const ConvArgs &a, const float *stg,
     const float(&bias8)[8] = q.bias;
 
     auto tile_vals = [&](int rl, float (&v)[8]) __attribute__((always_inline)) {
-        const float4 *p = reinterpret_cast<const float4 *>(stg + rl * STG_LD + cg * 8);
+        const int c8 = SWZ ? (cg * 8) ^ (((rl >> 2) & 1) << 5) : cg * 8;
+        const float4 *p = reinterpret_cast<const float4 *>(stg + rl * STG_LD + c8);
         const float4 x0 = p[0], x1 = p[1];
         v[0] = x0.x + bias8[0]; v[1] = x0.y + bias8[1]; v[2] = x0.z + bias8[2]; v[3] = x0.w + bias8[3];
         v[4] = x1.x + bias8[4]; v[5] = x1.y + bias8[5]; v[6] = x1.z + bias8[6]; v[7] = x1.w + bias8[7];
@@ -480,6 +489,7 @@ __device__ __forceinline__ void finish_rows(const ConvArgs &a, const float *stg,
                                             const uint4 (&res)[RowMap<TPR, BM, NTH>::PASSES][2]) {
     RowParams q;
     load_row_params(a, nb0 * 32 + (tid % TPR) * 8, q);
+    load_row_mod(a, nb0 * 32 + (tid % TPR) * 8, q);
     finish_rows<TPR, BM, STG_LD, NTH>(a, stg, part, m0, nb0, tile_rows, tid, res, q);
 }
 
