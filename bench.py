@@ -319,13 +319,25 @@ def mesh_stack(s3dx, W, stream, seed, d0, p0, ch0, k0):
     stages["level1_block_us"] = _event_us(s3dx, stream, run1, reps=5)
     stages["head_us"] = _event_us(s3dx, stream, run_head, reps=5)
     total = stages["level0_block_us"] + stages["level1_block_us"] + stages["head_us"]
+    # The two subdivides (children coordinates + their kernel maps) that feed the
+    # blocks, timed on reused buffers, wall clock with their one host synchronization each.
+    subs = {}
+    for lv, (cin_d, cn) in enumerate(((d0, p0), (ch0, n0))):
+        so = (s3dx.DeviceArray((8 * cn, 4), np.int32), s3dx.DeviceArray((8 * cn, 27), np.int32))
+        sw = s3dx.DeviceArray(s3dx.subdivide2_workspace_size(cn), np.uint8)
+        subs[f"subdivide{lv}_us_wall"] = _wall_us(
+            lambda: s3dx.subdivide2(cin_d, cn, True, stream, out=so, workspace=sw))
+    total_all = total + subs["subdivide0_us_wall"] + subs["subdivide1_us_wall"]
     fl = flops[0] + flops[1] + 2.0 * n1 * 96 * 101
-    return {**stages, "total_us": total, "parents": p0, "level0_children": n0, "level1_children": n1,
-            "tflops": fl / total / 1e6, "dtype": "bf16 blocks, fp32 head",
+    return {**stages, **subs, "total_us": total, "total_with_subdivides_us": total_all,
+            "parents": p0, "level0_children": n0, "level1_children": n1,
+            "tflops": fl / total / 1e6, "tflops_with_subdivides": fl / total_all / 1e6,
+            "dtype": "bf16 blocks, fp32 head",
             "note": "per block: GN32 stats, conv (GN affine+SiLU pass over the parents, gather of "
                     "parent row j>>3), 1x1 skip over the parents, GN32 stats, conv (GN affine+SiLU "
-                    "pass) + skip row i>>3 as residual; flops count the skip once per parent; the "
-                    "level-1 subdivide is outside the timed stages"}
+                    "pass) + skip row i>>3 as residual; flops count the skip once per parent; "
+                    "total_us is the three layer stages, total_with_subdivides_us adds the two "
+                    "subdivides (children + child kernel maps) that build their tables"}
 
 
 def copy_calibration(s3dx):
