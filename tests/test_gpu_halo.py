@@ -76,6 +76,10 @@ CASES = {
     "shuffled_cube_13824": (lambda W: _dense_cube(24, 0), 128, 128, True),          # every tile global
     "half_shuffled_cube_13824": (lambda W: _dense_cube(24, 6912), 128, 128, False),  # both modes
     "tiny_37": (lambda W: W.shells_union(2)[:37], 128, 128, True),                   # one partial tile
+    # one chunk (the first chunk is the last), an odd chunk count, two column groups
+    "shells_union_28265_cin64": (lambda W: W.shells_union(0), 64, 128, True),
+    "shells_union_3000_cin192": (lambda W: W.shells_union(1)[:3000], 192, 128, True),
+    "shells_union_3000_cout256": (lambda W: W.shells_union(1)[:3000], 128, 256, False),
 }
 
 
