@@ -318,7 +318,7 @@ S3DX_API s3dx_status s3dx_conv_run(const s3dx_conv *conv, const void *x, int64_t
  * in use.  create enqueues the build on `stream` and picks the records' tile
  * height from `conv`: 128 output rows when its halo kernel's 128-row tiles
  * fill the GPU's compute units in one pass (runs then use an 8-wave kernel
- * on those tiles; 14 KiB of device memory per 128 rows), else 64 rows (7
+ * on those tiles; 18 KiB of device memory per 128 rows), else 64 rows (7
  * KiB per 64 rows); free releases it. */
 typedef struct s3dx_gather_plan s3dx_gather_plan;
 S3DX_API s3dx_status s3dx_gather_plan_create(const s3dx_conv *conv, int64_t n_in, const int32_t *kmap,
