@@ -27,24 +27,20 @@ namespace {
 //    (b, x, y, z) packed as four int16 when the coordinate fits (a set with
 //    any other coordinate raises the "wide" flag and its slots are matched
 //    through the input rows instead).
-// Every key keeps its smallest row -- std::map::emplace's "first occurrence
-// wins" (sparse_ops.cpp:124-127).
+// The {row, tag} word is claimed with one 64-bit CAS; a second row with the
+// same coordinates lowers it with a 64-bit atomicMin, so every key keeps its
+// smallest row -- std::map::emplace's "first occurrence wins"
+// (sparse_ops.cpp:124-127).
 //
-// Every build draws a new seed, one above the last in the process, so the
-// table needs no clearing pass between builds:
-//  - a window cell is the 64-bit word {~row, seed}: the seed in the high half
-//    and the complemented row in the low half, so one atomicMax both replaces
-//    any earlier build's word and keeps the smallest row of this build (a
-//    word above the current seed -- memory that never held the table -- is
-//    replaced by CAS instead);
-//  - a hash slot is claimed with a CAS of {row, tag}, tag = tag_of(seed, index)
-//    (a bijection of seed ^ f(index)), and lowered with atomicMin by a second
-//    row of its key.
-// A cell or slot belongs to the current build only when it carries the
-// current seed or tag.  Memory that never held the table (a fresh workspace)
-// reads as empty except with probability 2^-32 per word; such a hash slot
-// must still match the packed 64-bit key (or, wide, the input row's
-// coordinates) before a lookup returns its row.
+// A cell or slot belongs to the current build only when its tag equals
+// tag_of(seed, index), and every build draws a new seed: tag_of is a
+// bijection of seed ^ f(index), so nothing written by another build carries
+// the current tag, and the table needs no clearing pass between builds.
+// Memory that never held the table (a fresh workspace) reads as empty except
+// with probability 2^-32 per word; such a hash slot must still match the
+// packed 64-bit key (or, wide, the input row's coordinates) before a lookup
+// returns its row, and a window cell's row is checked against the input
+// rows' coordinates on insert.
 constexpr int kWindow = 64;                                 // cells per axis
 constexpr int64_t kWindowCells = int64_t(kWindow) * kWindow * kWindow;
 
@@ -137,29 +133,23 @@ kmap_insert_kernel(const int4 *__restrict__ keys, int32_t n, KmapHash h) {
         kmap_hash_insert(keys, n, h, i, c);
         return;
     }
+    const uint32_t tag = tag_of(h.seed, static_cast<uint32_t>(cell));
     unsigned long long *word = h.cells + cell;
-    const unsigned long long mine = (static_cast<unsigned long long>(h.seed) << 32) | ~static_cast<uint32_t>(i);
-    unsigned long long cur = atomicMax(word, mine);
+    const unsigned long long mine = (static_cast<unsigned long long>(tag) << 32) | static_cast<uint32_t>(i);
+    unsigned long long cur = *word;  // a stale read only fails the CAS
     for (;;) {
-        const uint32_t build = static_cast<uint32_t>(cur >> 32);
-        if (build == h.seed) {  // another row of this build holds the cell (and so the key)
-            if (~static_cast<uint32_t>(cur) != static_cast<uint32_t>(i))
-                h.flags[kFlagDuplicate] = flag_of(h.seed, kFlagDuplicate);
+        // A current cell holds this key (one cell per key) unless its tag is
+        // a stale word's chance match, whose row names other coordinates.
+        const uint32_t r = static_cast<uint32_t>(cur);
+        if (static_cast<uint32_t>(cur >> 32) == tag && r < static_cast<uint32_t>(n) && same_key(keys[r], c)) {
+            atomicMin(word, mine);
+            h.flags[kFlagDuplicate] = flag_of(h.seed, kFlagDuplicate);
             return;
         }
-        if (build < h.seed) return;  // an earlier build's word, replaced
-        // a word above this build (never part of the table): replace it
         const unsigned long long prev = atomicCAS(word, cur, mine);
         if (prev == cur) return;
-        cur = prev;
-        if (static_cast<uint32_t>(cur >> 32) == h.seed) cur = atomicMax(word, mine);
+        cur = prev;  // claimed meanwhile by a row of this build (with this key)
     }
-}
-
-// The row a window word names in this build, or -1.
-__device__ __forceinline__ int32_t window_row(const KmapHash &h, int32_t n, unsigned long long v) {
-    const uint32_t r = ~static_cast<uint32_t>(v);
-    return static_cast<uint32_t>(v >> 32) == h.seed && r < static_cast<uint32_t>(n) ? static_cast<int32_t>(r) : -1;
 }
 
 // Hash path of kmap_find (coordinates outside the window).
@@ -184,62 +174,34 @@ __device__ __forceinline__ int32_t kmap_find(const KmapHash &h, const int4 *__re
                                              bool wide) {
     const int32_t cell = window_cell(q);
     if (cell < 0) return kmap_hash_find(h, keys, n, q, wide);
-    return window_row(h, n, h.cells[cell]);
+    const unsigned long long v = h.cells[cell];
+    return static_cast<uint32_t>(v >> 32) == tag_of(h.seed, static_cast<uint32_t>(cell))
+               ? static_cast<int32_t>(static_cast<uint32_t>(v))
+               : -1;
 }
 
-// One thread per voxel: kmap[i*27+o] = first row at coords[i]+d(o).  A voxel
-// whose 3x3x3 neighbourhood lies inside the window reads its 27 cells at
-// constant offsets from its own; the block's rows (27 entries each,
-// contiguous) leave through LDS as 16-byte stores.
+// One thread per (voxel, offset): kmap[i*27+o] = first row at coords[i]+d(o).
 __global__ void __launch_bounds__(kThreads)
 kmap_lookup_kernel(const int4 *__restrict__ coords, int32_t n, KmapHash h, int32_t missing,
                    int32_t *__restrict__ kmap) {
-    __shared__ int32_t stage[kThreads * 27];
-    const int32_t i0 = blockIdx.x * kThreads;
-    const int32_t i = i0 + threadIdx.x;
+    const int32_t g = blockIdx.x * kThreads + threadIdx.x;
+    if (g >= n * 27) return;
+    const int32_t i = g / 27;
+    const int32_t o = g - i * 27;
+    const int4 c = coords[i];
     const bool wide = h.flags[kFlagWide] == flag_of(h.seed, kFlagWide);
     const bool dup = h.flags[kFlagDuplicate] == flag_of(h.seed, kFlagDuplicate);
-    int32_t *row = stage + threadIdx.x * 27;  // stride 27 (odd): no bank conflicts
-    if (i < n) {
-        const int4 c = coords[i];
-        // Later duplicates of a coordinate keep an all-missing row
-        // (sparse_ops.cpp:129-139 only visits each key's first row).
-        const bool owner = !dup || kmap_find(h, coords, n, c, wide) == i;
-        const uint32_t x = static_cast<uint32_t>(c.y), y = static_cast<uint32_t>(c.z), z = static_cast<uint32_t>(c.w);
-        if (!owner) {
-            for (int o = 0; o < 27; ++o) row[o] = missing;
-        } else if (c.x == 0 && x - 1u < kWindow - 2u && y - 1u < kWindow - 2u && z - 1u < kWindow - 2u) {
-            const unsigned long long *center = h.cells + (x * kWindow + y) * kWindow + z;
-            unsigned long long v[27];
-#pragma unroll
-            for (int o = 0; o < 27; ++o)
-                v[o] = center[((o / 9 - 1) * kWindow + ((o / 3) % 3 - 1)) * kWindow + (o % 3 - 1)];
-#pragma unroll
-            for (int o = 0; o < 27; ++o) {
-                const int32_t r = window_row(h, n, v[o]);
-                row[o] = r >= 0 ? r : missing;
-            }
-        } else {
-            for (int o = 0; o < 27; ++o) {
-                int4 q = c;
-                int32_t r = -1;
-                if (add_fits(c.y, o / 9 - 1, &q.y) && add_fits(c.z, (o / 3) % 3 - 1, &q.z) &&
-                    add_fits(c.w, o % 3 - 1, &q.w))
-                    r = kmap_find(h, coords, n, q, wide);
-                row[o] = r >= 0 ? r : missing;
-            }
-        }
+    int32_t result = missing;
+    // Later duplicates of a coordinate keep an all-missing row
+    // (sparse_ops.cpp:129-139 only visits each key's first row).
+    const bool owner = !dup || kmap_find(h, coords, n, c, wide) == i;
+    int4 q = c;
+    if (owner && add_fits(c.y, o / 9 - 1, &q.y) && add_fits(c.z, (o / 3) % 3 - 1, &q.z) &&
+        add_fits(c.w, o % 3 - 1, &q.w)) {
+        const int32_t r = kmap_find(h, coords, n, q, wide);
+        if (r >= 0) result = r;
     }
-    __syncthreads();
-    const int32_t total = min(kThreads, n - i0) * 27;
-    int32_t *dst = kmap + static_cast<int64_t>(i0) * 27;
-    int32_t e0 = 0;
-    if ((reinterpret_cast<uintptr_t>(dst) & 15) == 0) {  // i0 * 108 bytes keeps 16-byte alignment
-        for (int32_t v4 = threadIdx.x; v4 < total / 4; v4 += kThreads)
-            reinterpret_cast<int4 *>(dst)[v4] = reinterpret_cast<const int4 *>(stage)[v4];
-        e0 = total / 4 * 4;
-    }
-    for (int32_t e = e0 + threadIdx.x; e < total; e += kThreads) dst[e] = stage[e];
+    kmap[g] = result;
 }
 
 // ---- subdivide ------------------------------------------------------------
@@ -312,9 +274,8 @@ void kmap_layout(W &w, int64_t n, KmapHash *h) {
     }
 }
 
-// A new seed for every build in the process, one above the last (window
-// cells order builds by it; never repeated before 2^32 builds), so cells and
-// slots of earlier builds read as empty.
+// A new seed for every build in the process (never repeated before 2^32
+// builds), so slots of earlier builds read as empty.
 uint32_t next_seed() {
     static std::atomic<uint32_t> counter{0x3C6EF372u};
     return counter.fetch_add(1, std::memory_order_relaxed);
@@ -326,7 +287,8 @@ void run_kmap(const int4 *coords, int32_t n, int32_t missing, int32_t *kmap, Kma
     h.seed = next_seed();
     kmap_insert_kernel<<<blocks_for(n), kThreads, 0, stream>>>(coords, n, h);
     launch_check("kmap_insert");
-    kmap_lookup_kernel<<<blocks_for(n), kThreads, 0, stream>>>(coords, n, h, missing, kmap);
+    kmap_lookup_kernel<<<blocks_for(static_cast<int64_t>(n) * 27), kThreads, 0, stream>>>(coords, n, h, missing,
+                                                                                           kmap);
     launch_check("kmap_lookup");
 }
 
