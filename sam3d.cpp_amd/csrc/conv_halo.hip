@@ -109,6 +109,7 @@ __device__ __forceinline__ int wave_reduce(int x, Op op) {
 
 // Exclusive prefix over the workgroup (256 threads) of one value each;
 // returns the prefix, writes the total to *total.  Every thread must call it.
+template <int WAVES = 4>
 __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t *wave_sums, uint32_t *total) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     uint32_t incl = v;
@@ -119,10 +120,13 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t *w
     }
     if (lane == 63) wave_sums[wave] = incl;
     __syncthreads();
-    uint32_t base = 0;
+    uint32_t base = 0, all = 0;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) base += w < wave ? wave_sums[w] : 0u;
-    *total = wave_sums[0] + wave_sums[1] + wave_sums[2] + wave_sums[3];
+    for (int w = 0; w < WAVES; ++w) {
+        base += w < wave ? wave_sums[w] : 0u;
+        all += wave_sums[w];
+    }
+    *total = all;
     return base + incl - v;
 }
 
@@ -134,7 +138,7 @@ struct TileDedupe {
     uint32_t mask, distinct;
     bool global_a;
 };
-template <int MB>
+template <int MB, bool ENTRY_ORDER = false, int NTH = 256>
 __device__ __forceinline__ TileDedupe dedupe_tile(const int32_t *kmap, int64_t n_src, int32_t row_shift, int64_t m0,
                                                   int tile_rows, uint16_t *table, int32_t *table32,
                                                   uint32_t *bitmap, uint32_t *prefix, uint32_t *slot_row,
@@ -145,14 +149,14 @@ __device__ __forceinline__ TileDedupe dedupe_tile(const int32_t *kmap, int64_t n
     // ---- 1. this tile's map slice (ROWS * 27 entries; 16-byte aligned,
     // ROWS * 108 bytes per tile), as source rows (-1: missing)
     constexpr int V4 = ENTRIES / 4;
-    constexpr int Q = (V4 + 255) / 256;
+    constexpr int Q = (V4 + NTH - 1) / NTH;
     const int count = tile_rows * kMaxKvol;
     int sj[Q][4];
     {
         const int4 *src = reinterpret_cast<const int4 *>(kmap + m0 * kMaxKvol);
 #pragma unroll
         for (int q = 0; q < Q; ++q) {
-            const int u = tid + q * 256;
+            const int u = tid + q * NTH;
             int4 v = make_int4(-1, -1, -1, -1);
             if (u < V4) {
                 if (4 * u + 3 < count) {
@@ -171,12 +175,15 @@ __device__ __forceinline__ TileDedupe dedupe_tile(const int32_t *kmap, int64_t n
             }
         }
     }
-    // ---- 2. range of named source rows and the offset mask
+    // ---- 2. range of named source rows and the offset mask (the range,
+    // mask and bitmap are reset while the slice's loads are in flight)
     if (tid == 0) {
         misc[0] = INT32_MAX;
         misc[1] = INT32_MIN;
         misc[2] = 0;
     }
+    for (int w = tid; w < SM::BITWORDS; w += NTH) bitmap[w] = 0u;
+    __syncthreads();
     {
         int lo = INT32_MAX, hi = INT32_MIN, m = 0;
 #pragma unroll
@@ -186,12 +193,11 @@ __device__ __forceinline__ TileDedupe dedupe_tile(const int32_t *kmap, int64_t n
                 if (sj[q][k] >= 0) {
                     lo = min(lo, sj[q][k]);
                     hi = max(hi, sj[q][k]);
-                    m |= 1 << ((4 * (tid + q * 256) + k) % kMaxKvol);
+                    m |= 1 << ((4 * (tid + q * NTH) + k) % kMaxKvol);
                 }
         lo = wave_reduce(lo, [](int x, int y) { return min(x, y); });
         hi = wave_reduce(hi, [](int x, int y) { return max(x, y); });
         m = wave_reduce(m, [](int x, int y) { return x | y; });
-        __syncthreads();
         if (lane == 0) {
             atomicMin(&misc[0], lo);
             atomicMax(&misc[1], hi);
@@ -207,8 +213,6 @@ __device__ __forceinline__ TileDedupe dedupe_tile(const int32_t *kmap, int64_t n
     if (!global_a && span > 0) {
         // ---- 3. bitmap of named rows -> slot = rank among them
         const int words = static_cast<int>((span + 31) / 32);
-        for (int w = tid; w < words; w += 256) bitmap[w] = 0u;
-        __syncthreads();
 #pragma unroll
         for (int q = 0; q < Q; ++q)
 #pragma unroll
@@ -218,7 +222,7 @@ __device__ __forceinline__ TileDedupe dedupe_tile(const int32_t *kmap, int64_t n
                     atomicOr(&bitmap[r >> 5], 1u << (r & 31));
                 }
         __syncthreads();
-        constexpr int WPT = SM::BITWORDS / 256;  // words per thread (4 or 2)
+        constexpr int WPT = SM::BITWORDS / NTH;  // words per thread
         uint32_t cnt[WPT], mine = 0;
 #pragma unroll
         for (int k = 0; k < WPT; ++k) {
@@ -226,7 +230,7 @@ __device__ __forceinline__ TileDedupe dedupe_tile(const int32_t *kmap, int64_t n
             cnt[k] = w < words ? static_cast<uint32_t>(__popc(bitmap[w])) : 0u;
             mine += cnt[k];
         }
-        uint32_t run = block_exclusive_scan(mine, reinterpret_cast<uint32_t *>(misc + 4), &distinct);
+        uint32_t run = block_exclusive_scan<NTH / 64>(mine, reinterpret_cast<uint32_t *>(misc + 4), &distinct);
 #pragma unroll
         for (int k = 0; k < WPT; ++k) {
             const int w = tid * WPT + k;
@@ -242,11 +246,12 @@ __device__ __forceinline__ TileDedupe dedupe_tile(const int32_t *kmap, int64_t n
     for (int q = 0; q < Q; ++q)
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            const int e = 4 * (tid + q * 256) + k;
+            const int e = 4 * (tid + q * NTH) + k;
             if (e >= ENTRIES) continue;
             const int r = e / kMaxKvol, o = e - r * kMaxKvol;
+            const int ti = ENTRY_ORDER ? e : o * ROWS + r;
             if (global_a) {
-                table32[o * ROWS + r] = sj[q][k];
+                table32[ti] = sj[q][k];
             } else {
                 uint32_t slot = CAP;
                 if (sj[q][k] >= 0) {
@@ -255,7 +260,7 @@ __device__ __forceinline__ TileDedupe dedupe_tile(const int32_t *kmap, int64_t n
                     slot = prefix[d >> 5] + static_cast<uint32_t>(__popc(bits & ((1u << (d & 31)) - 1u)));
                     slot_row[slot] = static_cast<uint32_t>(sj[q][k]);  // writers of one slot agree
                 }
-                table[o * ROWS + r] = static_cast<uint16_t>(slot);
+                table[ti] = static_cast<uint16_t>(slot);
             }
         }
     __syncthreads();
@@ -1144,13 +1149,18 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
     finish_rows<16, ROWS, STG_LD, kHalo8Threads, true>(a, stg, stg, m0, nb0, tile_rows, tid, res, params);
 }
 
+// Threads of a 128-row plan build: one workgroup per tile on most CUs, so
+// the dedupe's short dependent steps run on 16 waves (latency hidden by
+// more waves, fewer entries per thread).
+constexpr int kPlanBuild128Threads = 1024;
+
 // One workgroup per tile (64 or 128 rows): dedupe_tile, then the record to
 // memory.  128-row records hold halo byte offsets and name missing
 // neighbours by the zero row of the kernel's halo layout: slot kH8Single when
 // the tile's distinct rows need the single large buffer, else kH8Double (two
 // buffers, one per chunk).
-template <int MB>
-__global__ void __launch_bounds__(256) gather_plan_build_kernel(const int32_t *kmap, int64_t n_out, int64_t n_src,
+template <int MB, int NTH>
+__global__ void __launch_bounds__(NTH) gather_plan_build_kernel(const int32_t *kmap, int64_t n_out, int64_t n_src,
                                                                 int32_t row_shift, char *plan) {
     using SM = HaloSmem<MB>;
     constexpr int ROWS = SM::ROWS;
@@ -1161,31 +1171,35 @@ __global__ void __launch_bounds__(256) gather_plan_build_kernel(const int32_t *k
     __shared__ __align__(16) uint32_t bitmap[SM::BITWORDS];
     __shared__ __align__(16) uint32_t prefix[SM::BITWORDS];
     __shared__ __align__(16) uint32_t slot_row[SM::CAP];
-    __shared__ __align__(16) int32_t misc[16];
+    __shared__ __align__(16) int32_t misc[4 + NTH / 64];
     const int tile = blockIdx.x, tid = threadIdx.x;
     const int64_t m0 = static_cast<int64_t>(tile) * ROWS;
     const int tile_rows = static_cast<int>(min(static_cast<int64_t>(ROWS), n_out - m0));
-    const TileDedupe dd = dedupe_tile<MB>(kmap, n_src, row_shift, m0, tile_rows, table, table32, bitmap, prefix,
-                                          slot_row, misc);
+    // The tables come back in entry order (row-major, 27 per row: no LDS
+    // bank conflicts on writing them); the record stores them offset-major.
+    const TileDedupe dd = dedupe_tile<MB, true, NTH>(kmap, n_src, row_shift, m0, tile_rows, table, table32, bitmap,
+                                                prefix, slot_row, misc);
     char *rec = plan + static_cast<int64_t>(tile) * REC;
     if (tid == 0)
         *reinterpret_cast<uint4 *>(rec) = make_uint4(dd.global_a ? 1u : 0u, dd.distinct, dd.mask, 0u);
+    auto entry = [](int i) { return (i % ROWS) * kMaxKvol + i / ROWS; };  // record index -> entry
     if (dd.global_a) {
-        for (int i = tid; i < ROWS * kMaxKvol / 4; i += 256)
-            reinterpret_cast<uint4 *>(rec + kPlanHeader)[i] = reinterpret_cast<const uint4 *>(table32)[i];
+        for (int i = tid; i < ROWS * kMaxKvol; i += NTH)
+            reinterpret_cast<int32_t *>(rec + kPlanHeader)[i] = table32[entry(i)];
     } else {
         if constexpr (MB == 4) {
             const uint32_t z = dd.distinct <= static_cast<uint32_t>(kH8Double) ? kH8Double : kH8Single;
-            for (int i = tid; i < ROWS * kMaxKvol; i += 256) {
-                const uint32_t sl = table[i];
+            for (int i = tid; i < ROWS * kMaxKvol; i += NTH) {
+                const uint32_t sl = table[entry(i)];
                 reinterpret_cast<uint32_t *>(rec + kPlanHeader)[i] =
                     halo_offset(sl == static_cast<uint32_t>(SM::CAP) ? z : sl);
             }
         } else {
-            for (int i = tid; i < ROWS * kMaxKvol * 2 / 16; i += 256)
-                reinterpret_cast<uint4 *>(rec + kPlanHeader)[i] = reinterpret_cast<const uint4 *>(table)[i];
+            for (int i = tid; i < ROWS * kMaxKvol / 2; i += NTH)  // two rows of one offset per word
+                reinterpret_cast<uint32_t *>(rec + kPlanHeader)[i] =
+                    static_cast<uint32_t>(table[entry(2 * i)]) | static_cast<uint32_t>(table[entry(2 * i + 1)]) << 16;
         }
-        for (int i = tid; i < static_cast<int>(dd.distinct); i += 256)
+        for (int i = tid; i < static_cast<int>(dd.distinct); i += NTH)
             reinterpret_cast<uint32_t *>(rec + SLOTS)[i] = slot_row[i];
     }
 }
@@ -1204,11 +1218,12 @@ void launch_gather_plan_build(int rows, const int32_t *kmap, int64_t n_out, int6
                               void *plan, hipStream_t stream) {
     const unsigned tiles = static_cast<unsigned>((n_out + rows - 1) / rows);
     if (rows == 128)
-        hipLaunchKernelGGL(gather_plan_build_kernel<4>, dim3(tiles), dim3(256), 0, stream, kmap, n_out, n_src,
-                           row_shift, static_cast<char *>(plan));
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(gather_plan_build_kernel<4, kPlanBuild128Threads>), dim3(tiles),
+                           dim3(kPlanBuild128Threads), 0, stream, kmap, n_out, n_src, row_shift,
+                           static_cast<char *>(plan));
     else
-        hipLaunchKernelGGL(gather_plan_build_kernel<2>, dim3(tiles), dim3(256), 0, stream, kmap, n_out, n_src,
-                           row_shift, static_cast<char *>(plan));
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(gather_plan_build_kernel<2, 256>), dim3(tiles), dim3(256), 0, stream, kmap,
+                           n_out, n_src, row_shift, static_cast<char *>(plan));
 }
 
 }  // namespace s3dx
