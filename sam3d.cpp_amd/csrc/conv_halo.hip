@@ -1149,10 +1149,11 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
     finish_rows<16, ROWS, STG_LD, kHalo8Threads, true>(a, stg, stg, m0, nb0, tile_rows, tid, res, params);
 }
 
-// Threads of a 128-row plan build: one workgroup per tile on most CUs, so
-// the dedupe's short dependent steps run on 16 waves (latency hidden by
-// more waves, fewer entries per thread).
+// Threads of a plan build's workgroup (one per tile): the dedupe's short
+// dependent steps run on 16 (128-row) or 8 (64-row) waves, one bitmap word
+// and about four map entries per thread.
 constexpr int kPlanBuild128Threads = 1024;
+constexpr int kPlanBuild64Threads = 512;
 
 // One workgroup per tile (64 or 128 rows): dedupe_tile, then the record to
 // memory.  128-row records hold halo byte offsets and name missing
@@ -1222,8 +1223,9 @@ void launch_gather_plan_build(int rows, const int32_t *kmap, int64_t n_out, int6
                            dim3(kPlanBuild128Threads), 0, stream, kmap, n_out, n_src, row_shift,
                            static_cast<char *>(plan));
     else
-        hipLaunchKernelGGL(HIP_KERNEL_NAME(gather_plan_build_kernel<2, 256>), dim3(tiles), dim3(256), 0, stream, kmap,
-                           n_out, n_src, row_shift, static_cast<char *>(plan));
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(gather_plan_build_kernel<2, kPlanBuild64Threads>), dim3(tiles),
+                           dim3(kPlanBuild64Threads), 0, stream, kmap, n_out, n_src, row_shift,
+                           static_cast<char *>(plan));
 }
 
 }  // namespace s3dx
