@@ -263,23 +263,34 @@ __device__ __forceinline__ void load_residual(const ConvArgs &a, int64_t m0, int
 struct RowParams {
     float bias[8], lw[8], lb[8], ms[8], mh[8];
 };
-// Bias and LayerNorm affine; the modulation separately (load_row_mod).
-__device__ __forceinline__ void load_row_params(const ConvArgs &a, int col0, RowParams &q) {
+// Columns col0..col0+7 of a per-column float array (dflt for a null array
+// and past cout): two 16-byte loads when the eight are real and the array
+// is 16-byte aligned (col0 is a multiple of 8), else element loads.
+__device__ __forceinline__ void load_cols8(const float *p, int col0, int cout, float dflt, float (&o)[8]) {
+    if (p == nullptr) {
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const bool real = col0 + k < a.cout;
-        q.bias[k] = a.bias && real ? a.bias[col0 + k] : 0.0f;
-        q.lw[k] = a.ln_w && real ? a.ln_w[col0 + k] : 1.0f;
-        q.lb[k] = a.ln_b && real ? a.ln_b[col0 + k] : 0.0f;
+        for (int k = 0; k < 8; ++k) o[k] = dflt;
+        return;
+    }
+    if (col0 + 8 <= cout && (reinterpret_cast<uintptr_t>(p) & 15u) == 0) {
+        const float4 x0 = *reinterpret_cast<const float4 *>(p + col0);
+        const float4 x1 = *reinterpret_cast<const float4 *>(p + col0 + 4);
+        o[0] = x0.x; o[1] = x0.y; o[2] = x0.z; o[3] = x0.w;
+        o[4] = x1.x; o[5] = x1.y; o[6] = x1.z; o[7] = x1.w;
+    } else {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) o[k] = col0 + k < cout ? p[col0 + k] : dflt;
     }
 }
+// Bias and LayerNorm affine; the modulation separately (load_row_mod).
+__device__ __forceinline__ void load_row_params(const ConvArgs &a, int col0, RowParams &q) {
+    load_cols8(a.bias, col0, a.cout, 0.0f, q.bias);
+    load_cols8(a.ln_w, col0, a.cout, 1.0f, q.lw);
+    load_cols8(a.ln_b, col0, a.cout, 0.0f, q.lb);
+}
 __device__ __forceinline__ void load_row_mod(const ConvArgs &a, int col0, RowParams &q) {
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        const bool real = col0 + k < a.cout;
-        q.ms[k] = a.mod_scale && real ? a.mod_scale[col0 + k] : 0.0f;
-        q.mh[k] = a.mod_shift && real ? a.mod_shift[col0 + k] : 0.0f;
-    }
+    load_cols8(a.mod_scale, col0, a.cout, 0.0f, q.ms);
+    load_cols8(a.mod_shift, col0, a.cout, 0.0f, q.mh);
 }
 
 // SWZ: the tile's 16-byte group q of row r sits at q ^ 8 when r & 4.
@@ -353,10 +364,23 @@ __device__ __forceinline__ void finish_rows(const ConvArgs &a, const float *stg,
         }
     }
 
-    const float(&lw)[8] = q.lw;
-    const float(&lb)[8] = q.lb;
-    const float(&ms)[8] = q.ms;
-    const float(&mh)[8] = q.mh;
+    // LayerNorm affine and modulate as one affine per column: the row's
+    // t = (v - mean) * rstd becomes t * la + lc, la = lw (1 + ms) and
+    // lc = lb (1 + ms) + mh (the modulate h * ms + h + mh of h = t * lw + lb).
+    float la[8], lc[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        la[k] = q.lw[k];
+        lc[k] = q.lb[k];
+    }
+    if (a.ln && a.mod_scale) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float s1 = 1.0f + q.ms[k];
+            la[k] = q.lw[k] * s1;
+            lc[k] = fmaf(q.lb[k], s1, q.mh[k]);
+        }
+    }
     // Power-of-two groups: LayerNorm statistics of every pass first, all
     // passes in lockstep so the cross-lane sums overlap (two-pass mean /
     // variance; every lane of a group takes part, whatever its row).
@@ -375,11 +399,15 @@ __device__ __forceinline__ void finish_rows(const ConvArgs &a, const float *stg,
                             ((vs[p][4] + vs[p][5]) + (vs[p][6] + vs[p][7]));
 #pragma unroll
             for (int p = 0; p < PASSES; ++p) mean_p[p] = row_sum(mean_p[p]) * inv_c;
+            // vs becomes v - mean (used again to normalize)
 #pragma unroll
             for (int p = 0; p < PASSES; ++p) {
                 float d2 = 0.0f;
 #pragma unroll
-                for (int k = 0; k < 8; ++k) d2 += (vs[p][k] - mean_p[p]) * (vs[p][k] - mean_p[p]);
+                for (int k = 0; k < 8; ++k) {
+                    vs[p][k] -= mean_p[p];
+                    d2 += vs[p][k] * vs[p][k];
+                }
                 var_p[p] = d2;
             }
 #pragma unroll
@@ -402,7 +430,7 @@ __device__ __forceinline__ void finish_rows(const ConvArgs &a, const float *stg,
         if (a.ln) {
             float m, q;
             if constexpr (RM::POW2) {
-                m = mean_p[p];
+                m = 0.0f;  // v already holds v - mean
                 q = var_p[p];
             } else {
                 m = 0.0f;
@@ -415,11 +443,7 @@ __device__ __forceinline__ void finish_rows(const ConvArgs &a, const float *stg,
             }
             const float rstd = rsqrtf(q * inv_c + a.eps);
 #pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                float t = (v[k] - m) * rstd * lw[k] + lb[k];
-                if (a.mod_scale) t = (t * ms[k] + t) + mh[k];
-                v[k] = t;
-            }
+            for (int k = 0; k < 8; ++k) v[k] = fmaf((v[k] - m) * rstd, la[k], lc[k]);
         }
         if (a.silu) {
 #pragma unroll
