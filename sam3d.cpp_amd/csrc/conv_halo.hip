@@ -279,12 +279,16 @@ static_assert(kPlanHeader + 64 * kMaxKvol * 4 <= kGatherPlanRecord, "global reco
 static_assert(kGatherPlanRecord % 1024 == 0, "records copy as whole 1 KiB pieces");
 
 // 128-row records (the 8-wave kernel): the same header; halo tiles hold the
-// u32 table [27][128] of halo byte offsets (halo_offset of each slot), then
-// at kPlan128Slots the source row of each slot; global tiles the int32 row
-// table [27][128].
-constexpr int kPlan128Slots = kPlanHeader + 128 * kMaxKvol * 4;  // 13840
-static_assert(kPlan128Slots + HaloSmem<4>::CAP * 4 <= kGatherPlanRecord128, "halo record fits");
-static_assert(kPlanHeader + 128 * kMaxKvol * 4 <= kGatherPlanRecord128, "global record fits");
+// source row of each slot right after it, then at kPlan128Table the u32
+// table [27][128] of halo byte offsets (halo_offset of each slot); global
+// tiles the int32 row table [27][128] at kPlan128Table.  The header and the
+// rows come first so that a kernel can start copying rows while the table
+// is still on its way.
+constexpr int kPlan128Slots = kPlanHeader;     // 16
+constexpr int kPlan128Table = 4608;
+constexpr int kPlan128HeadPieces = (kPlan128Slots + HaloSmem<4>::CAP * 4 + 1023) / 1024;  // 5 KiB
+static_assert(kPlan128Slots + HaloSmem<4>::CAP * 4 <= kPlan128Table, "halo record fits");
+static_assert(kPlan128Table + 128 * kMaxKvol * 4 <= kGatherPlanRecord128, "tables fit");
 static_assert(kGatherPlanRecord128 % 1024 == 0, "records copy as whole 1 KiB pieces");
 // Halo layout of the 8-wave kernel: two buffers of kH8BufRows rows (one per
 // chunk, the next chunk's copied while the current one is in use) with the
@@ -629,7 +633,7 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
     char *halo = smem;
     char *rec = smem + kH8Dump + 1024;
     // [27][128] u32: halo byte offsets, or source rows for global gathers
-    const int32_t *table32 = reinterpret_cast<const int32_t *>(rec + kPlanHeader);
+    const int32_t *table32 = reinterpret_cast<const int32_t *>(rec + kPlan128Table);
     const uint32_t *slot_row = reinterpret_cast<const uint32_t *>(rec + kPlan128Slots);
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -655,16 +659,30 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
         const int64_t plan_bytes = (a.n_out + ROWS - 1) / ROWS * kGatherPlanRecord128;
         const auto p_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(a.plan), static_cast<short>(0),
                                                               static_cast<int32_t>(plan_bytes), 0x00020000);
-#pragma unroll
-        for (int k = 0; k < (kGatherPlanRecord128 / 1024 + 7) / 8; ++k) {
-            const int i = wave + 8 * k;
-            if (i < kGatherPlanRecord128 / 1024)
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(p_rsrc, (__attribute__((address_space(3))) void *)(rec + i * 1024),
-                                                         16, lane * 16, tile * kGatherPlanRecord128 + i * 1024, 0, 0);
-        }
+        // the header and the slot rows only: the table follows later
+        static_assert(kPlan128HeadPieces <= 8, "one head piece per wave");
+        if (wave < kPlan128HeadPieces)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(p_rsrc, (__attribute__((address_space(3))) void *)(rec + wave * 1024),
+                                                     16, lane * 16, tile * kGatherPlanRecord128 + wave * 1024, 0, 0);
         __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
         __syncthreads();
     }
+    // The rest of the record (the table) into LDS; a path waits for it
+    // before its first table read.  The full loop requests it after its first
+    // halo copy, so that the rows the first tasks need are first in line.
+    auto load_table = [&]() __attribute__((always_inline)) {
+        const int64_t plan_bytes = (a.n_out + ROWS - 1) / ROWS * kGatherPlanRecord128;
+        const auto p_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(a.plan), static_cast<short>(0),
+                                                              static_cast<int32_t>(plan_bytes), 0x00020000);
+        constexpr int kRest = kGatherPlanRecord128 / 1024 - kPlan128HeadPieces;
+#pragma unroll
+        for (int k = 0; k < (kRest + 7) / 8; ++k) {
+            const int i = kPlan128HeadPieces + wave + 8 * k;
+            if (wave + 8 * k < kRest)
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(p_rsrc, (__attribute__((address_space(3))) void *)(rec + i * 1024),
+                                                         16, lane * 16, tile * kGatherPlanRecord128 + i * 1024, 0, 0);
+        }
+    };
     const uint32_t *hdr = reinterpret_cast<const uint32_t *>(rec);
     const bool global_a = __builtin_amdgcn_readfirstlane(hdr[0]) != 0;
     const uint32_t distinct = __builtin_amdgcn_readfirstlane(hdr[1]);
@@ -691,13 +709,15 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
                                                               0x00020000);
         const int groups = (static_cast<int>(distinct) + 7) >> 3;
         for (int g0 = wave; g0 < groups; g0 += 32) {
-            uint32_t off[4];
+            uint32_t off[4], srow[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) srow[k] = slot_row[min((g0 + 8 * k) * 8 + (lane >> 3), kH8Single - 1)];
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 const int sl = (g0 + 8 * k) * 8 + (lane >> 3);
                 const int p = (lane & 7) ^ halo_swizzle(sl);
                 off[k] = sl < static_cast<int>(distinct)
-                             ? (slot_row[min(sl, kH8Single - 1)] * static_cast<uint32_t>(a.cin) + c * kHChunk + p * 8) * 2u
+                             ? (srow[k] * static_cast<uint32_t>(a.cin) + c * kHChunk + p * 8) * 2u
                              : 0x80000000u;  // past the buffer: zeros
             }
 #pragma unroll
@@ -926,14 +946,20 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
         const int groups = (static_cast<int>(distinct) + 7) >> 3;
         uint32_t piece_off[kPieces];  // source byte offset of each piece at chunk 0
         int piece_group[kPieces];
+        // (the slot rows are read unconditionally, at clamped indexes, so
+        // that the nine LDS reads go out together)
+        uint32_t srow[kPieces];
 #pragma unroll
         for (int j = 0; j < kPieces; ++j) {
             piece_group[j] = min(wave + 8 * j, groups - 1);
+            srow[j] = slot_row[min(piece_group[j] * 8 + (lane >> 3), kH8Double)];
+        }
+#pragma unroll
+        for (int j = 0; j < kPieces; ++j) {
             const int sl = piece_group[j] * 8 + (lane >> 3);
             const int p = (lane & 7) ^ halo_swizzle(sl);
-            piece_off[j] = sl < static_cast<int>(distinct)
-                               ? (slot_row[min(sl, kH8Double)] * static_cast<uint32_t>(a.cin) + p * 8) * 2u
-                               : 0x80000000u;  // past the buffer: zeros
+            piece_off[j] = sl < static_cast<int>(distinct) ? (srow[j] * static_cast<uint32_t>(a.cin) + p * 8) * 2u
+                                                           : 0x80000000u;  // past the buffer: zeros
         }
         // piece j of chunk cc into buffer dst (soffset is outside the range
         // check: the zero-fill offset stays out of range)
@@ -950,6 +976,7 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
 #pragma unroll
             for (int j = 0; j < kPieces; ++j) piece(x_rsrc, j, 0, piece_off[j], halo + piece_group[j] * 1024);
         }
+        load_table();
 #pragma unroll
         for (int k = 0; k < RF; ++k) {
             load_b_at(wb, bf[k]);
@@ -996,16 +1023,23 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
             });
         };
         for (int c = 0; c < chunks; ++c) {
-            // chunk c's pieces precede the last 2 RF weight loads, and after
-            // the barrier no wave reads the buffer of chunk c-1
+            // chunk c's pieces (and for c = 0 the table) precede the last
+            // 2 RF weight loads, and after the barrier no wave reads the
+            // buffer of chunk c-1
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * RF));
             __syncthreads();
             chunk(c, buf_of(c), buf_of(c + 1), table32, static_cast<const char *>(a.x));
         }
     };
-    if (global_a) chunk_loop(std::true_type{});
-    else if (dbl && mask == (1u << kMaxKvol) - 1u) full_loop();
-    else chunk_loop(std::false_type{});
+    if (dbl && !global_a && mask == (1u << kMaxKvol) - 1u) {
+        full_loop();  // requests the table itself; its first wait covers it
+    } else {
+        load_table();
+        __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
+        __syncthreads();
+        if (global_a) chunk_loop(std::true_type{});
+        else chunk_loop(std::false_type{});
+    }
     // the epilogue's column parameters, in flight during the reduction
     RowParams params;
     load_row_params(a, nb0 * 32 + (tid % 16) * 8, params);
@@ -1184,16 +1218,16 @@ __global__ void __launch_bounds__(NTH) gather_plan_build_kernel(const int32_t *k
     if (tid == 0)
         *reinterpret_cast<uint4 *>(rec) = make_uint4(dd.global_a ? 1u : 0u, dd.distinct, dd.mask, 0u);
     auto entry = [](int i) { return (i % ROWS) * kMaxKvol + i / ROWS; };  // record index -> entry
+    constexpr int TABLE = MB == 2 ? kPlanHeader : kPlan128Table;
     if (dd.global_a) {
         for (int i = tid; i < ROWS * kMaxKvol; i += NTH)
-            reinterpret_cast<int32_t *>(rec + kPlanHeader)[i] = table32[entry(i)];
+            reinterpret_cast<int32_t *>(rec + TABLE)[i] = table32[entry(i)];
     } else {
         if constexpr (MB == 4) {
             const uint32_t z = dd.distinct <= static_cast<uint32_t>(kH8Double) ? kH8Double : kH8Single;
             for (int i = tid; i < ROWS * kMaxKvol; i += NTH) {
                 const uint32_t sl = table[entry(i)];
-                reinterpret_cast<uint32_t *>(rec + kPlanHeader)[i] =
-                    halo_offset(sl == static_cast<uint32_t>(SM::CAP) ? z : sl);
+                reinterpret_cast<uint32_t *>(rec + TABLE)[i] = halo_offset(sl == static_cast<uint32_t>(SM::CAP) ? z : sl);
             }
         } else {
             for (int i = tid; i < ROWS * kMaxKvol / 2; i += NTH)  // two rows of one offset per word
