@@ -116,6 +116,15 @@ def test_planned_run_equals_unplanned(s3dx, O, W, monkeypatch, case):
     other.run(xd, n, kd, n, y1, s3dx.BF16, plan=gp)
     assert np.array_equal(y0.download(), y1.download())
     check_rel(_host(W, y1), _oracle(O, W, x, kmap, n, cin, cout, 41, False), 1e-2, f"{case} (second layer)")
+    # with a residual and no LayerNorm (the 8-wave kernel then finishes each
+    # column half on its own)
+    res2 = W.round_bf16(W.normal_f32(41, 4, (n, cout)))
+    rd2 = _bf(s3dx, W, res2)
+    other.run(xd, n, kd, n, y0, s3dx.BF16, rd2)
+    other.run(xd, n, kd, n, y1, s3dx.BF16, rd2, plan=gp)
+    assert np.array_equal(y0.download(), y1.download())
+    check_rel(_host(W, y1), _oracle(O, W, x, kmap, n, cin, cout, 41, False, res2), 1e-2,
+              f"{case} (second layer + residual)")
     conv.run(xd, n, kd, n, y1, s3dx.BF16, rd, plan=gp)
     check_rel(_host(W, y1), _oracle(O, W, x, kmap, n, cin, cout, 40, ln, res), 1e-2, case)
 
