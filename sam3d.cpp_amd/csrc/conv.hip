@@ -569,23 +569,27 @@ LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bo
         // distinct source row once per chunk into LDS and reads every weight
         // fragment once.  64-row tiles (tiling 21) by default, 128-row tiles
         // (tiling 20) with S3DX_CONV_HALO=128; S3DX_CONV_TILING=<other id> or
-        // S3DX_CONV_HALO=0 keeps the kernels above (tuning, tests).
+        // S3DX_CONV_HALO=0 keeps the kernels above (tuning, tests).  Layers
+        // whose columns come in 96 but not 128 (the mesh decoder's 192 and
+        // 96) take 64-row, 96-column tiles when no LayerNorm spans the row.
         {
             const char *te = std::getenv("S3DX_CONV_TILING");
             const char *he = std::getenv("S3DX_CONV_HALO");
             const int tid = te ? std::atoi(te) : 0;
             const bool allowed = te ? (tid == 20 || tid == 21) : !(he && std::atoi(he) == 0);
-            if (allowed && bf && conv->kvol == kMaxKvol && conv->cin % 64 == 0 && blocks % 4 == 0 && !p.xf &&
-                splitk_ok && (!conv->ln || conv->cout == 128)) {
+            const bool nb4 = blocks % 4 == 0 && (!conv->ln || conv->cout == 128);
+            const bool nb3 = !nb4 && blocks % 3 == 0 && !conv->ln && tid != 20 && !(he && std::atoi(he) == 128);
+            if (allowed && bf && conv->kvol == kMaxKvol && conv->cin % 64 == 0 && (nb4 || nb3) && !p.xf &&
+                splitk_ok) {
                 const int want = tid == 20 || tid == 21 ? tid : (he && std::atoi(he) == 128 ? 20 : 21);
                 for (const Tiling &t : kTilings)
                     if (t.id == want) p.tl = &t;
-                p.nb = 4;
+                p.nb = nb3 ? 3 : 4;
                 p.kc = 64;
             }
         }
         p.fused_ln = conv->ln && p.nb * 32 == conv->cout;
-        p.fn = tiling_kernel(p.tl->id, bf, p.kc, p.xf);
+        p.fn = p.tl->id == 21 && p.nb == 3 ? pick_halo_bf16(64, 3) : tiling_kernel(p.tl->id, bf, p.kc, p.xf);
         require(p.fn != nullptr, "no MFMA kernel for this shape");
         const int64_t mt = (n_out + p.tl->rows() - 1) / p.tl->rows();
         p.grid = dim3(static_cast<unsigned>(mt), static_cast<unsigned>(blocks / p.nb));
@@ -602,8 +606,8 @@ LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bo
 void apply_gather_plan(LaunchPlan &p, const s3dx_gather_plan *g, int64_t n_out, bool bf16_rows) {
     if (bf16_rows || !p.mfma || !p.tl || (p.tl->id != 20 && p.tl->id != 21)) return;
     if (g->rows == 64 && p.tl->id == 21) {
-        p.fn = pick_halo_bf16_planned(64);
-    } else if (g->rows == 128) {
+        p.fn = pick_halo_bf16_planned(64, p.nb);
+    } else if (g->rows == 128 && p.nb == 4) {
         for (const Tiling &t : kTilings)
             if (t.id == 22) p.tl = &t;
         p.fn = pick_halo_bf16_planned(128);
@@ -621,7 +625,7 @@ int gather_plan_rows(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out) {
         if (r == 64 || r == 128) return r;
     }
     const LaunchPlan p = plan_launch(conv, x_bytes, n_out, true);
-    if (!p.mfma || !p.tl || (p.tl->id != 20 && p.tl->id != 21)) return 64;
+    if (!p.mfma || !p.tl || (p.tl->id != 20 && p.tl->id != 21) || p.nb != 4) return 64;
     const int64_t tiles = (n_out + 127) / 128 * static_cast<int64_t>(p.grid.y);
     return tiles <= device_cus() ? 128 : 64;
 }
@@ -917,7 +921,8 @@ void describe_launch(const s3dx_conv *conv, const s3dx_gather_plan *gplan, int64
                     "gather plan was built for another map size or source rows");
             apply_gather_plan(p, gplan, n_out, bf16_rows);
         }
-        const bool planned = gplan && (p.fn == pick_halo_bf16_planned(64) || p.fn == pick_halo_bf16_planned(128));
+        const bool planned = gplan && (p.fn == pick_halo_bf16_planned(64) || p.fn == pick_halo_bf16_planned(128) ||
+                                       p.fn == pick_halo_bf16_planned(64, 3));
         char text[256];
         if (p.linear)
             std::snprintf(text, sizeof(text), "linear cols=%d ksteps=%d%s ln=%s grid=%u", p.nb * 32,
@@ -926,7 +931,7 @@ void describe_launch(const s3dx_conv *conv, const s3dx_gather_plan *gplan, int64
         else if (p.mfma)
             std::snprintf(text, sizeof(text), "mfma tiling=%d%s%s rows=%d cols=%d kc=%d xf=%d ln=%s grid=%ux%u",
                           p.tl->id, p.tl->splitk ? " split-k" : "", p.tl->id >= 20 ? " halo" : "", p.tl->rows(),
-                          p.tl->cols(), p.kc,
+                          p.tl->id >= 20 ? p.nb * 32 : p.tl->cols(), p.kc,
                           p.xf ? 1 : 0, conv->ln ? (p.fused_ln ? "fused" : "separate") : "none", p.grid.x,
                           p.grid.y);
         else
@@ -1049,7 +1054,9 @@ void conv_run_impl(const s3dx_conv *conv, const s3dx_gather_plan *gplan, const v
                     "gather plan was built for another map size or source rows");
             // Only the halo kernels read plans; other launches ignore it.
             apply_gather_plan(plan, gplan, n_out, bf16_rows);
-            if (plan.fn == pick_halo_bf16_planned(64) || plan.fn == pick_halo_bf16_planned(128)) a.plan = gplan->d;
+            if (plan.fn == pick_halo_bf16_planned(64) || plan.fn == pick_halo_bf16_planned(128) ||
+                plan.fn == pick_halo_bf16_planned(64, 3))
+                a.plan = gplan->d;
         }
         // A LayerNorm the epilogue cannot fuse runs as its own pass over the
         // conv's FP32 output (the layer's buffer), then modulate, SiLU and

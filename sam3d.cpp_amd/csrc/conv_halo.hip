@@ -318,8 +318,11 @@ struct HaloLds {
     static_assert(TOTAL <= (MB == 4 ? 160 * 1024 : 80 * 1024), "LDS budget");
 };
 
-template <int MB, bool PLAN>
+// NB 32-column blocks per tile: 4 (128 columns), or 3 (96 columns: wave w < 3
+// owns column block w in the reduction, wave 3 only hands its partials over).
+template <int MB, bool PLAN, int NB = 4>
 __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_halo_kernel(ConvArgs a) {
+    static_assert(NB == 4 || NB == 3, "128- or 96-column tiles");
     using SM = HaloSmem<MB>;
     constexpr int ROWS = SM::ROWS, CAP = SM::CAP, RPH = SM::RPH;
     __shared__ __align__(16) char smem[HaloLds<MB, PLAN>::TOTAL];
@@ -337,7 +340,7 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_halo_kernel(ConvArg
     const int half = lane >> 5;
     const int tile = xcd_tile(blockIdx.x, gridDim.x);
     const int64_t m0 = static_cast<int64_t>(tile) * ROWS;
-    const int nb0 = blockIdx.y * 4;
+    const int nb0 = blockIdx.y * NB;
     const int nbtot = a.cout_pad / 32;
     const int ksteps_total = a.cin / 16;
     const int chunks = a.cin / kHChunk;
@@ -379,20 +382,20 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_halo_kernel(ConvArg
             reinterpret_cast<uint4 *>(halo + CAP * kHRowBytes)[i] = make_uint4(0, 0, 0, 0);
     __syncthreads();
 
-    f32x16 acc[MB][4];
+    f32x16 acc[MB][NB];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = f32x16{};
+        for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f32x16{};
 
     const int ntasks = __popc(mask);
     // Fragment (k-step ks, column block cb) of the packed weights sits at
     // byte ((ks * nbtot + cb) * 64 + lane) * 16; wave w keeps column block
-    // (k + w) mod 4 in accumulator column k, so the block it owns in the
+    // (k + w) mod NB in accumulator column k, so the block it owns in the
     // final reduction is always accumulator column 0.
-    int32_t bvo[4];
+    int32_t bvo[NB];
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) bvo[nb] = lane * 16 + ((nb + wave) & 3) * 1024;
+    for (int nb = 0; nb < NB; ++nb) bvo[nb] = lane * 16 + ((nb + wave) % NB) * 1024;
     // Offsets walked by scalar cursors; past the last one a cursor repeats
     // it (prefetches beyond the end reload it harmlessly).  Offsets are
     // below 27, so bit 31 is free: the ctz of rest | bit 31 is 31 exactly
@@ -404,11 +407,11 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_halo_kernel(ConvArg
         rest &= rest - 1u;
         return c == 31 ? olast : c;
     };
-    auto mfmas = [&](const uint4 (&af)[MB], const uint4 (&bf)[4]) __attribute__((always_inline)) {
+    auto mfmas = [&](const uint4 (&af)[MB], const uint4 (&bf)[NB]) __attribute__((always_inline)) {
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-            for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = mfma_step<uint16_t>(af[mb], bf[nb], acc[mb][nb]);
+            for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = mfma_step<uint16_t>(af[mb], bf[nb], acc[mb][nb]);
     };
 
     // The chunk loop, for A from the halo (GA false) or from memory (GA
@@ -456,10 +459,10 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_halo_kernel(ConvArg
             // while t's MFMAs run; the weights of task t+R are requested
             // right after them.  Scheduling fences keep the weight loads in
             // that order.
-            auto load_b = [&](int o, uint4 (&bf)[4]) __attribute__((always_inline)) {
+            auto load_b = [&](int o, uint4 (&bf)[NB]) __attribute__((always_inline)) {
                 const int32_t sbase = ((o * ksteps_total + ks) * nbtot + nb0) * 1024;
 #pragma unroll
-                for (int nb = 0; nb < 4; ++nb) {
+                for (int nb = 0; nb < NB; ++nb) {
                     const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(w_rsrc, bvo[nb], sbase, 0);
                     bf[nb] = make_uint4(v.x, v.y, v.z, v.w);
                 }
@@ -494,7 +497,7 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_halo_kernel(ConvArg
             // Ring of R task sets (B requested R-1 tasks ahead: three for
             // 64-row tiles, whose tasks are half as long, else two).
             constexpr int R = MB == 2 ? 4 : 3;
-            uint4 bq[R][4], aq[R][MB];
+            uint4 bq[R][NB], aq[R][MB];
             int iq[R][MB];
             uint32_t rest_i = mask, rest_b = mask;
             // (issued in the loop's order, so the wait counts at the loop
@@ -563,8 +566,9 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_halo_kernel(ConvArg
 #pragma unroll
         for (int h = 0; h < RPH; ++h)
 #pragma unroll
-            for (int k = 1; k < 4; ++k) {
-                const int c = (k + wave) & 3;
+            for (int k = 0; k < NB; ++k) {
+                const int c = (k + wave) % NB;  // (waves below NB own block `wave`: column 0)
+                if (c == wave) continue;
                 float4 *slot = slot_of(h, c, wave);
 #pragma unroll
                 for (int g = 0; g < 4; ++g)
@@ -572,6 +576,7 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_halo_kernel(ConvArg
                                                       acc[RPH * p + h][k][4 * g + 2], acc[RPH * p + h][k][4 * g + 3]);
             }
         __syncthreads();
+        if (wave >= NB) continue;  // (a 96-column tile's wave 3 owns no block)
 #pragma unroll
         for (int h = 0; h < RPH; ++h)
 #pragma unroll
@@ -595,19 +600,22 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_halo_kernel(ConvArg
     __syncthreads();
     float *stg = reinterpret_cast<float *>(smem);
     float *part = stg + ROWS * SM::STG_LD;
+    if (wave < NB) {
 #pragma unroll
-    for (int p = 0; p < 2; ++p)
+        for (int p = 0; p < 2; ++p)
 #pragma unroll
-        for (int h = 0; h < RPH; ++h) {
-            const int col = wave * 32 + (lane & 31);
-            const int rb = (RPH * p + h) * 32 + 4 * half;
+            for (int h = 0; h < RPH; ++h) {
+                const int col = wave * 32 + (lane & 31);
+                const int rb = (RPH * p + h) * 32 + 4 * half;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) stg[(rb + 8 * (r >> 2) + (r & 3)) * SM::STG_LD + col] = fin[p][h][r];
-        }
-    uint4 res[RowMap<16, ROWS>::PASSES][2];
-    load_residual<16, ROWS>(a, m0, nb0, tile_rows, tid, res);
+                for (int r = 0; r < 16; ++r) stg[(rb + 8 * (r >> 2) + (r & 3)) * SM::STG_LD + col] = fin[p][h][r];
+            }
+    }
+    constexpr int TPR = NB * 4;  // threads per row: 8 columns each
+    uint4 res[RowMap<TPR, ROWS>::PASSES][2];
+    load_residual<TPR, ROWS>(a, m0, nb0, tile_rows, tid, res);
     __syncthreads();
-    finish_rows<16, ROWS, SM::STG_LD>(a, stg, part, m0, nb0, tile_rows, tid, res);
+    finish_rows<TPR, ROWS, SM::STG_LD>(a, stg, part, m0, nb0, tile_rows, tid, res);
 }
 
 // 128-row x 128-column tiles read through 128-row gather-plan records: one
@@ -1241,11 +1249,13 @@ __global__ void __launch_bounds__(NTH) gather_plan_build_kernel(const int32_t *k
 
 }  // namespace
 
-KernelFn pick_halo_bf16(int rows) {
+KernelFn pick_halo_bf16(int rows, int nb) {
+    if (nb == 3) return rows == 64 ? conv_halo_kernel<2, false, 3> : nullptr;
     return rows == 128 ? conv_halo_kernel<4, false> : rows == 64 ? conv_halo_kernel<2, false> : nullptr;
 }
 
-KernelFn pick_halo_bf16_planned(int rows) {
+KernelFn pick_halo_bf16_planned(int rows, int nb) {
+    if (nb == 3) return rows == 64 ? conv_halo_kernel<2, true, 3> : nullptr;
     return rows == 64 ? conv_halo_kernel<2, true> : rows == 128 ? conv_halo8_kernel : nullptr;
 }
 

@@ -67,16 +67,17 @@ KernelFn pick_mfma_f32(int id, int kc, bool xf);
 // 1x1-layer kernel for nbt 32-column blocks (1, 2, 3, 4, 6, 8), else nullptr.
 KernelFn pick_linear_bf16(int nbt);
 KernelFn pick_linear_f32(int nbt);
-// The halo-staged BF16 kernel for `rows`-row x 128-column tiles (tiling 20:
-// 128 rows, 21: 64 rows; 64-channel halo chunks; Cin a multiple of 64, Cout
-// padded to whole 128-column tiles, kvol 27, inputs and weights below
-// 2 GiB), else nullptr.
-KernelFn pick_halo_bf16(int rows);
+// The halo-staged BF16 kernel for `rows`-row x (nb * 32)-column tiles
+// (tiling 20: 128 rows, 21: 64 rows; nb 4, or 3 for 64-row tiles; 64-channel
+// halo chunks; Cin a multiple of 64, Cout padded to whole tiles, kvol 27,
+// inputs and weights below 2 GiB), else nullptr.
+KernelFn pick_halo_bf16(int rows, int nb = 4);
 // The halo kernels reading a precomputed gather plan (a.plan): 64-row tiles
-// (4 waves, two workgroups per CU) or 128-row tiles (8 waves, one workgroup
-// per CU, launched with kHalo8Threads threads); the plan builder (one
-// workgroup per tile of `rows` rows); a plan record's bytes.
-KernelFn pick_halo_bf16_planned(int rows);
+// (4 waves, two workgroups per CU; 128 or 96 columns) or 128-row tiles (8
+// waves, one workgroup per CU, launched with kHalo8Threads threads, 128
+// columns); the plan builder (one workgroup per tile of `rows` rows); a plan
+// record's bytes.
+KernelFn pick_halo_bf16_planned(int rows, int nb = 4);
 constexpr int kHalo8Threads = 512;
 void launch_gather_plan_build(int rows, const int32_t *kmap, int64_t n_out, int64_t n_src, int32_t row_shift,
                               void *plan, hipStream_t stream);

@@ -126,10 +126,15 @@ def test_conv_plan_names_the_launched_kernel(s3dx, monkeypatch):
     assert f64.plan(n, n).startswith("mfma tiling=12 split-k rows=128 cols=64 kc=64")
     # 96 bf16 channels: four 32-channel chunks make each 128-channel task.
     assert s3dx.SparseConv(96, 96, 27, s3dx.BF16).plan(n, n).startswith("mfma tiling=15 split-k rows=128 cols=96 kc=32")
-    # 192 output columns without LayerNorm: two 96-column split-K tiles; with
-    # more 128-row tiles than CUs (221 x 2) they become 64-row tiles, two per CU.
+    # 192 output columns without LayerNorm: two 96-column tiles of the
+    # 64-row halo kernel (the split-K kernels with S3DX_CONV_HALO=0: 64-row
+    # tiles, two per CU, as there are more 128-row tiles than CUs).
+    assert s3dx.SparseConv(192, 192, 27, s3dx.BF16).plan(n, n) == \
+        "mfma tiling=21 split-k halo rows=64 cols=96 kc=64 xf=0 ln=none grid=442x2"
+    monkeypatch.setenv("S3DX_CONV_HALO", "0")
     assert s3dx.SparseConv(192, 192, 27, s3dx.BF16).plan(n, n) == \
         "mfma tiling=19 split-k rows=64 cols=96 kc=64 xf=0 ln=none grid=442x2"
+    monkeypatch.delenv("S3DX_CONV_HALO")
     assert "cols=192" in s3dx.SparseConv(192, 192, 27, s3dx.BF16).set_layernorm(True, 1e-6).plan(n, n)
     # Cout not a multiple of 32: the generic kernel.
     assert s3dx.SparseConv(16, 40, 27, s3dx.F32).plan(100, 100) == "generic rows=64 cols=64 ln=none grid=2x1"

@@ -241,7 +241,7 @@ def test_config4_full_size(s3dx, O, W):
             .set_gather_parent(True, slot))
     plan = conv.plan(p, n)
     print(f"config 4 children={n}: {plan}", flush=True)
-    assert plan.startswith("pre=children mfma tiling=19 split-k rows=64 cols=96") and plan.endswith("grid=3534x2"), plan
+    assert plan.startswith("pre=children mfma tiling=21 split-k halo rows=64 cols=96") and plan.endswith("grid=3534x2"), plan
     xp = W.round_bf16(W.normal_f32(0, 400, (p, c)))
     y = _buf(s3dx, n, c, s3dx.BF16)
     conv.run(_dev(s3dx, W, xp, s3dx.BF16), p, s3dx.DeviceArray.from_host(kmap), n, y, s3dx.BF16)

@@ -149,6 +149,44 @@ def test_planned_config3_rows(s3dx, O, W):
     assert np.array_equal(y0.download(), y1.download())
 
 
+# Layers whose columns come in 96 but not 128 (the mesh decoder's 192 and 96
+# outputs) run 64-row, 96-column halo tiles: the three owning waves and the
+# fourth, which only hands its partials over.
+COLS96 = {
+    "shells_3000_cin192_cout192": (lambda W: W.shells_union(1)[:3000], 192, 192),
+    "shells_3000_cin64_cout96": (lambda W: W.shells_union(1)[:3000], 64, 96),
+    "shells_28265_cin128_cout192": (lambda W: W.shells_union(0), 128, 192),
+    "shuffled_cube_13824_cout96": (lambda W: _dense_cube(24, 0), 128, 96),          # every tile global
+    "half_shuffled_cube_13824_cout192": (lambda W: _dense_cube(24, 6912), 64, 192),  # both modes
+    "tiny_37_cout96": (lambda W: W.shells_union(2)[:37], 128, 96),
+}
+
+
+@pytest.mark.parametrize("case", list(COLS96))
+def test_96_column_tiles(s3dx, O, W, monkeypatch, case):
+    monkeypatch.delenv("S3DX_CONV_TILING", raising=False)
+    monkeypatch.delenv("S3DX_CONV_HALO", raising=False)
+    monkeypatch.delenv("S3DX_PLAN_ROWS", raising=False)
+    build, cin, cout = COLS96[case]
+    coords = build(W)
+    n = coords.shape[0]
+    kmap = O.kmap_subm3(coords, n)
+    conv = _layer(s3dx, W, cin, cout, 46, False)
+    x = W.round_bf16(W.normal_f32(46, 1, (n, cin)))
+    res = W.round_bf16(W.normal_f32(46, 4, (n, cout)))
+    xd, kd, rd = _bf(s3dx, W, x), s3dx.DeviceArray.from_host(kmap), _bf(s3dx, W, res)
+    gp = conv.gather_plan(n, kd, n)
+    plan_text, planned = conv.plan(n, n), conv.plan(n, n, gp)
+    print(f"{case} n={n}: {plan_text} | {planned}", flush=True)
+    assert plan_text.startswith("mfma tiling=21 split-k halo rows=64 cols=96"), plan_text
+    assert planned.endswith(f"grid={(n + 63) // 64}x{cout // 96} plan=64"), planned
+    y0, y1 = s3dx.DeviceArray((n, cout), np.uint16), s3dx.DeviceArray((n, cout), np.uint16)
+    conv.run(xd, n, kd, n, y0, s3dx.BF16, rd)
+    conv.run(xd, n, kd, n, y1, s3dx.BF16, rd, plan=gp)
+    assert np.array_equal(y0.download(), y1.download())
+    check_rel(_host(W, y1), _oracle(O, W, x, kmap, n, cin, cout, 46, False, res), 1e-2, case)
+
+
 @pytest.mark.parametrize("tiling", ["20", "21"])
 @pytest.mark.parametrize("shuffle_from", [None, 0, 6912])
 def test_halo_tilings_on_dense_and_shuffled_rows(s3dx, O, W, monkeypatch, tiling, shuffle_from):
