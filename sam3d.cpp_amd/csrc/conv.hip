@@ -561,6 +561,13 @@ LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bo
                         p = wide;
                     }
                     p = best;
+                    // FP32 32-column tiles: 32-row tiles (tiling 24) put several
+                    // waves on each SIMD instead of one wave running every
+                    // MFMA of a 128-row tile alone (the 64-channel sphere
+                    // shell: 33.9 -> 24.7 us).
+                    if (!bf && p.nb == 1 && tiling_kernel(24, bf, p.kc, p.xf))
+                        for (const Tiling &t : kTilings)
+                            if (t.id == 24) p.tl = &t;
                 }
             }
         }
@@ -924,14 +931,15 @@ void describe_launch(const s3dx_conv *conv, const s3dx_gather_plan *gplan, int64
         const bool planned = gplan && (p.fn == pick_halo_bf16_planned(64) || p.fn == pick_halo_bf16_planned(128) ||
                                        p.fn == pick_halo_bf16_planned(64, 3));
         char text[256];
+        const bool halo = p.mfma && !p.linear && p.tl->id >= 20 && p.tl->id <= 22;  // the halo-staged kernels
         if (p.linear)
             std::snprintf(text, sizeof(text), "linear cols=%d ksteps=%d%s ln=%s grid=%u", p.nb * 32,
                           conv->cin / (conv->dtype == S3DX_BF16 || p.split ? 16 : 8),
                           p.split ? " terms=3" : "", conv->ln ? "separate" : "none", p.grid.x);
         else if (p.mfma)
             std::snprintf(text, sizeof(text), "mfma tiling=%d%s%s rows=%d cols=%d kc=%d xf=%d ln=%s grid=%ux%u",
-                          p.tl->id, p.tl->splitk ? " split-k" : "", p.tl->id >= 20 ? " halo" : "", p.tl->rows(),
-                          p.tl->id >= 20 ? p.nb * 32 : p.tl->cols(), p.kc,
+                          p.tl->id, p.tl->splitk ? " split-k" : "", halo ? " halo" : "", p.tl->rows(),
+                          halo ? p.nb * 32 : p.tl->cols(), p.kc,
                           p.xf ? 1 : 0, conv->ln ? (p.fused_ln ? "fused" : "separate") : "none", p.grid.x,
                           p.grid.y);
         else

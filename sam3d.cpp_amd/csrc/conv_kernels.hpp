@@ -58,6 +58,7 @@ inline constexpr Tiling kTilings[] = {
     {10, 1, 4, 1, 0}, {11, 4, 4, 1, 1}, {12, 4, 2, 1, 1}, {13, 4, 3, 1, 1}, {14, 4, 1, 1, 1},
     {15, 4, 3, 1, 1}, {16, 4, 4, 1, 1}, {17, 2, 4, 1, 1}, {18, 2, 4, 1, 1},
     {19, 2, 3, 1, 1}, {20, 4, 4, 1, 1}, {21, 2, 4, 1, 1}, {22, 4, 4, 1, 1},
+    {23, 2, 1, 1, 1}, {24, 1, 1, 1, 1},
 };
 
 // MFMA kernel for tiling `id`, kc channels per task, xf 64-bit gathers;
@@ -1227,12 +1228,13 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_splitk_kernel(ConvA
     // so results are deterministic.  Accumulators are only indexed by
     // compile-time constants.
     constexpr int PPW = (RPH * NB + 3) / 4;  // pairs per wave per phase
+    constexpr int NPH = MB / RPH;            // phases (one for 32-row tiles)
     auto slot_of = [&](int h, int c, int writer) __attribute__((always_inline)) {
         return red + ((h * NB + c) * 4 + writer) * (4 * 64);
     };
-    float fin[2][PPW][16];
+    float fin[NPH][PPW][16];
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
+    for (int p = 0; p < NPH; ++p) {
         if (p) __syncthreads();
 #pragma unroll
         for (int h = 0; h < RPH; ++h)
@@ -1296,7 +1298,7 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_splitk_kernel(ConvA
     __syncthreads();
     // Summed blocks -> FP32 tile in LDS (the tile aliases the slots).
 #pragma unroll
-    for (int p = 0; p < 2; ++p)
+    for (int p = 0; p < NPH; ++p)
 #pragma unroll
         for (int i = 0; i < PPW; ++i) {
             const int q = wave + 4 * i;
@@ -1645,6 +1647,13 @@ KernelFn pick_tiling(int id) {
     case 19: {  // 15 with 64-row tiles, two workgroups per CU (16's 128 columns would spill)
         if constexpr (sizeof(T) == 2 && XF == 0 && (KC == 32 || KC == 64))
             return conv_splitk_kernel<T, 3, 128, XF, 128 / KC, 2>;
+        else
+            return nullptr;
+    }
+    case 23: case 24: {  // FP32 32-column tiles of 64 (23) or 32 (24) rows, for small sets
+        constexpr int KS = KC / (2 * Frag<T>::E);
+        if constexpr (sizeof(T) == 4 && XF == 0 && KS % 4 == 0)
+            return id == 23 ? conv_splitk_kernel<T, 1, KC, XF, 1, 2> : conv_splitk_kernel<T, 1, KC, XF, 1, 1>;
         else
             return nullptr;
     }

@@ -124,6 +124,9 @@ def test_conv_plan_names_the_launched_kernel(s3dx, monkeypatch):
     assert "halo" not in s3dx.SparseConv(128, 128, 27, s3dx.F32).plan(n, n)
     f64 = s3dx.SparseConv(64, 64, 27, s3dx.F32)
     assert f64.plan(n, n).startswith("mfma tiling=12 split-k rows=128 cols=64 kc=64")
+    # The 10,366-voxel sphere shell: 81 x 2 tiles of 128 x 32 would leave CUs
+    # idle; FP32 32-column tiles then take 32 rows each.
+    assert f64.plan(10366, 10366) == "mfma tiling=24 split-k rows=32 cols=32 kc=64 xf=0 ln=none grid=324x2"
     # 96 bf16 channels: four 32-channel chunks make each 128-channel task.
     assert s3dx.SparseConv(96, 96, 27, s3dx.BF16).plan(n, n).startswith("mfma tiling=15 split-k rows=128 cols=96 kc=32")
     # 192 output columns without LayerNorm: two 96-column tiles of the
