@@ -1323,6 +1323,7 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_splitk_kernel(ConvA
 //   15, 16: split-K, 128 rows x 96 / 128 columns, 128-channel tasks joined
 //           from 32- or 64-channel chunks; 19: 15 with 64 rows
 //   17, 18: split-K, 64 rows x 128 columns, 128- / 64-channel tasks
+//   23, 24: split-K, FP32, 64 / 32 rows x 32 columns
 // 1x1 layers (kvol 1, no map): y[r] = W x[r >> row_shift] + bias, then SiLU
 // and the residual.  Persistent workgroups: the packed weights (every k-step
 // of all NBT column blocks) are copied to LDS once; each wave then takes
