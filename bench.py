@@ -257,6 +257,21 @@ def extras(s3dx, W, stream, seed):
     y = s3dx.DeviceArray((n4, 192), np.uint16)
     conv_entry("config4_bf16_conv_192_children", conv, x, n2, k4, n4, y, bf, p4, 192, 192, PEAK_BF16_TFLOPS)
 
+    # Kernel maps (mesh sentinel -1) over the mesh decoder's child sets at
+    # 128^3 and 256^3: outside the 64^3 window, so every voxel takes the
+    # hashed path.  Algorithmic bytes: 16 B coordinates in + 108 B map out.
+    ch1, _ = s3dx.subdivide2(ch, n4, False, stream)
+    for name, cset, cn in (("kmap_subm3_mesh_children_128", ch, n4),
+                           ("kmap_subm3_mesh_children_256", ch1, 8 * n4)):
+        km = s3dx.DeviceArray((cn, 27), np.int32)
+        kw = s3dx.DeviceArray(s3dx.kmap_workspace_size(cn), np.uint8)
+        us = _event_us(s3dx, stream, lambda: s3dx.kmap_subm3(cset, cn, -1, km, kw, stream))
+        gbs = cn * KMAP_BYTES_PER_VOXEL / us / 1e3
+        out[name] = {"us": us, "voxels": cn, "mvox_s": cn / us, "gb_s": gbs, "peak_gb_s": PEAK_HBM_GBS,
+                     "frac": gbs / PEAK_HBM_GBS}
+        del km, kw
+    del ch1
+
     # config 5: 768-channel parents -> upsample block (768 -> 192) -> upsample
     # block (192 -> 96) -> linear 96 -> 101 (FP32), the mesh decoder's sparse stack
     out["config5_stack"] = mesh_stack(s3dx, W, stream, seed, d2, n2, ch, k4)

@@ -106,9 +106,12 @@ S3DX_API s3dx_status s3dx_kmap_workspace_size(int64_t n, uint64_t *bytes, char *
  * missing_value; rows of later duplicates of a coordinate stay entirely
  * missing_value (sparse_ops.cpp:120-141).  Byte-identical to the reference.
  * Requires 0 < n <= INT32_MAX / 27.  Asynchronous on `stream`, two
- * launches.  The workspace's contents on entry do not matter and need no
- * clearing: every build tags the words it writes with a fresh per-call tag,
- * so one workspace serves any sequence of builds on one stream. */
+ * launches.  The workspace needs no clearing: every build tags the words it
+ * writes with a fresh per-call tag, and a word is used only when its row's
+ * input coordinates are the ones looked up, so the map is byte-identical to
+ * the reference whatever the workspace holds on entry (zeros, an earlier
+ * build's table, or arbitrary bytes); one workspace serves any sequence of
+ * builds on one stream. */
 S3DX_API s3dx_status s3dx_kmap_subm3(const int32_t *coords, int64_t n, int32_t missing_value,
                                      int32_t *kmap, void *workspace, uint64_t workspace_bytes,
                                      s3dx_stream stream, char *error, uint64_t error_capacity);
@@ -119,8 +122,9 @@ S3DX_API s3dx_status s3dx_kmap_subm3(const int32_t *coords, int64_t n, int32_t m
  * hipMalloc.  The table lives in a static device array of the library
  * (18 MiB + 256 bytes on each GPU it runs on, held until the process ends),
  * so n is limited to 262144 voxels (S3DX_INVALID_ARGUMENT above that).  Same
- * kernels and results as s3dx_kmap_subm3 (per-call tags, no clearing
- * pass).  All calls on one GPU share that array:
+ * kernels and results as s3dx_kmap_subm3 (per-call tags, rows checked
+ * against the input coordinates, no clearing pass: the array starts zeroed
+ * and keeps the last call's table).  All calls on one GPU share that array:
  * calls that overlap in time on one GPU (different streams, threads) race
  * and must be serialized by the caller. */
 S3DX_API s3dx_status s3dx_kmap_subm3_static(const int32_t *coords, int64_t n, int32_t missing_value,

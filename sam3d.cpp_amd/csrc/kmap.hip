@@ -36,11 +36,19 @@ namespace {
 // tag_of(seed, index), and every build draws a new seed: tag_of is a
 // bijection of seed ^ f(index), so nothing written by another build carries
 // the current tag, and the table needs no clearing pass between builds.
-// Memory that never held the table (a fresh workspace) reads as empty except
-// with probability 2^-32 per word; such a hash slot must still match the
-// packed 64-bit key (or, wide, the input row's coordinates) before a lookup
-// returns its row, and a window cell's row is checked against the input
-// rows' coordinates on insert.
+// Memory that never held the table (a zero-filled or fresh workspace) can
+// carry the current tag by chance: mix32(0) == 0, so for every seed exactly
+// one index of a zero-filled table does, and random bytes do at 2^-32 per
+// word.  So no row is ever taken on its tag alone: the insert and the
+// lookup both return (or keep) a word's row r only when r < n and the input
+// row r has the queried coordinates.  A chance word whose row names other
+// coordinates reads as a foreign word (the insert claims it, the lookup
+// moves on or reports a miss); one whose row has the queried coordinates is
+// a row of that key, and the insert's atomicMin still leaves the key's
+// smallest row.  The maps are therefore exact whatever the table holds on
+// entry; the flag words alone are taken on their value, and a raised flag
+// that decides an error (subdivide's duplicate test) is confirmed by an
+// exact pass before it is reported.
 constexpr int kWindow = 64;                                 // cells per axis
 constexpr int64_t kWindowCells = int64_t(kWindow) * kWindow * kWindow;
 
@@ -52,7 +60,8 @@ struct KmapHash {
     uint32_t seed;
 };
 
-constexpr int kFlagWide = 2;  // some hashed coordinate does not fit int16
+constexpr int kFlagWide = 2;     // some hashed coordinate does not fit int16
+constexpr int kConfirmWord = 8;  // two counters of the exact recount behind a raised flag
 
 __device__ __host__ __forceinline__ uint32_t mix32(uint32_t h) {
     h ^= h >> 16;
@@ -107,13 +116,18 @@ __device__ __forceinline__ void kmap_hash_insert(const int4 *__restrict__ keys, 
             }
             cur = prev;  // claimed meanwhile, by a row of this build
         }
-        // The slot's row is of this build (or a stale word's chance match,
-        // whose row fails the comparison): compare coordinates through the
-        // input, since its packed key may not be written yet.
+        // The slot's row is of this build (or a chance match of a word that
+        // never held this build's table): compare coordinates through the
+        // input, since its packed key may not be written yet.  A chance
+        // word whose row has this key acts as the key's slot: lower its row
+        // and write the packed key it may lack.
         const uint32_t r = static_cast<uint32_t>(cur);
         if (r < static_cast<uint32_t>(n) && same_key(keys[r], c)) {
             atomicMin(word, mine);
-            h.flags[kFlagDuplicate] = flag_of(h.seed, kFlagDuplicate);
+            if (fits)
+                atomicExch(reinterpret_cast<unsigned long long *>(&h.slots[pos]),
+                           static_cast<unsigned long long>(pack16(c)));
+            if (r != static_cast<uint32_t>(i)) h.flags[kFlagDuplicate] = flag_of(h.seed, kFlagDuplicate);
             return;
         }
         pos = (pos + 1) & h.mask;
@@ -143,7 +157,7 @@ kmap_insert_kernel(const int4 *__restrict__ keys, int32_t n, KmapHash h) {
         const uint32_t r = static_cast<uint32_t>(cur);
         if (static_cast<uint32_t>(cur >> 32) == tag && r < static_cast<uint32_t>(n) && same_key(keys[r], c)) {
             atomicMin(word, mine);
-            h.flags[kFlagDuplicate] = flag_of(h.seed, kFlagDuplicate);
+            if (r != static_cast<uint32_t>(i)) h.flags[kFlagDuplicate] = flag_of(h.seed, kFlagDuplicate);
             return;
         }
         const unsigned long long prev = atomicCAS(word, cur, mine);
@@ -161,9 +175,11 @@ __device__ __forceinline__ int32_t kmap_hash_find(const KmapHash &h, const int4 
     for (uint32_t probe = 0; probe <= h.mask; ++probe) {
         const uint4 s = h.slots[pos];
         if (s.w != tag_of(h.seed, pos)) return -1;
-        const bool hit = wide ? s.z < static_cast<uint32_t>(n) && same_key(keys[s.z], q)
-                              : ((static_cast<uint64_t>(s.y) << 32) | s.x) == kq;
-        if (hit) return static_cast<int32_t>(s.z);
+        // The packed key (when every key fits) screens the probe chain; the
+        // row is returned only after its input coordinates match.
+        if ((wide || ((static_cast<uint64_t>(s.y) << 32) | s.x) == kq) && s.z < static_cast<uint32_t>(n) &&
+            same_key(keys[s.z], q))
+            return static_cast<int32_t>(s.z);
         pos = (pos + 1) & h.mask;
     }
     return -1;
@@ -175,8 +191,10 @@ __device__ __forceinline__ int32_t kmap_find(const KmapHash &h, const int4 *__re
     const int32_t cell = window_cell(q);
     if (cell < 0) return kmap_hash_find(h, keys, n, q, wide);
     const unsigned long long v = h.cells[cell];
-    return static_cast<uint32_t>(v >> 32) == tag_of(h.seed, static_cast<uint32_t>(cell))
-               ? static_cast<int32_t>(static_cast<uint32_t>(v))
+    const uint32_t r = static_cast<uint32_t>(v);
+    return static_cast<uint32_t>(v >> 32) == tag_of(h.seed, static_cast<uint32_t>(cell)) &&
+                   r < static_cast<uint32_t>(n) && same_key(keys[r], q)
+               ? static_cast<int32_t>(r)
                : -1;
 }
 
@@ -275,10 +293,29 @@ void kmap_layout(W &w, int64_t n, KmapHash *h) {
 }
 
 // A new seed for every build in the process (never repeated before 2^32
-// builds), so slots of earlier builds read as empty.
+// builds), so slots of earlier builds read as empty.  Seeds whose flag value
+// of some flag word is 0 are skipped (three of 2^32), so a zero-filled
+// table never reads as a raised flag.
+std::atomic<uint32_t> g_seed_counter{0x3C6EF372u};
 uint32_t next_seed() {
-    static std::atomic<uint32_t> counter{0x3C6EF372u};
-    return counter.fetch_add(1, std::memory_order_relaxed);
+    for (;;) {
+        const uint32_t s = g_seed_counter.fetch_add(1, std::memory_order_relaxed);
+        if (flag_of(s, kFlagDuplicate) != 0 && flag_of(s, kFlagOverflow) != 0 && flag_of(s, kFlagWide) != 0)
+            return s;
+    }
+}
+
+// Exact recount behind a raised flag (subdivide only, which reports it):
+// counts[0] = rows whose key the table lost (an exhausted probe sequence),
+// counts[1] = rows that are not the first row of their key.
+__global__ void __launch_bounds__(kThreads)
+kmap_confirm_kernel(const int4 *__restrict__ keys, int32_t n, KmapHash h, uint32_t *__restrict__ counts) {
+    const int32_t i = blockIdx.x * kThreads + threadIdx.x;
+    if (i >= n) return;
+    const bool wide = h.flags[kFlagWide] == flag_of(h.seed, kFlagWide);
+    const int32_t r = kmap_find(h, keys, n, keys[i], wide);
+    if (r < 0) atomicAdd(&counts[0], 1u);
+    else if (r != i) atomicAdd(&counts[1], 1u);
 }
 
 // Insert + lookup (two launches, no clearing pass), leaving the flags of
@@ -436,11 +473,39 @@ S3DX_API s3dx_status s3dx_subdivide2(const int32_t *parent_coords, int64_t paren
         hip_check(hipMemcpyAsync(flags, l.hash.flags, sizeof(flags), hipMemcpyDeviceToHost, s),
                   "hipMemcpyAsync flags");
         hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
-        require(flags[kFlagDuplicate] != flag_of(l.hash.seed, kFlagDuplicate), "duplicate parent coordinates");
-        if (flags[kFlagOverflow] == flag_of(l.hash.seed, kFlagOverflow))
-            throw std::runtime_error("hash table overflow");
+        if (flags[kFlagDuplicate] == flag_of(l.hash.seed, kFlagDuplicate) ||
+            flags[kFlagOverflow] == flag_of(l.hash.seed, kFlagOverflow)) {
+            // A raised flag word may be a chance value of a workspace that
+            // never held this build's table: recount exactly before failing.
+            uint32_t *counts = reinterpret_cast<uint32_t *>(l.hash.flags + kConfirmWord);
+            hip_check(hipMemsetAsync(counts, 0, 2 * sizeof(uint32_t), s), "hipMemsetAsync counts");
+            kmap_confirm_kernel<<<blocks_for(p), kThreads, 0, s>>>(reinterpret_cast<const int4 *>(parent_coords), p,
+                                                                   l.hash, counts);
+            launch_check("kmap_confirm");
+            uint32_t c[2] = {0, 0};
+            hip_check(hipMemcpyAsync(c, counts, sizeof(c), hipMemcpyDeviceToHost, s), "hipMemcpyAsync counts");
+            hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
+            require(c[1] == 0, "duplicate parent coordinates");
+            if (c[0] != 0) throw std::runtime_error("hash table overflow");
+        }
     });
 }
 
+/* Test-only hooks, exported for the test suite and absent from the public
+ * header: the seed of the next kernel-map build in this process (so a test
+ * can replay a build whose tags collide with a zero-filled table), and a
+ * clearing of the allocation-free entry point's static table on the current
+ * device (so a test can start it from zeros as a fresh process does). */
+S3DX_API s3dx_status s3dx_testing_set_kmap_seed(uint32_t seed, char *error, uint64_t error_capacity) {
+    return boundary(error, error_capacity, [&] { g_seed_counter.store(seed, std::memory_order_relaxed); });
+}
+
+S3DX_API s3dx_status s3dx_testing_zero_static_kmap(s3dx_stream stream, char *error, uint64_t error_capacity) {
+    return boundary(error, error_capacity, [&] {
+        const hipStream_t s = as_stream(stream);
+        hip_check(hipMemsetAsync(static_scratch(), 0, kStaticKmapBytes, s), "hipMemsetAsync scratch");
+        hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
+    });
+}
 
 }  // extern "C"

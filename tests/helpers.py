@@ -121,3 +121,63 @@ def gguf_bytes(kv, tensors, align=32):
         off += len(blob) + pad
     out += b"\0" * ((-len(out)) % align)
     return out + b"".join(blobs)
+
+
+# ---- test-only hooks of libs3dx_sparse.so (exported, not in the public header)
+
+def _mix32(h):
+    m = 0xFFFFFFFF
+    h ^= h >> 16
+    h = (h * 0x7FEB352D) & m
+    h ^= h >> 15
+    h = (h * 0x846CA68B) & m
+    h ^= h >> 16
+    return h
+
+
+def window_cell_index(x, y, z):
+    """Index of batch-0 cell (x, y, z) in the kernel-map table's 64^3 window."""
+    return (x * 64 + y) * 64 + z
+
+
+def colliding_seed(cell_index):
+    """The kernel-map seed whose tag for this window cell is 0: the tag is
+    mix32(seed ^ cell * 0x9E3779B1), mix32 is a bijection with mix32(0) == 0,
+    so a zero-filled word carries the current tag exactly for this seed."""
+    seed = (cell_index * 0x9E3779B1) & 0xFFFFFFFF
+    assert _mix32(seed ^ ((cell_index * 0x9E3779B1) & 0xFFFFFFFF)) == 0
+    return seed
+
+
+def flag_value(seed, k):
+    """The value flag word k holds when raised by the build with this seed."""
+    v = _mix32((seed + 0x632BE5AB * (k + 1)) & 0xFFFFFFFF)
+    return v - (1 << 32) if v >= 1 << 31 else v
+
+
+def kmap_flags_offset(n):
+    """Byte offset of the flag words in a kernel-map workspace for n voxels:
+    the 64^3 window of 8-byte cells, then the 16-byte slots (power of two,
+    >= 4n, >= 256), each region rounded up to 256 bytes."""
+    cap = 256
+    while cap < 4 * n:
+        cap <<= 1
+    return 64 ** 3 * 8 + cap * 16
+
+
+def set_kmap_seed(s3dx, seed):
+    import ctypes as C
+    fn = s3dx.lib().s3dx_testing_set_kmap_seed
+    fn.restype = C.c_uint32
+    fn.argtypes = [C.c_uint32, C.c_char_p, C.c_uint64]
+    buf = C.create_string_buffer(256)
+    assert fn(seed, buf, len(buf)) == 0, buf.value
+
+
+def zero_static_kmap(s3dx):
+    import ctypes as C
+    fn = s3dx.lib().s3dx_testing_zero_static_kmap
+    fn.restype = C.c_uint32
+    fn.argtypes = [C.c_void_p, C.c_char_p, C.c_uint64]
+    buf = C.create_string_buffer(256)
+    assert fn(None, buf, len(buf)) == 0, buf.value

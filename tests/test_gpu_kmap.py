@@ -3,7 +3,8 @@ the oracle and to the reference golden tables."""
 import numpy as np
 import pytest
 
-from helpers import SMALL, large_sets, sha
+from helpers import (SMALL, colliding_seed, flag_value, kmap_flags_offset, large_sets, set_kmap_seed, sha,
+                     window_cell_index)
 
 pytestmark = pytest.mark.gpu
 
@@ -186,3 +187,68 @@ def test_workspace_reuse_and_garbage(s3dx, O, W):
             print(f"kmap reuse garbage={garbage} {name} n={n}", flush=True)
             got = s3dx.kmap_subm3(s3dx.DeviceArray.from_host(c), n, -1, workspace=ws).download()
             assert np.array_equal(got, O.kmap_subm3(c, -1)), name
+
+
+def _zeroed(s3dx, nbytes):
+    ws = s3dx.DeviceArray(nbytes, np.uint8)
+    ws.upload(np.zeros(nbytes, np.uint8))
+    return ws
+
+
+def test_zero_filled_table_tag_collision(s3dx, W, golden):
+    # Window cell (0,27,22,46) is empty in config 2 (seed 0) but is the
+    # neighbour of three voxels.  Under the build seed whose tag for that
+    # cell is 0 (the 59,357th build of a process), a zero-filled table
+    # carries the current tag there, and a lookup that trusted the tag would
+    # return row 0 for those voxels.  The map must stay byte-identical to the
+    # reference's (golden SHA), for the SLat sentinel and for subdivide.
+    arrays, manifest = golden
+    coords = W.shells_union(0)
+    n = coords.shape[0]
+    cell = (27, 22, 46)
+    rows = {tuple(r): i for i, r in enumerate(coords[:, 1:].tolist())}
+    assert cell not in rows
+    near = [(rows[(cell[0] - dx, cell[1] - dy, cell[2] - dz)], (dx + 1) * 9 + (dy + 1) * 3 + (dz + 1))
+            for dx in (-1, 0, 1) for dy in (-1, 0, 1) for dz in (-1, 0, 1)
+            if (cell[0] - dx, cell[1] - dy, cell[2] - dz) in rows]
+    assert len(near) == 3
+    seed = colliding_seed(window_cell_index(*cell))
+    assert seed == 0x3C6EF372 + 59356
+    dc = s3dx.DeviceArray.from_host(coords)
+    print(f"kmap zero-filled workspace, seed {seed:#x}, n={n}", flush=True)
+    set_kmap_seed(s3dx, seed)
+    got = s3dx.kmap_subm3(dc, n, n, workspace=_zeroed(s3dx, s3dx.kmap_workspace_size(n))).download()
+    assert all(got[i, o] == n for i, o in near), [(i, o, got[i, o]) for i, o in near]
+    assert sha(got) == manifest["shells_union_s0"]["conv_fine_sha256"]
+    print("subdivide zero-filled workspace, same seed", flush=True)
+    set_kmap_seed(s3dx, seed)
+    child, kmap = s3dx.subdivide2(dc, n, True, workspace=_zeroed(s3dx, s3dx.subdivide2_workspace_size(n)))
+    sub = manifest["shells_union_s0"]["subdivide"]
+    assert sha(child.download()) == sub["child_coords_sha256"]
+    assert sha(kmap.download()) == sub["neighbors_sha256"]
+
+
+def test_subdivide_confirms_chance_flags(s3dx, W):
+    # A workspace whose flag words hold, by chance, the values this build
+    # raises them to (duplicate, overflow) on a duplicate-free set: the
+    # exact recount behind a raised flag must clear it, and a set with a
+    # real duplicate must still be rejected.
+    parents = np.ascontiguousarray(W.shells_union(1)[:5000])
+    n = parents.shape[0]
+    seed = 0x51ED270B
+    nbytes = s3dx.subdivide2_workspace_size(n)
+    host = np.zeros(nbytes, np.uint8)
+    off = kmap_flags_offset(n)
+    host[off:off + 8] = np.array([flag_value(seed, 0), flag_value(seed, 1)], np.int32).view(np.uint8)
+    ws = s3dx.DeviceArray(nbytes, np.uint8)
+    ws.upload(host)
+    dc = s3dx.DeviceArray.from_host(parents)
+    print(f"subdivide with planted flag words, n={n}", flush=True)
+    set_kmap_seed(s3dx, seed)
+    child, kmap = s3dx.subdivide2(dc, n, True, workspace=ws)
+    child2, kmap2 = s3dx.subdivide2(dc, n, True)
+    assert np.array_equal(child.download(), child2.download())
+    assert np.array_equal(kmap.download(), kmap2.download())
+    dup = np.ascontiguousarray(np.concatenate([parents, parents[17:18]]))
+    with pytest.raises(s3dx.S3dxError, match="duplicate"):
+        s3dx.subdivide2(s3dx.DeviceArray.from_host(dup), n + 1)
