@@ -275,7 +275,142 @@ def extras(s3dx, W, stream, seed):
     # config 5: 768-channel parents -> upsample block (768 -> 192) -> upsample
     # block (192 -> 96) -> linear 96 -> 101 (FP32), the mesh decoder's sparse stack
     out["config5_stack"] = mesh_stack(s3dx, W, stream, seed, d2, n2, ch, k4)
+    # one SLat flow forward's sparse stages, BF16 and FP32
+    out["slat_forward_bf16"] = slat_forward(s3dx, W, stream, seed, s3dx.BF16)
+    out["slat_forward_fp32"] = slat_forward(s3dx, W, stream, seed, s3dx.F32, reps=3)
     return out
+
+
+def slat_forward(s3dx, W, stream, seed, dtype, reps=5):
+    """One SLat flow forward's sparse stages at config-2 shapes (28,265 fine /
+    5,086 coarse voxels), slat_flow_graph.cpp:284-291 and 441-503, each op
+    timed by HIP events around it: input_blocks.0 (128 -> 128), 2x mean-pool,
+    input_blocks.1 (128 -> 1024, Linear skip), concat skip1 + upsample,
+    out_blocks.0 (2048 -> 128), concat skip0, out_blocks.1 (256 -> 128).  Each
+    block: LayerNorm(affine) + SiLU pass, conv1 (+ LayerNorm + modulate +
+    SiLU), Linear skip, conv2 (+ skip).  Convs run with the fine or coarse
+    map's gather plan (built once per sample, timed apart).  The reference
+    runs 38 such forwards per sample (session.cpp:1689-1763)."""
+    bf = dtype == s3dx.BF16
+    store = np.uint16 if bf else np.float32
+    es = 2 if bf else 4
+    peak = PEAK_BF16_TFLOPS if bf else PEAK_FP32_TFLOPS
+    coords = W.shells_union(seed)
+    t = s3dx.SlatTables()
+    t.build(coords, stream)
+    nf, nc = t.nf, t.nc
+    pf = W.kmap_pairs(t.conv_fine.download(stream), nf)
+    pc = W.kmap_pairs(t.conv_coarse.download(stream)[:nc], nc)
+
+    def dev(a):
+        a = np.ascontiguousarray(a, np.float32)
+        return s3dx.DeviceArray.from_host(W.f32_to_bf16_bits(a) if bf else a, stream)
+
+    blocks = []
+    for b, (cin, cout, coarse) in enumerate(((128, 128, False), (128, 1024, True), (2048, 128, False),
+                                             (256, 128, False))):
+        k = 700 + 20 * b
+        blk = {"cin": cin, "cout": cout, "coarse": coarse,
+               "n1w": s3dx.DeviceArray.from_host(W.normal_f32(seed, k, (cin,), 0.2) + 1.0, stream),
+               "n1b": s3dx.DeviceArray.from_host(W.normal_f32(seed, k + 1, (cin,), 0.2), stream),
+               "ms": s3dx.DeviceArray.from_host(W.normal_f32(seed, k + 2, (cout,), 0.3), stream),
+               "mh": s3dx.DeviceArray.from_host(W.normal_f32(seed, k + 9, (cout,), 0.3), stream)}
+        blk["conv1"] = (s3dx.SparseConv(cin, cout, 27, dtype)
+                        .set_weights(W.conv_weight(seed, k + 3, cin, cout), s3dx.WEIGHT_SLAT,
+                                     W.normal_f32(seed, k + 4, (cout,), 0.1))
+                        .set_layernorm(True, 1e-6).set_silu(True))
+        blk["conv1"].set_modulate(blk["ms"], blk["mh"])
+        blk["conv2"] = s3dx.SparseConv(cout, cout, 27, dtype).set_weights(
+            W.conv_weight(seed, k + 5, cout, cout), s3dx.WEIGHT_SLAT, W.normal_f32(seed, k + 6, (cout,), 0.1))
+        blk["skip"] = (s3dx.SparseConv(cin, cout, 1, dtype).set_weights(
+            W.conv_weight(seed, k + 7, cin, cout, kvol=1), s3dx.WEIGHT_SLAT, W.normal_f32(seed, k + 8, (cout,), 0.1))
+            if cin != cout else None)
+        blocks.append(blk)
+    plan_f = blocks[0]["conv1"].gather_plan(nf, t.conv_fine, nf, stream)
+    plan_c = blocks[1]["conv2"].gather_plan(nc, t.conv_coarse, nc, stream)
+    plan_us = {"fine": _event_us(s3dx, stream, lambda: plan_f.rebuild(blocks[0]["conv1"], nf, t.conv_fine, nf, stream)),
+               "coarse": _event_us(s3dx, stream,
+                                   lambda: plan_c.rebuild(blocks[1]["conv2"], nc, t.conv_coarse, nc, stream))}
+    h0 = dev(W.normal_f32(seed, 790, (nf, 128)))
+    trunk = dev(W.normal_f32(seed, 791, (nc, 1024)))
+    buf = lambda rows, c: s3dx.DeviceArray((rows, c), store)  # noqa: E731
+    skip0, xc, skip1 = buf(nf, 128), buf(nc, 128), buf(nc, 1024)
+    xcat, h1, out = buf(nf, 2048), buf(nf, 128), buf(nf, 128)
+    tmp_h, tmp_y1, tmp_s = buf(nf, 2048), buf(nf, 1024), buf(nf, 1024)
+    ops = []  # (stage, op, fn, flops, bytes)
+
+    def block_ops(stage, blk, x, y):
+        n = nc if blk["coarse"] else nf
+        kmap = t.conv_coarse if blk["coarse"] else t.conv_fine
+        plan = plan_c if blk["coarse"] else plan_f
+        pairs = pc if blk["coarse"] else pf
+        cin, cout = blk["cin"], blk["cout"]
+        h, y1, sk = tmp_h, tmp_y1, tmp_s
+        ops.append((stage, "layernorm_silu", lambda: s3dx.layernorm_rows(
+            x, dtype, n, cin, 1e-6, blk["n1w"], blk["n1b"], silu=True, y=h, y_dtype=dtype, stream=stream),
+            0.0, 2.0 * n * cin * es))
+        ops.append((stage, f"conv1_{cin}_{cout}", lambda: blk["conv1"].run(
+            h, n, kmap, n, y1, dtype, None, stream, plan=plan), 2.0 * cin * cout * pairs, None))
+        res = x
+        if blk["skip"] is not None:
+            ops.append((stage, f"skip_{cin}_{cout}", lambda: blk["skip"].run(x, n, None, n, sk, dtype, None, stream),
+                        2.0 * cin * cout * n, None))
+            res = sk
+        ops.append((stage, f"conv2_{cout}_{cout}", lambda: blk["conv2"].run(
+            y1, n, kmap, n, y, dtype, res, stream, plan=plan), 2.0 * cout * cout * pairs, None))
+
+    block_ops("input_blocks.0", blocks[0], h0, skip0)
+    ops.append(("input_blocks.1", "downsample_mean", lambda: s3dx.downsample_mean(
+        skip0, dtype, nf, 128, t.coarse_children, t.coarse_inv_count, nc, xc, stream), 0.0,
+        (nf * 128 + nc * 128) * es + nc * 36))
+    block_ops("input_blocks.1", blocks[1], xc, skip1)
+    ops.append(("out_blocks.0", "concat_upsample", lambda: s3dx.concat_rows(
+        trunk, 1024, skip1, 1024, dtype, nc, t.fine_to_coarse, nf, xcat, stream), 0.0,
+        (2 * nc * 1024 + nf * 2048) * es + nf * 4))
+    block_ops("out_blocks.0", blocks[2], xcat, h1)
+    ops.append(("out_blocks.1", "concat", lambda: s3dx.concat_rows(
+        h1, 128, skip0, 128, dtype, nf, None, nf, xcat, stream), 0.0, 2 * nf * 256 * es))
+    block_ops("out_blocks.1", blocks[3], xcat, out)
+
+    def forward(ev=None):
+        for i, (_, _, fn, _, _) in enumerate(ops):
+            if ev:
+                ev[i].record(stream)
+            fn()
+        if ev:
+            ev[len(ops)].record(stream)
+
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < 0.1:
+        forward()
+        stream.synchronize()
+    times = [[] for _ in ops]
+    for _ in range(reps):
+        ev = [s3dx.Event(timing=True) for _ in range(len(ops) + 1)]
+        forward(ev)
+        stream.synchronize()
+        for i in range(len(ops)):
+            times[i].append(ev[i].elapsed_ms(ev[i + 1]) * 1e3)
+    stages, total, total_flops = {}, 0.0, 0.0
+    for (stage, op, _, fl, nbytes), tt in zip(ops, times):
+        us = statistics.median(tt)
+        e = {"us": us}
+        if fl:
+            e.update(tflops=fl / us / 1e6, frac=fl / us / 1e6 / peak)
+        else:
+            e.update(gb_s=nbytes / us / 1e3, frac=nbytes / us / 1e3 / PEAK_HBM_GBS)
+        stages.setdefault(stage, {})[op] = e
+        total += us
+        total_flops += fl
+    plans = {b: {"conv1": blk["conv1"].plan(nc if blk["coarse"] else nf, nc if blk["coarse"] else nf,
+                                            plan_c if blk["coarse"] else plan_f),
+                 "conv2": blk["conv2"].plan(nc if blk["coarse"] else nf, nc if blk["coarse"] else nf,
+                                            plan_c if blk["coarse"] else plan_f)}
+             for b, blk in zip(("input_blocks.0", "input_blocks.1", "out_blocks.0", "out_blocks.1"), blocks)}
+    return {"us_per_forward": total, "tflops": total_flops / total / 1e6, "frac": total_flops / total / 1e6 / peak,
+            "fine": nf, "coarse": nc, "pairs_fine": pf, "pairs_coarse": pc, "gather_plan_us": plan_us,
+            "ms_per_sample_38_forwards": 38 * total / 1e3, "stages": stages, "plans": plans,
+            "dtype": "bf16" if bf else "fp32"}
 
 
 def mesh_stack(s3dx, W, stream, seed, d0, p0, ch0, k0):

@@ -405,6 +405,15 @@ S3DX_API s3dx_status s3dx_upsample_nearest(const void *coarse, int32_t dtype, in
                                            int32_t c, const int32_t *fine_to_coarse, int64_t nf,
                                            void *y, s3dx_stream stream, char *error,
                                            uint64_t error_capacity);
+/* Row concatenation along channels (ggml_concat of the SLat out blocks,
+ * slat_flow_graph.cpp:443, 477), optionally through a row index:
+ * y[i] = [a[r][0..ca), b[r][0..cb)] with r = rows[i] (rows NULL: r = i),
+ * zero rows for r outside [0, n_src).  With rows = fine_to_coarse it is
+ * out_blocks.0's concat + nearest upsample (:443-444) in one pass.  A copy,
+ * bit-exact; y [n][ca + cb] must not overlap a or b. */
+S3DX_API s3dx_status s3dx_concat_rows(const void *a, int32_t ca, const void *b, int32_t cb, int32_t dtype,
+                                      int64_t n_src, const int32_t *rows, int64_t n, void *y,
+                                      s3dx_stream stream, char *error, uint64_t error_capacity);
 /* dtype conversion F32 <-> BF16 (round to nearest even), count elements. */
 S3DX_API s3dx_status s3dx_convert(const void *x, int32_t x_dtype, int64_t count, void *y,
                                   int32_t y_dtype, s3dx_stream stream, char *error,

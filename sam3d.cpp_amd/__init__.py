@@ -95,6 +95,7 @@ SIGNATURES = {
     "s3dx_affine_rows": (_u32, [_vp, _i32, _i64, _i32, _vp, _vp, _i32, _vp, _i32, _vp], True),
     "s3dx_downsample_mean": (_u32, [_vp, _i32, _i64, _i32, _vp, _vp, _i64, _vp, _vp], True),
     "s3dx_upsample_nearest": (_u32, [_vp, _i32, _i64, _i32, _vp, _i64, _vp, _vp], True),
+    "s3dx_concat_rows": (_u32, [_vp, _i32, _vp, _i32, _i32, _i64, _vp, _i64, _vp, _vp], True),
     "s3dx_convert": (_u32, [_vp, _i32, _i64, _vp, _i32, _vp], True),
 }
 
@@ -600,6 +601,12 @@ def downsample_mean(x, dtype, nf, c, children, inv_count, nc, y, stream=None):
 def upsample_nearest(coarse, dtype, nc, c, f2c, nf, y, stream=None):
     call("s3dx_upsample_nearest", _dptr(coarse), _i32(dtype), _i64(nc), _i32(c), _dptr(f2c), _i64(nf),
          _dptr(y), _sptr(stream))
+
+
+def concat_rows(a, ca, b, cb, dtype, n_src, rows, n, y, stream=None):
+    """y[i] = [a[r], b[r]], r = rows[i] or i (ggml_concat, slat_flow_graph.cpp:443, 477)."""
+    call("s3dx_concat_rows", _dptr(a), _i32(ca), _dptr(b), _i32(cb), _i32(dtype), _i64(n_src), _dptr(rows),
+         _i64(n), _dptr(y), _sptr(stream))
 
 
 def convert(x, x_dtype, count, y, y_dtype, stream=None):

@@ -314,6 +314,39 @@ upsample16_kernel(const uint4 *coarse, int64_t nc, int32_t ppr, const int32_t *f
     }
 }
 
+// Row concatenation through an optional row index: y[i] = [a[r], b[r]],
+// r = rows ? rows[i] : i, zero rows for r outside [0, n_src).  The piece
+// variant moves 16-byte pieces (both halves whole pieces, buffers aligned);
+// the element variant any widths.  A copy: bit-exact in either dtype.
+__global__ void __launch_bounds__(256)
+concat16_kernel(const uint4 *a, int32_t ppa, const uint4 *b, int32_t ppb, int64_t n_src, const int32_t *rows,
+                int32_t count, uint4 *y) {
+    const int32_t ppr = ppa + ppb;
+    for (int32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < count; i += gridDim.x * blockDim.x) {
+        const int32_t r = i / ppr, pc = i - r * ppr;
+        const int64_t src = rows ? rows[r] : r;
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (src >= 0 && src < n_src) v = pc < ppa ? a[src * ppa + pc] : b[src * ppb + (pc - ppa)];
+        y[i] = v;
+    }
+}
+
+template <class T>
+__global__ void __launch_bounds__(256)
+concat_kernel(const T *a, int32_t ca, const T *b, int32_t cb, int64_t n_src, const int32_t *rows, int64_t n, T *y) {
+    const int32_t c = ca + cb;
+    const int64_t count = n * c;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < count; i += stride) {
+        const int64_t r = i / c;
+        const int32_t ch = static_cast<int32_t>(i - r * c);
+        const int64_t src = rows ? rows[r] : r;
+        T v = T(0);
+        if (src >= 0 && src < n_src) v = ch < ca ? a[src * ca + ch] : b[src * cb + (ch - ca)];
+        y[i] = v;
+    }
+}
+
 template <class TI, class TO>
 __global__ void __launch_bounds__(256) convert_kernel(const void *x, int64_t count, void *y) {
     const int64_t stride = static_cast<int64_t>(gridDim.x) * blockDim.x;
@@ -538,6 +571,36 @@ S3DX_API s3dx_status s3dx_upsample_nearest(const void *coarse, int32_t dtype, in
             upsample_kernel<float><<<grid_for(nf * c), 256, 0, s>>>(coarse, nc, c, fine_to_coarse, nf, y);
         }
         launch_check("upsample");
+    });
+}
+
+S3DX_API s3dx_status s3dx_concat_rows(const void *a, int32_t ca, const void *b, int32_t cb, int32_t dtype,
+                                      int64_t n_src, const int32_t *rows, int64_t n, void *y, s3dx_stream stream,
+                                      char *error, uint64_t error_capacity) {
+    return boundary(error, error_capacity, [&] {
+        require(a && b && y, "NULL argument");
+        require(ca > 0 && cb > 0 && n > 0 && n_src > 0, "sizes must be positive");
+        require(rows != nullptr || n <= n_src, "without a row index n must not exceed n_src");
+        require_dtype(dtype);
+        const hipStream_t s = as_stream(stream);
+        const int64_t es = dtype_size(dtype), ab = ca * es, bb = cb * es;
+        if (ab % 16 == 0 && bb % 16 == 0 && aligned(a, 16) && aligned(b, 16) && aligned(y, 16) &&
+            n * ((ab + bb) / 16) < (int64_t(1) << 30)) {
+            const int32_t ppa = static_cast<int32_t>(ab / 16), ppb = static_cast<int32_t>(bb / 16);
+            const int32_t count = static_cast<int32_t>(n * (ppa + ppb));
+            concat16_kernel<<<grid_for(count), 256, 0, s>>>(static_cast<const uint4 *>(a), ppa,
+                                                           static_cast<const uint4 *>(b), ppb, n_src, rows, count,
+                                                           static_cast<uint4 *>(y));
+        } else if (dtype == S3DX_BF16) {
+            concat_kernel<uint16_t><<<grid_for(n * (ca + cb)), 256, 0, s>>>(
+                static_cast<const uint16_t *>(a), ca, static_cast<const uint16_t *>(b), cb, n_src, rows, n,
+                static_cast<uint16_t *>(y));
+        } else {
+            concat_kernel<float><<<grid_for(n * (ca + cb)), 256, 0, s>>>(
+                static_cast<const float *>(a), ca, static_cast<const float *>(b), cb, n_src, rows, n,
+                static_cast<float *>(y));
+        }
+        launch_check("concat_rows");
     });
 }
 

@@ -32,9 +32,43 @@ def large_sets(W, O, arrays):
     return sets
 
 
+BF16_ROW_TOL = 1e-2  # worst row's rel-L2, BF16 gates
+BF16_ABS_TOL = 1e-2  # worst element's |error| / max |ref|, BF16 gates
+
+
+def row_errors(got, ref):
+    """(worst row rel-L2, worst |error| / max |ref|) over the rows of 2-D
+    arrays (1-D: one row).  A row's norm is floored at 0.1 x the RMS row norm,
+    so near-zero rows are judged against the scale of the whole output."""
+    a = np.asarray(got, np.float64)
+    b = np.asarray(ref, np.float64)
+    a = a.reshape(1, -1) if a.ndim == 1 else a.reshape(a.shape[0], -1)
+    b = b.reshape(1, -1) if b.ndim == 1 else b.reshape(b.shape[0], -1)
+    d = a - b
+    rn = np.sqrt(np.einsum("ij,ij->i", b, b))
+    floor = max(0.1 * float(np.sqrt(np.mean(rn * rn))), np.finfo(np.float64).tiny)
+    row = float(np.max(np.sqrt(np.einsum("ij,ij->i", d, d)) / np.maximum(rn, floor))) if d.size else 0.0
+    big = float(np.max(np.abs(b))) if b.size else 0.0
+    mabs = float(np.max(np.abs(d)) / max(big, np.finfo(np.float64).tiny)) if d.size else 0.0
+    return row, mabs
+
+
 def check_rel(got, ref, tol, what="") -> float:
-    """Asserts rel-L2(got, ref) <= tol, printing the measured value first."""
+    """Asserts rel-L2(got, ref) <= tol, printing the measured value first.
+    BF16-level gates (tol >= 1e-3) also bound the worst row (rel-L2 <= 1e-2)
+    and the worst element (|error| <= 1e-2 max |ref|): a localized error --
+    a wrong halo slot, a tail tile, a missed neighbour in 0.1% of rows --
+    stays under a global 1e-2 but not under these (a row missing one of ~21
+    neighbours is off by ~0.2)."""
     e = rel_l2(got, ref)
+    if tol >= 1e-3:
+        row, mabs = row_errors(got, ref)
+        print(f"  rel-L2 {e:.3e} (gate {tol:.0e}), worst row {row:.3e}, max-abs/max {mabs:.3e} "
+              f"(gates {BF16_ROW_TOL:.0e}) {what}", flush=True)
+        assert e <= tol, (what, e, tol)
+        assert row <= BF16_ROW_TOL, (what, "worst row", row)
+        assert mabs <= BF16_ABS_TOL, (what, "max abs", mabs)
+        return e
     print(f"  rel-L2 {e:.3e} (gate {tol:.0e}) {what}", flush=True)
     assert e <= tol, (what, e, tol)
     return e

@@ -279,3 +279,42 @@ def test_plan_tile_heights_agree(s3dx, O, W, monkeypatch, rows):
     conv.run(xd, n, kd, n, y0, s3dx.BF16, res)
     conv.run(xd, n, kd, n, y1, s3dx.BF16, res, plan=gp)
     assert np.array_equal(y0.download(), y1.download())
+
+
+@pytest.mark.parametrize("cin", [128, 2048])
+def test_planned_layernorm_modulate_full_size(s3dx, O, W, cin):
+    # The res_block's conv1 as the benchmark times it and as the SLat flow
+    # runs it (slat_flow_graph.cpp:216-275, out_blocks.0 at :441-470): BF16,
+    # LayerNorm (no affine) + h*(1+scale)+shift + SiLU fused, scale/shift in
+    # device buffers rewritten between forwards, on the config-2 set with the
+    # map's 128-row gather plan (the 8-wave kernel, tiling 22).  Each forward:
+    # planned == unplanned bit for bit, and both against the float64 oracle
+    # (all rows at 128 input channels, 3,000 sampled rows at 2048).
+    coords = W.shells_union(0)
+    n = coords.shape[0]
+    kmap = O.kmap_subm3(coords, n)
+    cout, seed = 128, 80 + cin // 128
+    w, b = W.conv_weight(seed, 2, cin, cout), W.normal_f32(seed, 3, (cout,), 0.1)
+    ms, mh = s3dx.DeviceArray((cout,), np.float32), s3dx.DeviceArray((cout,), np.float32)
+    conv = (s3dx.SparseConv(cin, cout, 27, s3dx.BF16).set_weights(w, s3dx.WEIGHT_SLAT, b)
+            .set_layernorm(True, 1e-6).set_modulate(ms, mh).set_silu(True))
+    dk = s3dx.DeviceArray.from_host(kmap)
+    gp = conv.gather_plan(n, dk, n)
+    plan = conv.plan(n, n, gp)
+    print(f"planned LN+modulate+SiLU {cin}->{cout}: {plan} | unplanned: {conv.plan(n, n)}", flush=True)
+    assert plan == "mfma tiling=22 split-k halo rows=128 cols=128 kc=64 xf=0 ln=fused grid=221x1 plan=128", plan
+    x = W.round_bf16(W.normal_f32(seed, 1, (n, cin)))
+    xd = _bf(s3dx, W, x)
+    rows = np.arange(n) if cin == 128 else np.sort(np.random.default_rng(seed).choice(n, 3000, replace=False))
+    h = O.layernorm(O.conv(x, kmap[rows], n, W.round_bf16(w), 0, cout, b), 1e-6)
+    yp, yu = s3dx.DeviceArray((n, cout), np.uint16), s3dx.DeviceArray((n, cout), np.uint16)
+    for fwd in range(2):
+        scale, shift = W.normal_f32(seed, 10 + fwd, (cout,), 0.3), W.normal_f32(seed, 20 + fwd, (cout,), 0.3)
+        ms.upload(scale)
+        mh.upload(shift)
+        conv.run(xd, n, dk, n, yp, s3dx.BF16, plan=gp)
+        conv.run(xd, n, dk, n, yu, s3dx.BF16)
+        got = yp.download()
+        assert np.array_equal(got, yu.download()), f"forward {fwd}: planned != unplanned"
+        got = W.bf16_bits_to_f32(got).reshape(n, cout)[rows]
+        check_rel(got, O.silu(O.modulate(h, scale, shift)), 1e-2, f"{cin}->{cout} forward {fwd}")

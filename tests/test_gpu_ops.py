@@ -103,3 +103,33 @@ def test_convert_roundtrip(s3dx, W, count):
     same = s3dx.DeviceArray((count,), np.float32)
     s3dx.convert(back, s3dx.F32, count, same, s3dx.F32)
     assert np.array_equal(same.download(), back.download())
+
+
+@pytest.mark.parametrize("dtype,ca,cb", [(1, 1024, 1024), (1, 128, 128), (0, 128, 128), (1, 24, 8), (0, 5, 3)])
+@pytest.mark.parametrize("gather", [False, True])
+def test_concat_rows(s3dx, W, dtype, ca, cb, gather):
+    # The SLat out blocks' ggml_concat (slat_flow_graph.cpp:443, 477): with a
+    # row index (fine_to_coarse) it is out_blocks.0's concat + upsample in one
+    # pass.  Bit-exact against numpy; indices outside the source give zero rows.
+    coords = W.shells_union(1)
+    n = coords.shape[0]
+    nc, cc, f2c, ch, inv = s3dx.coarsen2(dev(s3dx, coords), n)
+    src = nc if gather else n
+    store = np.uint16 if dtype == s3dx.BF16 else np.float32
+    a = W.normal_f32(15, ca, (src, ca))
+    b = W.normal_f32(16, cb, (src, cb))
+    if dtype == s3dx.BF16:
+        a, b = W.f32_to_bf16_bits(a), W.f32_to_bf16_bits(b)
+    rows = f2c.download().copy() if gather else None
+    if gather:
+        rows[::97] = -1
+        rows[1::89] = nc
+    print(f"concat dtype={dtype} {ca}+{cb} gather={gather} rows={n}", flush=True)
+    y = s3dx.DeviceArray((n, ca + cb), store)
+    s3dx.concat_rows(dev(s3dx, a), ca, dev(s3dx, b), cb, dtype, src,
+                     dev(s3dx, rows) if gather else None, n, y)
+    want = np.concatenate([a, b], 1)
+    if gather:
+        ok = (rows >= 0) & (rows < nc)
+        want = np.where(ok[:, None], want[np.clip(rows, 0, nc - 1)], 0).astype(store)
+    assert np.array_equal(y.download(), want)

@@ -281,3 +281,31 @@ def test_round_bf16_nearest_even(O):
     r = O.round_bf16(v)
     assert r[0] == 1.0 and r[1] == 1.0 and r[2] == np.float32(1.015625)
     assert np.all(r.view(np.uint32) & 0xFFFF == 0)
+
+
+def test_bf16_gates_catch_localized_errors(O, W):
+    # The BF16 parity gates' per-row and max-abs bounds (tests/helpers.py):
+    # the oracle's output rounded to BF16 passes all three; the same conv
+    # with one neighbour dropped from 0.1% of the rows (a planted map error,
+    # as a wrong halo slot or a stale table word would make) stays under the
+    # global rel-L2 gate of 1e-2 but fails the per-row bound.
+    from helpers import BF16_ABS_TOL, BF16_ROW_TOL, rel_l2, row_errors
+    coords = np.ascontiguousarray(W.shells_union(0)[:8000])
+    n = coords.shape[0]
+    kmap = O.kmap_subm3(coords, n)
+    x = W.normal_f32(1, 1, (n, 64))
+    w = W.conv_weight(1, 2, 64, 64)
+    ref = O.conv(x, kmap, n, w, 0, 64)
+    good = W.round_bf16(ref)
+    row, mabs = row_errors(good, ref)
+    assert rel_l2(good, ref) < 1e-2 and row < BF16_ROW_TOL and mabs < BF16_ABS_TOL, (row, mabs)
+    bad_map = kmap.copy()
+    rng = np.random.default_rng(3)
+    for i in rng.choice(n, n // 1000, replace=False):
+        o = next(o for o in range(27) if o != 13 and kmap[i, o] < n)
+        bad_map[i, o] = n
+    bad = W.round_bf16(O.conv(x, bad_map, n, w, 0, 64))
+    row, mabs = row_errors(bad, ref)
+    print(f"planted error: rel-L2 {rel_l2(bad, ref):.2e}, worst row {row:.2e}, max-abs {mabs:.2e}")
+    assert rel_l2(bad, ref) <= 1e-2
+    assert row > BF16_ROW_TOL
