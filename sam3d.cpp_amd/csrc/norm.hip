@@ -57,6 +57,145 @@ layernorm_kernel(const void *x, int64_t n, int32_t c, float eps, const float *w,
     }
 }
 
+// VE elements of T at element offset `elem` as floats (one 8- or 16-byte
+// access, or two 16-byte ones), and back.
+template <class T, int VE>
+__device__ __forceinline__ void vload(const void *base, int64_t elem, float (&v)[VE]) {
+    constexpr int BYTES = VE * static_cast<int>(sizeof(T));
+    const char *p = static_cast<const char *>(base) + elem * static_cast<int64_t>(sizeof(T));
+    uint32_t wd[BYTES / 4];
+    if constexpr (BYTES == 8) {
+        const uint2 t = *reinterpret_cast<const uint2 *>(p);
+        wd[0] = t.x;
+        wd[1] = t.y;
+    } else {
+#pragma unroll
+        for (int q = 0; q < BYTES / 16; ++q) {
+            const uint4 t = reinterpret_cast<const uint4 *>(p)[q];
+            wd[4 * q] = t.x;
+            wd[4 * q + 1] = t.y;
+            wd[4 * q + 2] = t.z;
+            wd[4 * q + 3] = t.w;
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < VE; ++e) {
+        if constexpr (sizeof(T) == 2)
+            v[e] = bf16_to_f32(static_cast<uint16_t>(e & 1 ? wd[e >> 1] >> 16 : wd[e >> 1] & 0xffffu));
+        else
+            v[e] = __builtin_bit_cast(float, wd[e]);
+    }
+}
+template <class T, int VE>
+__device__ __forceinline__ void vstore(void *base, int64_t elem, const float (&v)[VE]) {
+    constexpr int BYTES = VE * static_cast<int>(sizeof(T));
+    char *p = static_cast<char *>(base) + elem * static_cast<int64_t>(sizeof(T));
+    uint32_t wd[BYTES / 4];
+#pragma unroll
+    for (int e = 0; e < VE; ++e) {
+        if constexpr (sizeof(T) == 2) {
+            const uint32_t h = f32_to_bf16(v[e]);
+            if (e & 1) wd[e >> 1] |= h << 16;
+            else wd[e >> 1] = h;
+        } else {
+            wd[e] = __builtin_bit_cast(uint32_t, v[e]);
+        }
+    }
+    if constexpr (BYTES == 8) {
+        *reinterpret_cast<uint2 *>(p) = make_uint2(wd[0], wd[1]);
+    } else {
+#pragma unroll
+        for (int q = 0; q < BYTES / 16; ++q)
+            reinterpret_cast<uint4 *>(p)[q] = make_uint4(wd[4 * q], wd[4 * q + 1], wd[4 * q + 2], wd[4 * q + 3]);
+    }
+}
+
+// LayerNorm with the row held in registers: 2^lpr_log2 lanes per row (64 /
+// lanes rows per wave), each lane PPL pieces of VE = 16 / sizeof(TI)
+// elements (piece p*lanes + lane: consecutive lanes read consecutive 16-byte
+// pieces), so the row is read once and written once.  Mean, then the
+// centred variance of the held values, both reduced over the row's lanes
+// by xor shuffles.  Requires rows of whole pieces and 16-byte aligned
+// buffers and parameter vectors.
+template <class TI, class TO, int PPL>
+__global__ void __launch_bounds__(256)
+layernorm_vec_kernel(const void *x, int64_t n, int32_t c, int32_t lpr_log2, float eps, const float *w,
+                     const float *b, const float *ms, const float *mh, int32_t do_silu, void *y, const void *res,
+                     int32_t res_shift) {
+    constexpr int VE = 16 / static_cast<int>(sizeof(TI));
+    const int lane = threadIdx.x & 63;
+    const int lpr = 1 << lpr_log2;
+    const int64_t row = (static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6)) * (64 >> lpr_log2) +
+                        (lane >> lpr_log2);
+    const int sl = lane & (lpr - 1);
+    const int ppr = c / VE;
+    const bool active = row < n;
+    float v[PPL][VE];
+    float sum = 0.0f;
+#pragma unroll
+    for (int p = 0; p < PPL; ++p) {
+        const int pi = p * lpr + sl;
+        if (active && pi < ppr) {
+            vload<TI, VE>(x, row * c + static_cast<int64_t>(pi) * VE, v[p]);
+        } else {
+#pragma unroll
+            for (int e = 0; e < VE; ++e) v[p][e] = 0.0f;
+        }
+#pragma unroll
+        for (int e = 0; e < VE; ++e) sum += v[p][e];
+    }
+    for (int d = 1; d < lpr; d <<= 1) sum += __shfl_xor(sum, d, 64);
+    const float mean = sum / static_cast<float>(c);
+    float q = 0.0f;
+#pragma unroll
+    for (int p = 0; p < PPL; ++p) {
+        if (p * lpr + sl >= ppr) continue;
+#pragma unroll
+        for (int e = 0; e < VE; ++e) {
+            const float t = v[p][e] - mean;
+            q += t * t;
+        }
+    }
+    for (int d = 1; d < lpr; d <<= 1) q += __shfl_xor(q, d, 64);
+    const float rstd = rsqrtf(q / static_cast<float>(c) + eps);
+    if (!active) return;
+#pragma unroll
+    for (int p = 0; p < PPL; ++p) {
+        const int pi = p * lpr + sl;
+        if (pi >= ppr) continue;
+        const int64_t ch = static_cast<int64_t>(pi) * VE;
+        float t[VE], pw[VE], pb[VE], r[VE];
+#pragma unroll
+        for (int e = 0; e < VE; ++e) t[e] = (v[p][e] - mean) * rstd;
+        if (w) {
+            vload<float, VE>(w, ch, pw);
+#pragma unroll
+            for (int e = 0; e < VE; ++e) t[e] *= pw[e];
+        }
+        if (b) {
+            vload<float, VE>(b, ch, pb);
+#pragma unroll
+            for (int e = 0; e < VE; ++e) t[e] += pb[e];
+        }
+        if (ms) {
+            vload<float, VE>(ms, ch, pw);
+            vload<float, VE>(mh, ch, pb);
+#pragma unroll
+            for (int e = 0; e < VE; ++e) t[e] = (t[e] * pw[e] + t[e]) + pb[e];
+        }
+        if (do_silu) {
+#pragma unroll
+            for (int e = 0; e < VE; ++e) t[e] = silu(t[e]);
+        }
+        if (res) {
+            vload<TO, VE>(res, (row >> res_shift) * c + ch, r);
+#pragma unroll
+            for (int e = 0; e < VE; ++e) t[e] += r[e];
+        }
+        vstore<TO, VE>(y, row * c + ch, t);
+    }
+}
+
 // GroupNorm statistics in one pass over x.  Each channel's values are
 // shifted by its row-0 value K (the shifted-data variance method), so
 // sum (x - K) and sum (x - K)^2 stay well conditioned when |mean| >> std.
@@ -403,6 +542,29 @@ unsigned grid_for(int64_t count) {
         else KERNEL<float, float> __VA_ARGS__;                                               \
     } while (0)
 
+struct LnVecArgs {
+    const void *x;
+    int64_t n;
+    int32_t c, lg;
+    float eps;
+    const float *w, *b, *ms, *mh;
+    int32_t silu;
+    void *y;
+    const void *res;
+    int32_t res_shift;
+};
+template <int PPL>
+void ln_vec_launch(const LnVecArgs &a, int32_t xd, int32_t yd, unsigned blocks, hipStream_t stream) {
+#define S3DX_LN_VEC(TI, TO)                                                                                   \
+    layernorm_vec_kernel<TI, TO, PPL><<<blocks, 256, 0, stream>>>(a.x, a.n, a.c, a.lg, a.eps, a.w, a.b, a.ms, \
+                                                                  a.mh, a.silu, a.y, a.res, a.res_shift)
+    if (xd == S3DX_BF16 && yd == S3DX_BF16) S3DX_LN_VEC(uint16_t, uint16_t);
+    else if (xd == S3DX_BF16) S3DX_LN_VEC(uint16_t, float);
+    else if (yd == S3DX_BF16) S3DX_LN_VEC(float, uint16_t);
+    else S3DX_LN_VEC(float, float);
+#undef S3DX_LN_VEC
+}
+
 struct GnLayout {
     float *partials;  // [kStatBlocks][2][c]
 };
@@ -418,10 +580,28 @@ void layernorm_rows_launch(const void *x, int32_t x_dtype, int64_t n, int32_t c,
                            const float *w, const float *b, const float *mod_scale,
                            const float *mod_shift, int32_t do_silu, void *y, int32_t y_dtype,
                            hipStream_t stream, const void *residual, int32_t residual_shift) {
-    const unsigned blocks = static_cast<unsigned>((n + 3) / 4);
-    S3DX_DISPATCH2(x_dtype, y_dtype, layernorm_kernel,
-                   <<<blocks, 256, 0, stream>>>(x, n, c, eps, w, b, mod_scale, mod_shift, do_silu, y,
-                                                residual, residual_shift));
+    const int64_t ve = 16 / dtype_size(x_dtype);
+    const int64_t ppr = c % ve == 0 ? c / ve : 0;
+    const bool vec = ppr > 0 && ppr <= 512 && x != y && aligned(x, 16) && aligned(y, 16) &&
+                     (!residual || aligned(residual, 16)) && (!w || aligned(w, 16)) && (!b || aligned(b, 16)) &&
+                     (!mod_scale || (aligned(mod_scale, 16) && aligned(mod_shift, 16)));
+    if (vec) {
+        int lg = 0;
+        while ((1 << lg) < ppr && lg < 6) ++lg;  // lanes per row: 2^lg, at most 64
+        const int64_t ppl = (ppr + (1 << lg) - 1) >> lg;
+        const int64_t rows_per_block = 4 * (64 >> lg);
+        const unsigned blocks = static_cast<unsigned>((n + rows_per_block - 1) / rows_per_block);
+        const LnVecArgs la{x, n, c, lg, eps, w, b, mod_scale, mod_shift, do_silu, y, residual, residual_shift};
+        if (ppl <= 1) ln_vec_launch<1>(la, x_dtype, y_dtype, blocks, stream);
+        else if (ppl <= 2) ln_vec_launch<2>(la, x_dtype, y_dtype, blocks, stream);
+        else if (ppl <= 4) ln_vec_launch<4>(la, x_dtype, y_dtype, blocks, stream);
+        else ln_vec_launch<8>(la, x_dtype, y_dtype, blocks, stream);
+    } else {
+        const unsigned blocks = static_cast<unsigned>((n + 3) / 4);
+        S3DX_DISPATCH2(x_dtype, y_dtype, layernorm_kernel,
+                       <<<blocks, 256, 0, stream>>>(x, n, c, eps, w, b, mod_scale, mod_shift, do_silu, y,
+                                                    residual, residual_shift));
+    }
     launch_check("layernorm");
 }
 

@@ -30,6 +30,33 @@ def test_layernorm_rows(s3dx, O, W, c):
     check_rel(got, O.layernorm(W.round_bf16(x), 1e-6), 1e-2)
 
 
+@pytest.mark.parametrize("xd,yd,c", [
+    (1, 1, 128), (1, 1, 256), (1, 1, 1024), (1, 1, 2048), (1, 1, 4096), (1, 1, 96), (1, 1, 6144),
+    (0, 0, 128), (0, 0, 2048), (0, 1, 1024), (1, 0, 192), (0, 0, 20), (1, 1, 24)])
+def test_layernorm_rows_vector_path(s3dx, O, W, xd, yd, c):
+    # Out of place with 16-byte aligned rows: the register-resident kernel
+    # (2^k lanes per row, 1-8 pieces per lane, several rows per wave for
+    # narrow rows); rows wider than 512 pieces (BF16 6144) or not whole
+    # pieces (FP32 20) take the element kernel.  Row count not a multiple of
+    # the rows per block.  norm1's affine + SiLU, then the modulate form.
+    n = 3001
+    x = W.normal_f32(12, c, (n, c), 2.0) + 0.5
+    w, b = W.normal_f32(12, 2, (c,)), W.normal_f32(12, 3, (c,))
+    ms, mh = W.normal_f32(12, 4, (c,)), W.normal_f32(12, 5, (c,))
+    store = {0: np.float32, 1: np.uint16}
+    xin = W.f32_to_bf16_bits(x) if xd == 1 else x
+    xr = W.round_bf16(x) if xd == 1 else x
+    host = (lambda d: W.bf16_bits_to_f32(d.download()).reshape(n, c)) if yd == 1 else (lambda d: d.download())
+    tol = 1e-2 if yd == 1 else 1e-5
+    print(f"layernorm vector path x={xd} y={yd} c={c}", flush=True)
+    dx = dev(s3dx, xin)
+    y = s3dx.DeviceArray((n, c), store[yd])
+    s3dx.layernorm_rows(dx, xd, n, c, 1e-6, dev(s3dx, w), dev(s3dx, b), silu=True, y=y, y_dtype=yd)
+    check_rel(host(y), O.silu(O.layernorm(xr, 1e-6, w, b)), tol, "affine + SiLU")
+    s3dx.layernorm_rows(dx, xd, n, c, 1e-6, None, None, dev(s3dx, ms), dev(s3dx, mh), y=y, y_dtype=yd)
+    check_rel(host(y), O.modulate(O.layernorm(xr, 1e-6), ms, mh), tol, "modulate")
+
+
 @pytest.mark.parametrize("n,c,groups,mean,std", [
     (5000, 96, 32, 2.0, 1.5), (40000, 192, 32, 2.0, 1.5), (3000, 768, 32, 2.0, 1.5),
     (20000, 96, 32, 300.0, 0.05),  # |mean| >> std: the shifted sums keep the variance
