@@ -19,9 +19,12 @@ namespace {
 
 // ---- the kernel-map table ----------------------------------------------------
 // Two structures, chosen per coordinate:
-//  - a direct-index window of 64^3 cells for batch 0 and x, y, z in [0, 64)
-//    (the SLat grids: 64^3 fine, 32^3 coarse), one 64-bit word {row, tag} per
-//    cell: a lookup is one 8-byte read, an insert a read and a CAS;
+//  - a direct-index window of E^3 cells for batch 0 and x, y, z in [0, E),
+//    one 64-bit word {row, tag} per cell: a lookup is one 8-byte read, an
+//    insert a read and a CAS.  E is 64 (the SLat grids: 64^3 fine, 32^3
+//    coarse, the mesh decoder's 64^3 parents), or 128 / 256 when the set is
+//    large enough that the window takes no more bytes than the hash slots
+//    (the mesh decoder's 128^3 and 256^3 child sets: 226k and 1.81M voxels);
 //  - for every other coordinate, open addressing with linear probing at load
 //    <= 1/4 over 16-byte slots {key lo, key hi, row, tag}.  The key is
 //    (b, x, y, z) packed as four int16 when the coordinate fits (a set with
@@ -49,15 +52,16 @@ namespace {
 // entry; the flag words alone are taken on their value, and a raised flag
 // that decides an error (subdivide's duplicate test) is confirmed by an
 // exact pass before it is reported.
-constexpr int kWindow = 64;                                 // cells per axis
-constexpr int64_t kWindowCells = int64_t(kWindow) * kWindow * kWindow;
+constexpr int kWindowMinLog2 = 6;  // 64 cells per axis
+constexpr int kWindowMaxLog2 = 8;  // 256 cells per axis
 
 struct KmapHash {
-    unsigned long long *cells;  // kWindowCells words {row, tag}
+    unsigned long long *cells;  // 2^(3 * wlog2) words {row, tag}
     uint4 *slots;               // mask + 1 slots
     int32_t *flags;             // [kFlag*] == flag_of(seed, k) when raised in this build
     uint32_t mask;
     uint32_t seed;
+    int32_t wlog2;              // window extent 2^wlog2 cells per axis
 };
 
 constexpr int kFlagWide = 2;     // some hashed coordinate does not fit int16
@@ -78,11 +82,11 @@ __device__ __host__ __forceinline__ int32_t flag_of(uint32_t seed, int k) {
     return static_cast<int32_t>(mix32(seed + 0x632BE5ABu * static_cast<uint32_t>(k + 1)));
 }
 
-// The window cell of c, or -1.
-__device__ __forceinline__ int32_t window_cell(int4 c) {
+// The window cell of c (x-major, z fastest), or -1.
+__device__ __forceinline__ int32_t window_cell(int4 c, int32_t wlog2) {
     const uint32_t x = static_cast<uint32_t>(c.y), y = static_cast<uint32_t>(c.z), z = static_cast<uint32_t>(c.w);
-    if (c.x != 0 || (x | y | z) >= static_cast<uint32_t>(kWindow)) return -1;
-    return static_cast<int32_t>((x * kWindow + y) * kWindow + z);
+    if (c.x != 0 || (x | y | z) >= (1u << wlog2)) return -1;
+    return static_cast<int32_t>((((x << wlog2) | y) << wlog2) | z);
 }
 
 __device__ __forceinline__ bool fits16(int4 c) {
@@ -142,7 +146,7 @@ kmap_insert_kernel(const int4 *__restrict__ keys, int32_t n, KmapHash h) {
     const int32_t i = blockIdx.x * kThreads + threadIdx.x;
     if (i >= n) return;
     const int4 c = keys[i];
-    const int32_t cell = window_cell(c);
+    const int32_t cell = window_cell(c, h.wlog2);
     if (cell < 0) {
         kmap_hash_insert(keys, n, h, i, c);
         return;
@@ -188,7 +192,7 @@ __device__ __forceinline__ int32_t kmap_hash_find(const KmapHash &h, const int4 
 // Smallest row whose key equals q, or -1 (after kmap_insert_kernel).
 __device__ __forceinline__ int32_t kmap_find(const KmapHash &h, const int4 *__restrict__ keys, int32_t n, int4 q,
                                              bool wide) {
-    const int32_t cell = window_cell(q);
+    const int32_t cell = window_cell(q, h.wlog2);
     if (cell < 0) return kmap_hash_find(h, keys, n, q, wide);
     const unsigned long long v = h.cells[cell];
     const uint32_t r = static_cast<uint32_t>(v);
@@ -276,17 +280,30 @@ constexpr uint64_t kmap_capacity(int64_t n) {
     return cap;
 }
 
+// log2 of the window extent for n voxels: the largest of 64, 128, 256
+// (at most max_log2) whose 8-byte cells take no more bytes than the
+// 16-byte hash slots, so the window at most doubles the workspace.
+constexpr int32_t window_log2(int64_t n, int32_t max_log2) {
+    const uint64_t slot_bytes = kmap_capacity(n) * 16;
+    int32_t lg = kWindowMinLog2;
+    while (lg < max_log2 && (uint64_t(8) << (3 * (lg + 1))) <= slot_bytes) ++lg;
+    return lg;
+}
+
 template <class W>
-void kmap_layout(W &w, int64_t n, KmapHash *h) {
+void kmap_layout(W &w, int64_t n, KmapHash *h, int32_t max_log2 = kWindowMaxLog2) {
     const uint64_t cap = kmap_capacity(n);
+    const int32_t lg = window_log2(n, max_log2);
+    const uint64_t cells = uint64_t(1) << (3 * lg);
     if constexpr (std::is_same_v<W, Carver>) {
-        h->cells = w.template take<unsigned long long>(kWindowCells);
+        h->cells = w.template take<unsigned long long>(cells);
         h->slots = w.template take<uint4>(cap);
         h->flags = w.template take<int32_t>(64);
         h->mask = static_cast<uint32_t>(cap - 1);
         h->seed = 0;
+        h->wlog2 = lg;
     } else {
-        w.template take<unsigned long long>(kWindowCells);
+        w.template take<unsigned long long>(cells);
         w.template take<uint4>(cap);
         w.template take<int32_t>(64);
     }
@@ -332,7 +349,9 @@ void run_kmap(const int4 *coords, int32_t n, int32_t missing, int32_t *kmap, Kma
 // Allocation-free kernel maps: the hash table lives in `scratch`, one array
 // per device for the life of the process, sized for kStaticKmapMaxVoxels.
 constexpr int64_t kStaticKmapMaxVoxels = int64_t(1) << 18;
-constexpr uint64_t kStaticKmapBytes = kWindowCells * 8 + (kmap_capacity(kStaticKmapMaxVoxels) * 16 + 255) / 256 * 256 +
+// (its window stays 64^3: the array is sized for that layout)
+constexpr uint64_t kStaticKmapBytes = (uint64_t(8) << (3 * kWindowMinLog2)) +
+                                      (kmap_capacity(kStaticKmapMaxVoxels) * 16 + 255) / 256 * 256 +
                                       (64 * 4 + 255) / 256 * 256;
 static __device__ __align__(256) unsigned char scratch[kStaticKmapBytes];
 
@@ -422,7 +441,7 @@ S3DX_API s3dx_status s3dx_kmap_subm3_static(const int32_t *coords, int64_t n, in
         require(n <= kStaticKmapMaxVoxels, "voxel count exceeds the static table's maximum (262144)");
         Carver w(static_scratch(), kStaticKmapBytes);
         KmapHash h;
-        kmap_layout(w, n, &h);
+        kmap_layout(w, n, &h, kWindowMinLog2);
         run_kmap(reinterpret_cast<const int4 *>(coords), static_cast<int32_t>(n), missing_value, kmap, h,
                  as_stream(stream));
     });

@@ -191,12 +191,16 @@ def flag_value(seed, k):
 
 def kmap_flags_offset(n):
     """Byte offset of the flag words in a kernel-map workspace for n voxels:
-    the 64^3 window of 8-byte cells, then the 16-byte slots (power of two,
-    >= 4n, >= 256), each region rounded up to 256 bytes."""
+    the window of 8-byte cells (64^3, or 128^3 / 256^3 when those take no
+    more bytes than the slots), then the 16-byte slots (power of two, >= 4n,
+    >= 256), each region a multiple of 256 bytes."""
     cap = 256
     while cap < 4 * n:
         cap <<= 1
-    return 64 ** 3 * 8 + cap * 16
+    lg = 6
+    while lg < 8 and 8 << (3 * (lg + 1)) <= cap * 16:
+        lg += 1
+    return (8 << (3 * lg)) + cap * 16
 
 
 def set_kmap_seed(s3dx, seed):

@@ -252,3 +252,29 @@ def test_subdivide_confirms_chance_flags(s3dx, W):
     dup = np.ascontiguousarray(np.concatenate([parents, parents[17:18]]))
     with pytest.raises(s3dx.S3dxError, match="duplicate"):
         s3dx.subdivide2(s3dx.DeviceArray.from_host(dup), n + 1)
+
+
+@pytest.mark.parametrize("extent,n", [(128, 150_000), (256, 1_100_000)])
+def test_wide_window_sets(s3dx, O, extent, n):
+    # Sets large enough for a 128^3 or 256^3 direct-index window (above
+    # 131,072 and 1,048,576 voxels): coordinates spread over the window,
+    # some outside it (batch 1, negative, beyond the extent: the hashed
+    # path), duplicated rows, a shuffled order; against the oracle, and on a
+    # workspace refilled with random bytes.
+    rng = np.random.default_rng(extent)
+    c = rng.integers(0, extent, size=(n, 4)).astype(np.int32)
+    c[:, 0] = 0
+    out = rng.choice(n, n // 50, replace=False)
+    c[out[: len(out) // 3], 0] = 1
+    c[out[len(out) // 3: 2 * len(out) // 3], 1] -= extent
+    c[out[2 * len(out) // 3:], 3] += extent
+    c[rng.choice(n, n // 100, replace=False)] = c[rng.choice(n, n // 100, replace=False)]
+    c = np.ascontiguousarray(c)
+    print(f"wide window extent={extent} n={n}", flush=True)
+    want = O.kmap_subm3(c, -1)
+    ws = s3dx.DeviceArray(s3dx.kmap_workspace_size(n), np.uint8)
+    for garbage in (False, True):
+        if garbage:
+            ws.upload(rng.integers(0, 256, size=ws.nbytes, dtype=np.uint8))
+        got = s3dx.kmap_subm3(s3dx.DeviceArray.from_host(c), n, -1, workspace=ws).download()
+        assert np.array_equal(got, want), f"garbage={garbage}"
