@@ -336,6 +336,19 @@ S3DX_API void s3dx_gather_plan_free(s3dx_gather_plan *plan);
 S3DX_API s3dx_status s3dx_gather_plan_rebuild(s3dx_gather_plan *plan, const s3dx_conv *conv, int64_t n_in,
                                               const int32_t *kmap, int64_t n_out, s3dx_stream stream,
                                               char *error, uint64_t error_capacity);
+/* s3dx_kmap_subm3 followed by s3dx_gather_plan_rebuild(plan, conv, n, kmap,
+ * n) in one pass: the kernel map of coords into kmap (byte-identical to
+ * s3dx_kmap_subm3, same workspace and guarantees) and, from the same
+ * lookups, the map's gather plan for `conv`'s source rows -- two launches
+ * instead of three, and the map is not read back.  No counterpart as a call:
+ * the reference builds its tables on the host once per sample
+ * (session.cpp:1563-1566) and gathers im2col rows afresh in every forward.
+ * For layers that gather the map's own rows (not s3dx_conv_set_gather_parent);
+ * n at most the rows the plan was created for. */
+S3DX_API s3dx_status s3dx_kmap_subm3_planned(const int32_t *coords, int64_t n, int32_t missing_value,
+                                             int32_t *kmap, s3dx_gather_plan *plan, const s3dx_conv *conv,
+                                             void *workspace, uint64_t workspace_bytes, s3dx_stream stream,
+                                             char *error, uint64_t error_capacity);
 /* s3dx_conv_run with a gather plan built for the same kmap, n_out and source
  * rows (S3DX_INVALID_ARGUMENT when the sizes or the source setup differ).
  * Results are bit-identical to s3dx_conv_run; launches that do not use the

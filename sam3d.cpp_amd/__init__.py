@@ -88,6 +88,7 @@ SIGNATURES = {
     "s3dx_gather_plan_free": (None, [_vp], False),
     "s3dx_gather_plan_rebuild": (_u32, [_vp, _vp, _i64, _vp, _i64, _vp], True),
     "s3dx_conv_plan_planned": (_u32, [_vp, _vp, _i64, _i64, C.c_char_p, _u64], True),
+    "s3dx_kmap_subm3_planned": (_u32, [_vp, _i64, _i32, _vp, _vp, _vp, _vp, _u64, _vp], True),
     "s3dx_conv_run_planned": (_u32, [_vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _i32, _vp], True),
     "s3dx_layernorm_rows": (_u32, [_vp, _i32, _i64, _i32, _f32, _vp, _vp, _vp, _vp, _i32, _vp, _i32, _vp], True),
     "s3dx_groupnorm_workspace_size": (_u32, [_i64, _i32, _i32, C.POINTER(_u64)], True),
@@ -267,6 +268,16 @@ def kmap_subm3(coords: DeviceArray, n: int, missing: int, kmap: DeviceArray = No
         workspace = DeviceArray(kmap_workspace_size(n), np.uint8)
     call("s3dx_kmap_subm3", _dptr(coords), _i64(n), _i32(missing), _dptr(kmap), _dptr(workspace),
          _u64(workspace.nbytes), _sptr(stream))
+    return kmap
+
+
+def kmap_subm3_planned(coords: DeviceArray, n: int, missing: int, kmap: DeviceArray, plan: "GatherPlan",
+                       conv: "SparseConv", workspace: DeviceArray = None, stream=None) -> DeviceArray:
+    """kmap_subm3 and plan.rebuild(conv, n, kmap, n) in one pass (s3dx_kmap_subm3_planned)."""
+    if workspace is None:
+        workspace = DeviceArray(kmap_workspace_size(n), np.uint8)
+    call("s3dx_kmap_subm3_planned", _dptr(coords), _i64(n), _i32(missing), _dptr(kmap), _vp(plan.handle),
+         _vp(conv.handle), _dptr(workspace), _u64(workspace.nbytes), _sptr(stream))
     return kmap
 
 

@@ -1168,6 +1168,26 @@ S3DX_API s3dx_status s3dx_gather_plan_rebuild(s3dx_gather_plan *plan, const s3dx
     });
 }
 
+S3DX_API s3dx_status s3dx_kmap_subm3_planned(const int32_t *coords, int64_t n, int32_t missing_value,
+                                             int32_t *kmap, s3dx_gather_plan *plan, const s3dx_conv *conv,
+                                             void *workspace, uint64_t workspace_bytes, s3dx_stream stream,
+                                             char *error, uint64_t error_capacity) {
+    return boundary(error, error_capacity, [&] {
+        require(coords != nullptr && aligned(coords, 16), "coords must be non-NULL and 16-byte aligned");
+        require(n > 0 && n <= INT32_MAX / 27, "voxel count out of range");
+        require(plan != nullptr && workspace != nullptr, "NULL argument");
+        gather_plan_check(conv, n, kmap, n);
+        require(!conv->gather_parent, "the layer gathers parent rows: its plan does not name the map's own rows");
+        require(n <= plan->capacity, "n exceeds the rows the plan was created for");
+        launch_kmap_plan(plan->rows, coords, n, missing_value, kmap, workspace, workspace_bytes, plan->d,
+                         as_stream(stream));
+        launch_check("kmap_plan");
+        plan->n_out = n;
+        plan->n_src = n;
+        plan->shift = 0;
+    });
+}
+
 S3DX_API s3dx_status s3dx_conv_run_planned(const s3dx_conv *conv, const s3dx_gather_plan *plan, const void *x,
                                            int64_t n_in, const int32_t *kmap, int64_t n_out, const void *residual,
                                            void *y, int32_t y_dtype, s3dx_stream stream, char *error,

@@ -29,6 +29,7 @@
 // (deterministic) and finished row-major (bias, LayerNorm, modulate, SiLU,
 // residual) by the shared finish_rows.
 #include "conv_kernels.hpp"
+#include "kmap_table.hpp"
 
 #include <type_traits>
 
@@ -138,35 +139,44 @@ struct TileDedupe {
     uint32_t mask, distinct;
     bool global_a;
 };
-template <int MB, bool ENTRY_ORDER = false, int NTH = 256>
-__device__ __forceinline__ TileDedupe dedupe_tile(const int32_t *kmap, int64_t n_src, int32_t row_shift, int64_t m0,
+// The tile's map slice read from memory: entries 4u..4u+3 of the tile
+// (16-byte aligned, ROWS * 108 bytes per tile); entries past `count` read
+// as -1.
+struct SliceLoad {
+    const int32_t *kmap;
+    __device__ __forceinline__ int4 operator()(int64_t m0, int u, int count) const {
+        const int4 *src = reinterpret_cast<const int4 *>(kmap + m0 * kMaxKvol);
+        int4 v = make_int4(-1, -1, -1, -1);
+        if (4 * u + 3 < count) {
+            v = src[u];
+        } else {
+            if (4 * u < count) v.x = kmap[m0 * kMaxKvol + 4 * u];
+            if (4 * u + 1 < count) v.y = kmap[m0 * kMaxKvol + 4 * u + 1];
+            if (4 * u + 2 < count) v.z = kmap[m0 * kMaxKvol + 4 * u + 2];
+        }
+        return v;
+    }
+};
+
+template <int MB, bool ENTRY_ORDER = false, int NTH = 256, class Fetch = SliceLoad>
+__device__ __forceinline__ TileDedupe dedupe_tile(Fetch fetch, int64_t n_src, int32_t row_shift, int64_t m0,
                                                   int tile_rows, uint16_t *table, int32_t *table32,
                                                   uint32_t *bitmap, uint32_t *prefix, uint32_t *slot_row,
                                                   int32_t *misc) {
     using SM = HaloSmem<MB>;
     constexpr int ROWS = SM::ROWS, CAP = SM::CAP, ENTRIES = SM::ENTRIES;
     const int tid = threadIdx.x, lane = tid & 63;
-    // ---- 1. this tile's map slice (ROWS * 27 entries; 16-byte aligned,
-    // ROWS * 108 bytes per tile), as source rows (-1: missing)
+    // ---- 1. this tile's map slice (ROWS * 27 entries) from `fetch`, as
+    // source rows (-1: missing)
     constexpr int V4 = ENTRIES / 4;
     constexpr int Q = (V4 + NTH - 1) / NTH;
     const int count = tile_rows * kMaxKvol;
     int sj[Q][4];
     {
-        const int4 *src = reinterpret_cast<const int4 *>(kmap + m0 * kMaxKvol);
 #pragma unroll
         for (int q = 0; q < Q; ++q) {
             const int u = tid + q * NTH;
-            int4 v = make_int4(-1, -1, -1, -1);
-            if (u < V4) {
-                if (4 * u + 3 < count) {
-                    v = src[u];
-                } else {
-                    if (4 * u < count) v.x = kmap[m0 * kMaxKvol + 4 * u];
-                    if (4 * u + 1 < count) v.y = kmap[m0 * kMaxKvol + 4 * u + 1];
-                    if (4 * u + 2 < count) v.z = kmap[m0 * kMaxKvol + 4 * u + 2];
-                }
-            }
+            const int4 v = u < V4 ? fetch(m0, u, count) : make_int4(-1, -1, -1, -1);
             const int jv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
@@ -372,7 +382,7 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_halo_kernel(ConvArg
         dd.distinct = __builtin_amdgcn_readfirstlane(hdr[1]);
         dd.mask = __builtin_amdgcn_readfirstlane(hdr[2]);
     } else {
-        dd = dedupe_tile<MB>(a.kmap, a.n_src, a.row_shift, m0, tile_rows, table, table32, bitmap, prefix, slot_row,
+        dd = dedupe_tile<MB>(SliceLoad{a.kmap}, a.n_src, a.row_shift, m0, tile_rows, table, table32, bitmap, prefix, slot_row,
                              misc);
     }
     const uint32_t mask = dd.mask, distinct = dd.distinct;
@@ -1202,9 +1212,8 @@ constexpr int kPlanBuild64Threads = 512;
 // neighbours by the zero row of the kernel's halo layout: slot kH8Single when
 // the tile's distinct rows need the single large buffer, else kH8Double (two
 // buffers, one per chunk).
-template <int MB, int NTH>
-__global__ void __launch_bounds__(NTH) gather_plan_build_kernel(const int32_t *kmap, int64_t n_out, int64_t n_src,
-                                                                int32_t row_shift, char *plan) {
+template <int MB, int NTH, class Fetch>
+__device__ __forceinline__ void plan_tile(Fetch fetch, int64_t n_out, int64_t n_src, int32_t row_shift, char *plan) {
     using SM = HaloSmem<MB>;
     constexpr int ROWS = SM::ROWS;
     constexpr int REC = MB == 2 ? kGatherPlanRecord : kGatherPlanRecord128;
@@ -1220,8 +1229,8 @@ __global__ void __launch_bounds__(NTH) gather_plan_build_kernel(const int32_t *k
     const int tile_rows = static_cast<int>(min(static_cast<int64_t>(ROWS), n_out - m0));
     // The tables come back in entry order (row-major, 27 per row: no LDS
     // bank conflicts on writing them); the record stores them offset-major.
-    const TileDedupe dd = dedupe_tile<MB, true, NTH>(kmap, n_src, row_shift, m0, tile_rows, table, table32, bitmap,
-                                                prefix, slot_row, misc);
+    const TileDedupe dd = dedupe_tile<MB, true, NTH>(fetch, n_src, row_shift, m0, tile_rows, table, table32, bitmap,
+                                                     prefix, slot_row, misc);
     char *rec = plan + static_cast<int64_t>(tile) * REC;
     if (tid == 0)
         *reinterpret_cast<uint4 *>(rec) = make_uint4(dd.global_a ? 1u : 0u, dd.distinct, dd.mask, 0u);
@@ -1247,7 +1256,101 @@ __global__ void __launch_bounds__(NTH) gather_plan_build_kernel(const int32_t *k
     }
 }
 
+template <int MB, int NTH>
+__global__ void __launch_bounds__(NTH) gather_plan_build_kernel(const int32_t *kmap, int64_t n_out, int64_t n_src,
+                                                                int32_t row_shift, char *plan) {
+    plan_tile<MB, NTH>(SliceLoad{kmap}, n_out, n_src, row_shift, plan);
+}
+
+// The tile's map slice computed by the lookups of the kernel map (and stored
+// into it) instead of read back: the map and its gather plan in one pass.
+struct SliceLookup {
+    const int4 *coords;
+    int32_t n, missing;
+    KmapHash h;
+    bool wide, dup;
+    int32_t *kmap;
+    __device__ __forceinline__ int4 operator()(int64_t m0, int u, int count) const {
+        // The four entries' loads go out together, step by step (coordinates,
+        // window cells, then the rows' coordinates that confirm them); an
+        // entry outside the window, or any entry when the set holds
+        // duplicates, takes the general kmap_entry instead.
+        int e[4], i[4], o[4], cell[4];
+        int4 c[4];
+        const int64_t g0 = m0 * kMaxKvol + 4 * u;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int64_t g = g0 + k;
+            i[k] = static_cast<int32_t>(g / kMaxKvol);
+            o[k] = static_cast<int32_t>(g - int64_t(i[k]) * kMaxKvol);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) c[k] = 4 * u + k < count ? coords[i[k]] : make_int4(-1, 0, 0, 0);
+        unsigned long long v[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            int4 q = c[k];
+            cell[k] = -1;
+            if (add_fits(c[k].y, o[k] / 9 - 1, &q.y) && add_fits(c[k].z, (o[k] / 3) % 3 - 1, &q.z) &&
+                add_fits(c[k].w, o[k] % 3 - 1, &q.w))
+                cell[k] = window_cell(q, h.wlog2);
+            c[k] = q;
+            v[k] = cell[k] >= 0 ? h.cells[cell[k]] : 0ull;
+        }
+        int4 rc[4];
+        uint32_t r[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            r[k] = static_cast<uint32_t>(v[k]);
+            const bool tagged = cell[k] >= 0 && static_cast<uint32_t>(v[k] >> 32) ==
+                                                    tag_of(h.seed, static_cast<uint32_t>(cell[k]));
+            if (!tagged || r[k] >= static_cast<uint32_t>(n)) r[k] = 0xFFFFFFFFu;
+            rc[k] = r[k] != 0xFFFFFFFFu ? coords[r[k]] : make_int4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            if (4 * u + k >= count) {
+                e[k] = -1;
+            } else if (dup || cell[k] < 0) {
+                e[k] = kmap_entry(h, coords, n, i[k], o[k], missing, wide, dup);
+            } else {
+                e[k] = r[k] != 0xFFFFFFFFu && same_key(rc[k], c[k]) ? static_cast<int32_t>(r[k]) : missing;
+            }
+        }
+        if (4 * u + 3 < count) {
+            *reinterpret_cast<int4 *>(kmap + g0) = make_int4(e[0], e[1], e[2], e[3]);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 3; ++k)
+                if (4 * u + k < count) kmap[g0 + k] = e[k];
+        }
+        return make_int4(e[0], e[1], e[2], e[3]);
+    }
+};
+
+template <int MB, int NTH>
+__global__ void __launch_bounds__(NTH) kmap_plan_kernel(const int4 *coords, int32_t n, KmapHash h, int32_t missing,
+                                                        int32_t *kmap, char *plan) {
+    const SliceLookup fetch{coords, n, missing, h, kmap_wide(h), kmap_dup(h), kmap};
+    plan_tile<MB, NTH>(fetch, n, n, 0, plan);
+}
+
 }  // namespace
+
+void launch_kmap_plan(int rows, const int32_t *coords, int64_t n, int32_t missing, int32_t *kmap, void *workspace,
+                      uint64_t workspace_bytes, void *plan, hipStream_t stream) {
+    const KmapHash h = kmap_insert_launch(reinterpret_cast<const int4 *>(coords), static_cast<int32_t>(n), workspace,
+                                          workspace_bytes, stream);
+    const unsigned tiles = static_cast<unsigned>((n + rows - 1) / rows);
+    if (rows == 128)
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(kmap_plan_kernel<4, kPlanBuild128Threads>), dim3(tiles),
+                           dim3(kPlanBuild128Threads), 0, stream, reinterpret_cast<const int4 *>(coords),
+                           static_cast<int32_t>(n), h, missing, kmap, static_cast<char *>(plan));
+    else
+        hipLaunchKernelGGL(HIP_KERNEL_NAME(kmap_plan_kernel<2, kPlanBuild64Threads>), dim3(tiles),
+                           dim3(kPlanBuild64Threads), 0, stream, reinterpret_cast<const int4 *>(coords),
+                           static_cast<int32_t>(n), h, missing, kmap, static_cast<char *>(plan));
+}
 
 KernelFn pick_halo_bf16(int rows, int nb) {
     if (nb == 3) return rows == 64 ? conv_halo_kernel<2, false, 3> : nullptr;

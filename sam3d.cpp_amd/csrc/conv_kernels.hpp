@@ -82,6 +82,10 @@ KernelFn pick_halo_bf16_planned(int rows, int nb = 4);
 constexpr int kHalo8Threads = 512;
 void launch_gather_plan_build(int rows, const int32_t *kmap, int64_t n_out, int64_t n_src, int32_t row_shift,
                               void *plan, hipStream_t stream);
+// Kernel map of coords (insert, then one workgroup per plan tile computing
+// its 27 * rows entries) and the map's gather plan from the same lookups.
+void launch_kmap_plan(int rows, const int32_t *coords, int64_t n, int32_t missing, int32_t *kmap, void *workspace,
+                      uint64_t workspace_bytes, void *plan, hipStream_t stream);
 constexpr int kGatherPlanRecord = 7168;      // 64-row tiles
 constexpr int kGatherPlanRecord128 = 18432;  // 128-row tiles
 // The FP32 1x1-layer kernel reading BF16 rows, else nullptr.

@@ -1,0 +1,155 @@
+// The kernel-map table shared by the map's kernels (kmap.hip) and the
+// one-pass map + gather-plan kernel (conv_halo.hip): its layout, tags and
+// lookups.  The insert kernel and the host side are in kmap.hip.
+#pragma once
+
+#include "coord_hash.hpp"
+
+namespace s3dx {
+
+struct KmapHash {
+    unsigned long long *cells;  // 2^(3 * wlog2) words {row, tag}
+    uint4 *slots;               // mask + 1 slots
+    int32_t *flags;             // [kFlag*] == flag_of(seed, k) when raised in this build
+    uint32_t mask;
+    uint32_t seed;
+    int32_t wlog2;              // window extent 2^wlog2 cells per axis
+};
+
+// Lays out `workspace` for n voxels, draws a new seed and launches the
+// insert; the returned table is ready for kmap_find once the launch has run
+// (kmap.hip).
+KmapHash kmap_insert_launch(const int4 *coords, int32_t n, void *workspace, uint64_t workspace_bytes,
+                            hipStream_t stream);
+
+namespace {
+
+// ---- the kernel-map table ----------------------------------------------------
+// Two structures, chosen per coordinate:
+//  - a direct-index window of E^3 cells for batch 0 and x, y, z in [0, E),
+//    one 64-bit word {row, tag} per cell: a lookup is one 8-byte read, an
+//    insert a read and a CAS.  E is 64 (the SLat grids: 64^3 fine, 32^3
+//    coarse, the mesh decoder's 64^3 parents), or 128 / 256 when the set is
+//    large enough that the window takes no more bytes than the hash slots
+//    (the mesh decoder's 128^3 and 256^3 child sets: 226k and 1.81M voxels);
+//  - for every other coordinate, open addressing with linear probing at load
+//    <= 1/4 over 16-byte slots {key lo, key hi, row, tag}.  The key is
+//    (b, x, y, z) packed as four int16 when the coordinate fits (a set with
+//    any other coordinate raises the "wide" flag and its slots are matched
+//    through the input rows instead).
+// The {row, tag} word is claimed with one 64-bit CAS; a second row with the
+// same coordinates lowers it with a 64-bit atomicMin, so every key keeps its
+// smallest row -- std::map::emplace's "first occurrence wins"
+// (sparse_ops.cpp:124-127).
+//
+// A cell or slot belongs to the current build only when its tag equals
+// tag_of(seed, index), and every build draws a new seed: tag_of is a
+// bijection of seed ^ f(index), so nothing written by another build carries
+// the current tag, and the table needs no clearing pass between builds.
+// Memory that never held the table (a zero-filled or fresh workspace) can
+// carry the current tag by chance: mix32(0) == 0, so for every seed exactly
+// one index of a zero-filled table does, and random bytes do at 2^-32 per
+// word.  So no row is ever taken on its tag alone: the insert and the
+// lookup both return (or keep) a word's row r only when r < n and the input
+// row r has the queried coordinates.  A chance word whose row names other
+// coordinates reads as a foreign word (the insert claims it, the lookup
+// moves on or reports a miss); one whose row has the queried coordinates is
+// a row of that key, and the insert's atomicMin still leaves the key's
+// smallest row.  The maps are therefore exact whatever the table holds on
+// entry; the flag words alone are taken on their value, and a raised flag
+// that decides an error (subdivide's duplicate test) is confirmed by an
+// exact pass before it is reported.
+constexpr int kWindowMinLog2 = 6;  // 64 cells per axis
+constexpr int kWindowMaxLog2 = 8;  // 256 cells per axis
+
+
+constexpr int kFlagWide = 2;     // some hashed coordinate does not fit int16
+constexpr int kConfirmWord = 8;  // two counters of the exact recount behind a raised flag
+
+__device__ __host__ __forceinline__ uint32_t mix32(uint32_t h) {
+    h ^= h >> 16;
+    h *= 0x7FEB352Du;
+    h ^= h >> 15;
+    h *= 0x846CA68Bu;
+    h ^= h >> 16;
+    return h;
+}
+__device__ __forceinline__ uint32_t tag_of(uint32_t seed, uint32_t index) {
+    return mix32(seed ^ (index * 0x9E3779B1u));
+}
+__device__ __host__ __forceinline__ int32_t flag_of(uint32_t seed, int k) {
+    return static_cast<int32_t>(mix32(seed + 0x632BE5ABu * static_cast<uint32_t>(k + 1)));
+}
+
+// The window cell of c (x-major, z fastest), or -1.
+__device__ __forceinline__ int32_t window_cell(int4 c, int32_t wlog2) {
+    const uint32_t x = static_cast<uint32_t>(c.y), y = static_cast<uint32_t>(c.z), z = static_cast<uint32_t>(c.w);
+    if (c.x != 0 || (x | y | z) >= (1u << wlog2)) return -1;
+    return static_cast<int32_t>((((x << wlog2) | y) << wlog2) | z);
+}
+
+__device__ __forceinline__ bool fits16(int4 c) {
+    auto f = [](int32_t v) { return v >= -32768 && v <= 32767; };
+    return f(c.x) && f(c.y) && f(c.z) && f(c.w);
+}
+__device__ __forceinline__ uint64_t pack16(int4 c) {
+    return (static_cast<uint64_t>(static_cast<uint16_t>(c.x)) << 48) |
+           (static_cast<uint64_t>(static_cast<uint16_t>(c.y)) << 32) |
+           (static_cast<uint64_t>(static_cast<uint16_t>(c.z)) << 16) | static_cast<uint64_t>(static_cast<uint16_t>(c.w));
+}
+
+// Hash path of kmap_find (coordinates outside the window).
+__device__ __forceinline__ int32_t kmap_hash_find(const KmapHash &h, const int4 *__restrict__ keys, int32_t n, int4 q,
+                                          bool wide) {
+    if (!wide && !fits16(q)) return -1;
+    const uint64_t kq = pack16(q);
+    uint32_t pos = key_hash(q) & h.mask;
+    for (uint32_t probe = 0; probe <= h.mask; ++probe) {
+        const uint4 s = h.slots[pos];
+        if (s.w != tag_of(h.seed, pos)) return -1;
+        // The packed key (when every key fits) screens the probe chain; the
+        // row is returned only after its input coordinates match.
+        if ((wide || ((static_cast<uint64_t>(s.y) << 32) | s.x) == kq) && s.z < static_cast<uint32_t>(n) &&
+            same_key(keys[s.z], q))
+            return static_cast<int32_t>(s.z);
+        pos = (pos + 1) & h.mask;
+    }
+    return -1;
+}
+
+// Smallest row whose key equals q, or -1 (after kmap_insert_kernel).
+__device__ __forceinline__ int32_t kmap_find(const KmapHash &h, const int4 *__restrict__ keys, int32_t n, int4 q,
+                                             bool wide) {
+    const int32_t cell = window_cell(q, h.wlog2);
+    if (cell < 0) return kmap_hash_find(h, keys, n, q, wide);
+    const unsigned long long v = h.cells[cell];
+    const uint32_t r = static_cast<uint32_t>(v);
+    return static_cast<uint32_t>(v >> 32) == tag_of(h.seed, static_cast<uint32_t>(cell)) &&
+                   r < static_cast<uint32_t>(n) && same_key(keys[r], q)
+               ? static_cast<int32_t>(r)
+               : -1;
+}
+
+
+// Map entry (i, o): the first row at coords[i] + delta(o), or `missing`; a
+// later duplicate of a coordinate keeps an all-missing row
+// (sparse_ops.cpp:129-139 only visits each key's first row).
+__device__ __forceinline__ int32_t kmap_entry(const KmapHash &h, const int4 *__restrict__ coords, int32_t n, int32_t i,
+                                              int32_t o, int32_t missing, bool wide, bool dup) {
+    const int4 c = coords[i];
+    const bool owner = !dup || kmap_find(h, coords, n, c, wide) == i;
+    int4 q = c;
+    if (owner && add_fits(c.y, o / 9 - 1, &q.y) && add_fits(c.z, (o / 3) % 3 - 1, &q.z) &&
+        add_fits(c.w, o % 3 - 1, &q.w)) {
+        const int32_t r = kmap_find(h, coords, n, q, wide);
+        if (r >= 0) return r;
+    }
+    return missing;
+}
+__device__ __forceinline__ bool kmap_wide(const KmapHash &h) { return h.flags[kFlagWide] == flag_of(h.seed, kFlagWide); }
+__device__ __forceinline__ bool kmap_dup(const KmapHash &h) {
+    return h.flags[kFlagDuplicate] == flag_of(h.seed, kFlagDuplicate);
+}
+
+}  // namespace
+}  // namespace s3dx

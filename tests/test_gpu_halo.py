@@ -318,3 +318,46 @@ def test_planned_layernorm_modulate_full_size(s3dx, O, W, cin):
         assert np.array_equal(got, yu.download()), f"forward {fwd}: planned != unplanned"
         got = W.bf16_bits_to_f32(got).reshape(n, cout)[rows]
         check_rel(got, O.silu(O.modulate(h, scale, shift)), 1e-2, f"{cin}->{cout} forward {fwd}")
+
+
+@pytest.mark.parametrize("rows", ["128", "64"])
+def test_kmap_planned_one_pass(s3dx, O, W, golden, monkeypatch, rows):
+    # s3dx_kmap_subm3_planned: the kernel map and its gather plan from the
+    # same lookups.  The map is byte-identical to s3dx_kmap_subm3's (golden
+    # SHA on config 2, the oracle on a set with duplicates and coordinates
+    # outside the window, a zeroed workspace under the seed whose tag for an
+    # empty cell next to the set is 0); its plan drives the planned conv to
+    # the same bits as a plan rebuilt from the map and as the unplanned run.
+    from helpers import colliding_seed, set_kmap_seed, sha, window_cell_index
+    arrays, manifest = golden
+    monkeypatch.setenv("S3DX_PLAN_ROWS", rows)
+    base = W.shells_union(0)
+    dup = np.concatenate([base[:9000], base[2000:2600], base[9000:12000] - np.array([0, 20, 0, 0], np.int32)])
+    for name, coords in (("config 2", base), ("duplicates + hashed", np.ascontiguousarray(dup))):
+        n = coords.shape[0]
+        want = O.kmap_subm3(coords, n)
+        conv = _layer(s3dx, W, 128, 128, 48, True)
+        dc = s3dx.DeviceArray.from_host(coords)
+        k_sep = s3dx.DeviceArray.from_host(want)
+        plan_sep = conv.gather_plan(n, k_sep, n)
+        plan_one = conv.gather_plan(n, k_sep, n)
+        k_one = s3dx.DeviceArray((n, 27), np.int32)
+        ws = s3dx.DeviceArray(s3dx.kmap_workspace_size(n), np.uint8)
+        ws.upload(np.zeros(ws.nbytes, np.uint8))
+        if name == "config 2":
+            set_kmap_seed(s3dx, colliding_seed(window_cell_index(27, 22, 46)))
+        s3dx.kmap_subm3_planned(dc, n, n, k_one, plan_one, conv, ws)
+        got = k_one.download()
+        print(f"kmap+plan one pass rows={rows} {name} n={n}: {conv.plan(n, n, plan_one)}", flush=True)
+        assert np.array_equal(got, want), name
+        if name == "config 2":
+            assert sha(got) == manifest["shells_union_s0"]["conv_fine_sha256"]
+        x = W.round_bf16(W.normal_f32(48, 1, (n, 128)))
+        xd = _bf(s3dx, W, x)
+        ys = [s3dx.DeviceArray((n, 128), np.uint16) for _ in range(3)]
+        conv.run(xd, n, k_one, n, ys[0], s3dx.BF16, plan=plan_one)
+        conv.run(xd, n, k_sep, n, ys[1], s3dx.BF16, plan=plan_sep)
+        conv.run(xd, n, k_sep, n, ys[2], s3dx.BF16)
+        a, b, c = (y.download() for y in ys)
+        assert np.array_equal(a, b) and np.array_equal(a, c), name
+        check_rel(_host(W, ys[0]), _oracle(O, W, x, want, n, 128, 128, 48, True), 1e-2, name)
