@@ -369,6 +369,7 @@ struct LaunchPlan {
     int nb = 0, kc = 0;     // 32-column blocks per workgroup, channels per task
     bool linear = false;    // the 1x1-layer kernel (weights resident in LDS)
     bool split = false;     // linear_split_kernel: BF16 rows, three-term BF16 weights
+    bool half_chunk = false;  // halo kernel with a last chunk of 32 channels (64-row tiles only)
     unsigned smem = 0;      // dynamic LDS bytes
     unsigned threads = 256; // workgroup size
     const Tiling *tl = nullptr;
@@ -579,6 +580,11 @@ LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bo
         // S3DX_CONV_HALO=0 keeps the kernels above (tuning, tests).  Layers
         // whose columns come in 96 but not 128 (the mesh decoder's 192 and
         // 96) take 64-row, 96-column tiles when no LayerNorm spans the row.
+        // Cin 32 above a multiple of 64 (the mesh decoder's 96) can run the
+        // 64-row kernel with a half-width last chunk, but only when tiling
+        // 21 is forced: a 64-row tile of Cin 96 holds too little MFMA work
+        // for its staging and four-way reduction, and the split-K kernel is
+        // faster (96 -> 96 on 1.81M rows: 1,247 us against 1,443 us).
         {
             const char *te = std::getenv("S3DX_CONV_TILING");
             const char *he = std::getenv("S3DX_CONV_HALO");
@@ -586,13 +592,14 @@ LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bo
             const bool allowed = te ? (tid == 20 || tid == 21) : !(he && std::atoi(he) == 0);
             const bool nb4 = blocks % 4 == 0 && (!conv->ln || conv->cout == 128);
             const bool nb3 = !nb4 && blocks % 3 == 0 && !conv->ln && tid != 20 && !(he && std::atoi(he) == 128);
-            if (allowed && bf && conv->kvol == kMaxKvol && conv->cin % 64 == 0 && (nb4 || nb3) && !p.xf &&
-                splitk_ok) {
-                const int want = tid == 20 || tid == 21 ? tid : (he && std::atoi(he) == 128 ? 20 : 21);
+            const int want = tid == 20 || tid == 21 ? tid : (he && std::atoi(he) == 128 ? 20 : 21);
+            const bool chunks_ok = conv->cin % 64 == 0 || (conv->cin % 32 == 0 && tid == 21);
+            if (allowed && bf && conv->kvol == kMaxKvol && chunks_ok && (nb4 || nb3) && !p.xf && splitk_ok) {
                 for (const Tiling &t : kTilings)
                     if (t.id == want) p.tl = &t;
                 p.nb = nb3 ? 3 : 4;
                 p.kc = 64;
+                p.half_chunk = conv->cin % 64 != 0;
             }
         }
         p.fused_ln = conv->ln && p.nb * 32 == conv->cout;
@@ -614,7 +621,7 @@ void apply_gather_plan(LaunchPlan &p, const s3dx_gather_plan *g, int64_t n_out, 
     if (bf16_rows || !p.mfma || !p.tl || (p.tl->id != 20 && p.tl->id != 21)) return;
     if (g->rows == 64 && p.tl->id == 21) {
         p.fn = pick_halo_bf16_planned(64, p.nb);
-    } else if (g->rows == 128 && p.nb == 4) {
+    } else if (g->rows == 128 && p.nb == 4 && !p.half_chunk) {
         for (const Tiling &t : kTilings)
             if (t.id == 22) p.tl = &t;
         p.fn = pick_halo_bf16_planned(128);
@@ -632,7 +639,7 @@ int gather_plan_rows(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out) {
         if (r == 64 || r == 128) return r;
     }
     const LaunchPlan p = plan_launch(conv, x_bytes, n_out, true);
-    if (!p.mfma || !p.tl || (p.tl->id != 20 && p.tl->id != 21) || p.nb != 4) return 64;
+    if (!p.mfma || !p.tl || (p.tl->id != 20 && p.tl->id != 21) || p.nb != 4 || p.half_chunk) return 64;
     const int64_t tiles = (n_out + 127) / 128 * static_cast<int64_t>(p.grid.y);
     return tiles <= device_cus() ? 128 : 64;
 }
@@ -937,9 +944,9 @@ void describe_launch(const s3dx_conv *conv, const s3dx_gather_plan *gplan, int64
                           conv->cin / (conv->dtype == S3DX_BF16 || p.split ? 16 : 8),
                           p.split ? " terms=3" : "", conv->ln ? "separate" : "none", p.grid.x);
         else if (p.mfma)
-            std::snprintf(text, sizeof(text), "mfma tiling=%d%s%s rows=%d cols=%d kc=%d xf=%d ln=%s grid=%ux%u",
+            std::snprintf(text, sizeof(text), "mfma tiling=%d%s%s rows=%d cols=%d kc=%d%s xf=%d ln=%s grid=%ux%u",
                           p.tl->id, p.tl->splitk ? " split-k" : "", halo ? " halo" : "", p.tl->rows(),
-                          halo ? p.nb * 32 : p.tl->cols(), p.kc,
+                          halo ? p.nb * 32 : p.tl->cols(), p.kc, p.half_chunk ? "+32" : "",
                           p.xf ? 1 : 0, conv->ln ? (p.fused_ln ? "fused" : "separate") : "none", p.grid.x,
                           p.grid.y);
         else

@@ -353,7 +353,11 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_halo_kernel(ConvArg
     const int nb0 = blockIdx.y * NB;
     const int nbtot = a.cout_pad / 32;
     const int ksteps_total = a.cin / 16;
-    const int chunks = a.cin / kHChunk;
+    // Cin a multiple of 64, or (64-row tiles) 32 more: the last chunk then
+    // holds two k-steps, and wave w takes k-step w & 1 of it on every other
+    // present offset (parity w >> 1), so the four waves still share it.
+    const int chunks = (a.cin + kHChunk - 1) / kHChunk;
+    const bool half_last = a.cin % kHChunk != 0;
     const int tile_rows = static_cast<int>(min(static_cast<int64_t>(ROWS), a.n_out - m0));
     const int32_t xbytes = static_cast<int32_t>(a.x_bytes < INT32_MAX ? a.x_bytes : INT32_MAX);
     const int64_t w_bytes = static_cast<int64_t>(kMaxKvol) * a.cin * a.cout_pad * 2;
@@ -411,12 +415,6 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_halo_kernel(ConvArg
     // below 27, so bit 31 is free: the ctz of rest | bit 31 is 31 exactly
     // when rest is empty (testing rest itself beside rest - 1 would turn
     // into a vector subtract and a readfirstlane).
-    const int olast = ntasks > 0 ? 31 - __builtin_clz(mask) : 0;
-    auto advance = [&](uint32_t &rest) __attribute__((always_inline)) {
-        const int c = __builtin_ctz(rest | 0x80000000u);
-        rest &= rest - 1u;
-        return c == 31 ? olast : c;
-    };
     auto mfmas = [&](const uint4 (&af)[MB], const uint4 (&bf)[NB]) __attribute__((always_inline)) {
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb)
@@ -429,7 +427,28 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_halo_kernel(ConvArg
     auto chunk_loop = [&](auto ga) __attribute__((always_inline)) {
         constexpr bool GA = decltype(ga)::value;
         for (int c = 0; c < chunks && ntasks > 0; ++c) {
-            const int ks = c * 4 + wave;  // this wave's k-step over the whole Cin
+            const bool hc = half_last && c == chunks - 1;
+            const int kl = hc ? (wave & 1) : wave;  // this wave's k-step within the chunk
+            const int ks = c * 4 + kl;             // and over the whole Cin
+            // This wave's offsets in chunk c: every present one, or in a
+            // half-width chunk every other one (parity wave >> 1).
+            uint32_t cmask = mask;
+            if (hc) {
+                cmask = 0u;
+                int k = 0;
+                for (uint32_t r = mask; r != 0u; r &= r - 1u, ++k)
+                    if ((k & 1) == (wave >> 1)) cmask |= r & (0u - r);
+            }
+            const int cn = __popc(cmask);
+            const int olast = cn > 0 ? 31 - __builtin_clz(cmask) : 0;
+            auto advance = [&](uint32_t &rest) __attribute__((always_inline)) {
+                const int o = __builtin_ctz(rest | 0x80000000u);
+                rest &= rest - 1u;
+                return o == 31 ? olast : o;
+            };
+            // channels of chunk c that exist (the half chunk's upper 32 are
+            // never read; their copy pieces are zero fills)
+            const int cpieces = hc ? (a.cin - c * kHChunk) / 8 : 8;
             if constexpr (!GA) {
                 if (c > 0) __syncthreads();  // every wave is done with chunk c-1
                 // ---- 5. chunk c of every distinct row into its slot,
@@ -447,7 +466,7 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_halo_kernel(ConvArg
                     for (int k = 0; k < 4; ++k) {
                         const int s = (g0 + 4 * k) * 8 + (lane >> 3);
                         const int p = (lane & 7) ^ halo_swizzle(s);
-                        off[k] = s < static_cast<int>(distinct)
+                        off[k] = s < static_cast<int>(distinct) && p < cpieces
                                      ? (slot_row[min(s, CAP - 1)] * static_cast<uint32_t>(a.cin) + c * kHChunk +
                                         p * 8) * 2u
                                      : 0x80000000u;  // past the buffer: zeros
@@ -499,7 +518,7 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_halo_kernel(ConvArg
                         const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, static_cast<int32_t>(off), 0, 0);
                         af[mb] = make_uint4(v.x, v.y, v.z, v.w);
                     } else {
-                        const int p = 2 * wave + half;
+                        const int p = 2 * kl + half;
                         af[mb] = *reinterpret_cast<const uint4 *>(halo + ix[mb] * kHRowBytes + ((p ^ halo_swizzle(ix[mb])) << 4));
                     }
                 }
@@ -509,7 +528,7 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_halo_kernel(ConvArg
             constexpr int R = MB == 2 ? 4 : 3;
             uint4 bq[R][NB], aq[R][MB];
             int iq[R][MB];
-            uint32_t rest_i = mask, rest_b = mask;
+            uint32_t rest_i = cmask, rest_b = cmask;
             // (issued in the loop's order, so the wait counts at the loop
             // head match the steady state)
 #pragma unroll
@@ -535,7 +554,7 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_halo_kernel(ConvArg
                 sched_fence();
             };
             int t = 0;
-            for (; t + R <= ntasks; t += R) {
+            for (; t + R <= cn; t += R) {
                 body(std::integral_constant<int, 0>{});
                 body(std::integral_constant<int, 1>{});
                 body(std::integral_constant<int, 2>{});
@@ -543,7 +562,7 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_halo_kernel(ConvArg
             }
             // Fewer than R tasks left: set k holds task t+k's weights; the
             // A of task t is in set 0 and the slots of task t+1 in set 1.
-            const int left = ntasks - t;
+            const int left = cn - t;
             if (left >= 1) mfmas(aq[0], bq[0]);
             if (left >= 2) {
                 load_a(iq[1], aq[1]);

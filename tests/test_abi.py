@@ -127,8 +127,13 @@ def test_conv_plan_names_the_launched_kernel(s3dx, monkeypatch):
     # The 10,366-voxel sphere shell: 81 x 2 tiles of 128 x 32 would leave CUs
     # idle; FP32 32-column tiles then take 32 rows each.
     assert f64.plan(10366, 10366) == "mfma tiling=24 split-k rows=32 cols=32 kc=64 xf=0 ln=none grid=324x2"
-    # 96 bf16 channels: four 32-channel chunks make each 128-channel task.
+    # 96 bf16 channels: four 32-channel chunks make each 128-channel task;
+    # forced, the 64-row halo kernel with a half-width last chunk.
     assert s3dx.SparseConv(96, 96, 27, s3dx.BF16).plan(n, n).startswith("mfma tiling=15 split-k rows=128 cols=96 kc=32")
+    monkeypatch.setenv("S3DX_CONV_TILING", "21")
+    assert s3dx.SparseConv(96, 96, 27, s3dx.BF16).plan(n, n) == \
+        "mfma tiling=21 split-k halo rows=64 cols=96 kc=64+32 xf=0 ln=none grid=442x1"
+    monkeypatch.delenv("S3DX_CONV_TILING")
     # 192 output columns without LayerNorm: two 96-column tiles of the
     # 64-row halo kernel (the split-K kernels with S3DX_CONV_HALO=0: 64-row
     # tiles, two per CU, as there are more 128-row tiles than CUs).

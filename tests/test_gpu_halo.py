@@ -361,3 +361,48 @@ def test_kmap_planned_one_pass(s3dx, O, W, golden, monkeypatch, rows):
         a, b, c = (y.download() for y in ys)
         assert np.array_equal(a, b) and np.array_equal(a, c), name
         check_rel(_host(W, ys[0]), _oracle(O, W, x, want, n, 128, 128, 48, True), 1e-2, name)
+
+
+HALF_CHUNK = {
+    # name: (coords builder, cin, cout) -- Cin 32 above a multiple of 64
+    "shells_union_3000_96_96": (lambda W: W.shells_union(1)[:3000], 96, 96),
+    "shells_union_3000_96_192": (lambda W: W.shells_union(1)[:3000], 96, 192),
+    "shells_union_3000_160_128": (lambda W: W.shells_union(1)[:3000], 160, 128),
+    "shuffled_cube_13824_96_96": (lambda W: _dense_cube(24, 0), 96, 96),          # every tile global
+    "half_shuffled_cube_13824_96_96": (lambda W: _dense_cube(24, 6912), 96, 96),  # both modes
+    "isolated_points_96_96": (lambda W: _sparse_points(3, False), 96, 96),       # one offset: waves 2, 3 idle
+    "point_pairs_96_128": (lambda W: _sparse_points(4, True), 96, 128),           # three offsets
+    "tiny_37_96_96": (lambda W: W.shells_union(2)[:37], 96, 96),                  # one partial tile
+}
+
+
+@pytest.mark.parametrize("plan_rows", ["64", "128"])
+@pytest.mark.parametrize("case", list(HALF_CHUNK))
+def test_half_width_last_chunk(s3dx, O, W, monkeypatch, case, plan_rows):
+    # The 64-row halo kernel with Cin 32 above a multiple of 64 (forced:
+    # split-K is the default there): the last chunk's two k-steps split
+    # over the four waves by offset parity.  Planned == unplanned bit for bit
+    # (a 128-row plan is not used by this kernel and leaves the launch as it
+    # is), both against the oracle.
+    monkeypatch.setenv("S3DX_CONV_TILING", "21")
+    monkeypatch.delenv("S3DX_CONV_HALO", raising=False)
+    monkeypatch.setenv("S3DX_PLAN_ROWS", plan_rows)
+    build, cin, cout = HALF_CHUNK[case]
+    coords = build(W)
+    n = coords.shape[0]
+    kmap = O.kmap_subm3(coords, n)
+    conv = _layer(s3dx, W, cin, cout, 47, False)
+    x = W.round_bf16(W.normal_f32(47, 1, (n, cin)))
+    res = W.round_bf16(W.normal_f32(47, 4, (n, cout)))
+    xd, kd, rd = _bf(s3dx, W, x), s3dx.DeviceArray.from_host(kmap), _bf(s3dx, W, res)
+    gp = conv.gather_plan(n, kd, n)
+    plan_text, planned = conv.plan(n, n), conv.plan(n, n, gp)
+    print(f"{case} n={n} plan rows {plan_rows}: {plan_text} | {planned}", flush=True)
+    cols = 128 if cout % 128 == 0 else 96
+    assert plan_text.startswith(f"mfma tiling=21 split-k halo rows=64 cols={cols} kc=64+32"), plan_text
+    assert planned == (plan_text + " plan=64" if plan_rows == "64" else plan_text), planned
+    y0, y1 = s3dx.DeviceArray((n, cout), np.uint16), s3dx.DeviceArray((n, cout), np.uint16)
+    conv.run(xd, n, kd, n, y0, s3dx.BF16, rd)
+    conv.run(xd, n, kd, n, y1, s3dx.BF16, rd, plan=gp)
+    assert np.array_equal(y0.download(), y1.download())
+    check_rel(_host(W, y1), _oracle(O, W, x, kmap, n, cin, cout, 47, False, res), 1e-2, case)
