@@ -333,9 +333,16 @@ KernelFn tiling_kernel(int id, bool bf, int kc, bool xf) {
 // workgroup per CU.  S3DX_CONV_TILING=<id> overrides (tuning).
 // splitk_ok: the packed weights fit the split-K kernel's 32-bit buffer
 // offsets (< 2 GiB).
-const Tiling *choose_tiling(int64_t n_out, int nb, int ntiles, bool bf, int kc, bool xf, bool splitk_ok) {
+// Task channels tiling `id` runs at for kc: tiling 11 takes at most 64
+// (BF16) or 32 (FP32) channels, where its 128 x 128 tiles do not spill.
+int tiling_kc(int id, bool bf, int kc, int cin) {
+    const int cap = bf ? 64 : 32;
+    return id == 11 && kc > cap && cin % cap == 0 ? cap : kc;
+}
+
+const Tiling *choose_tiling(int64_t n_out, int nb, int ntiles, bool bf, int kc, bool xf, bool splitk_ok, int cin) {
     auto usable = [&](const Tiling &t) {
-        return t.cols() == nb * 32 && (splitk_ok || !t.splitk) && tiling_kernel(t.id, bf, kc, xf);
+        return t.cols() == nb * 32 && (splitk_ok || !t.splitk) && tiling_kernel(t.id, bf, tiling_kc(t.id, bf, kc, cin), xf);
     };
     if (const char *e = std::getenv("S3DX_CONV_TILING")) {
         const int id = std::atoi(e);
@@ -490,13 +497,20 @@ LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bo
         const int blocks = conv->cout_pad / 32;
         int forced = 0;
         if (const char *e = std::getenv("S3DX_CONV_NB")) forced = std::atoi(e);
+        // S3DX_CONV_KC=<channels> overrides the task width where the layer
+        // allows it (tuning).
+        int forced_kc = 0;
+        if (const char *e = std::getenv("S3DX_CONV_KC")) forced_kc = std::atoi(e);
         auto try_nb = [&](int nb) {
-            const int kc = task_channels(conv->cin, nb, bf);
+            int kc = task_channels(conv->cin, nb, bf);
             if (kc == 0) return false;
-            const Tiling *t = choose_tiling(n_out, nb, blocks / nb, bf, kc, p.xf, splitk_ok);
+            if ((forced_kc == 32 || forced_kc == 64 || forced_kc == 128) && forced_kc <= kc &&
+                conv->cin % forced_kc == 0)
+                kc = forced_kc;
+            const Tiling *t = choose_tiling(n_out, nb, blocks / nb, bf, kc, p.xf, splitk_ok, conv->cin);
             if (!t) return false;
             p.nb = nb;
-            p.kc = kc;
+            p.kc = tiling_kc(t->id, bf, kc, conv->cin);
             p.tl = t;
             return true;
         };
@@ -520,24 +534,25 @@ LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bo
                     if (!found && nb < conv->nb && blocks % nb == 0 && try_nb(nb)) found = p.tl->splitk;
                 if (!found) p = whole;
             }
-            // 128-column BF16 tiles: 64-row tiles with two workgroups per CU
-            // overlap one workgroup's gathers, barriers and epilogue with the
-            // other's MFMAs.  More 128-row tiles than one pass over the CUs:
-            // 128-channel tasks (tiling 17; shortens the last pass, config 3
-            // ~15%); one reasonably full pass: 64-channel tasks (tiling 18,
-            // fewer registers; config 2 ~5%).
+            // 128-column tiles: 64-row tiles with two workgroups per CU
+            // (tiling 18, half-width tasks) overlap one workgroup's gathers,
+            // barriers and epilogue with the other's MFMAs, once there are at
+            // least half as many 128-row tiles as CUs (config 2 ~5%).  (A
+            // 128-channel-task variant spilled 16 VGPRs and ran the 128 ->
+            // 1024 skip on 5,086 rows in 13.1 us against 11.1 us here.)
             if (p.tl->id == 11 && forced == 0 && !std::getenv("S3DX_CONV_TILING")) {
                 const int64_t rt = (n_out + 127) / 128;
                 const int64_t cus = device_cus(), tiles = rt * (blocks / p.nb);
                 const int kc18 = bf ? 64 : 32;  // half-width tasks
-                const int id = tiles > cus ? 17 : (2 * tiles >= cus && conv->cin % kc18 == 0 ? 18 : 0);
-                const int kc = id == 18 ? kc18 : p.kc;
-                if (id != 0 && tiling_kernel(id, bf, kc, p.xf)) {
+                if (2 * tiles >= cus && conv->cin % kc18 == 0 && tiling_kernel(18, bf, kc18, p.xf)) {
                     for (const Tiling &t : kTilings)
-                        if (t.id == id) p.tl = &t;
-                    p.kc = kc;
+                        if (t.id == 18) p.tl = &t;
+                    p.kc = kc18;
                 }
             }
+            // (Tiling 11 runs 64-channel BF16 or 32-channel FP32 tasks, see
+            // tiling_kc: the wider ones spilled 8-12 bytes a lane and ran no
+            // faster -- FP32 1024 -> 1024 on 5,086 rows: 3,300 us either way.)
             // Joined-chunk 96-column tasks (15) over more 128-row tiles than
             // one pass over the CUs: the same kernel with 64-row tiles, two
             // workgroups per CU (19).
@@ -590,7 +605,10 @@ LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bo
             const char *he = std::getenv("S3DX_CONV_HALO");
             const int tid = te ? std::atoi(te) : 0;
             const bool allowed = te ? (tid == 20 || tid == 21) : !(he && std::atoi(he) == 0);
-            const bool nb4 = blocks % 4 == 0 && (!conv->ln || conv->cout == 128);
+            // A LayerNorm the split-K tile could not fuse either (its tile
+            // narrower than the row) runs as its own pass after the halo kernel.
+            const bool ln_ok = !conv->ln || conv->cout == 128 || p.nb * 32 != conv->cout;
+            const bool nb4 = blocks % 4 == 0 && ln_ok;
             const bool nb3 = !nb4 && blocks % 3 == 0 && !conv->ln && tid != 20 && !(he && std::atoi(he) == 128);
             const int want = tid == 20 || tid == 21 ? tid : (he && std::atoi(he) == 128 ? 20 : 21);
             const bool chunks_ok = conv->cin % 64 == 0 || (conv->cin % 32 == 0 && tid == 21);

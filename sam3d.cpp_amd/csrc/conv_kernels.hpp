@@ -56,7 +56,7 @@ inline constexpr Tiling kTilings[] = {
     {0, 1, 1, 1, 0}, {1, 1, 1, 2, 0}, {2, 1, 3, 1, 0}, {3, 1, 2, 2, 0}, {4, 1, 3, 2, 0},
     {5, 1, 4, 2, 0}, {6, 2, 1, 2, 0}, {7, 2, 3, 1, 0}, {8, 2, 2, 2, 0}, {9, 2, 3, 2, 0},
     {10, 1, 4, 1, 0}, {11, 4, 4, 1, 1}, {12, 4, 2, 1, 1}, {13, 4, 3, 1, 1}, {14, 4, 1, 1, 1},
-    {15, 4, 3, 1, 1}, {16, 4, 4, 1, 1}, {17, 2, 4, 1, 1}, {18, 2, 4, 1, 1},
+    {15, 4, 3, 1, 1}, {16, 4, 4, 1, 1}, {18, 2, 4, 1, 1},
     {19, 2, 3, 1, 1}, {20, 4, 4, 1, 1}, {21, 2, 4, 1, 1}, {22, 4, 4, 1, 1},
     {23, 2, 1, 1, 1}, {24, 1, 1, 1, 1},
 };
@@ -1633,7 +1633,12 @@ KernelFn pick_tiling(int id) {
     case 11: case 12: case 13: case 14: {
         constexpr int KS = KC / (2 * Frag<T>::E);
         if constexpr (KS % 4 == 0) {
-            if (id == 11) return conv_splitk_kernel<T, 4, KC, XF, 1, 4>;
+            // 128 x 128 tiles with 128-channel BF16 or 64-channel FP32 tasks
+            // spill: not built (the host takes 64 / 32 channels for tiling 11).
+            if (id == 11) {
+                if constexpr (sizeof(T) == 2 ? KC <= 64 : KC <= 32) return conv_splitk_kernel<T, 4, KC, XF, 1, 4>;
+                else return nullptr;
+            }
             if (id == 12) return conv_splitk_kernel<T, 2, KC, XF, 1, 4>;
             if (id == 13) return conv_splitk_kernel<T, 3, KC, XF, 1, 4>;
             return conv_splitk_kernel<T, 1, KC, XF, 1, 4>;
@@ -1662,13 +1667,11 @@ KernelFn pick_tiling(int id) {
         else
             return nullptr;
     }
-    case 17: case 18: {  // 64-row tiles, two workgroups per CU (18: half-width tasks)
-        if constexpr (sizeof(T) == 2 && XF == 0 && KC == 128)
-            return id == 17 ? conv_splitk_kernel<T, 4, 128, XF, 1, 2> : nullptr;
-        else if constexpr (sizeof(T) == 2 && XF == 0 && KC == 64)
-            return id == 18 ? conv_splitk_kernel<T, 4, 64, XF, 1, 2> : nullptr;
+    case 18: {  // 64-row tiles, two workgroups per CU, half-width tasks
+        if constexpr (sizeof(T) == 2 && XF == 0 && KC == 64)
+            return conv_splitk_kernel<T, 4, 64, XF, 1, 2>;
         else if constexpr (sizeof(T) == 4 && XF == 0 && KC == 32)
-            return id == 18 ? conv_splitk_kernel<T, 4, 32, XF, 1, 2> : nullptr;
+            return conv_splitk_kernel<T, 4, 32, XF, 1, 2>;
         else
             return nullptr;
     }

@@ -282,7 +282,7 @@ def test_deterministic_and_empty_rows(s3dx, O, W):
 
 TILINGS = {  # cout -> tiling ids whose workgroup spans the whole row (11-14, 23, 24: split-K; 20, 21: halo)
     32: ["0", "14", "23", "24"], 64: ["1", "6", "12"], 96: ["2", "7", "13"],
-    128: ["3", "8", "10", "11", "17", "18", "20", "21"],
+    128: ["3", "8", "10", "11", "18", "20", "21"],
     192: ["4", "9"], 256: ["5"]}
 
 
