@@ -64,6 +64,9 @@ def parse():
     p.add_argument("--profile-only", action="store_true",
                    help="run --steps untimed steps (kernel map + BF16 block) and exit: a short "
                         "program for counter collection")
+    p.add_argument("--profile-kmap", action="store_true",
+                   help="run --steps untimed kernel maps on each of the mesh decoder's child sets "
+                        "(226,120 and 1,808,960 voxels) and exit: for counter collection")
     return p.parse_args()
 
 
@@ -491,6 +494,23 @@ def mesh_stack(s3dx, W, stream, seed, d0, p0, ch0, k0):
                     "subdivides (children + child kernel maps) that build their tables"}
 
 
+def profile_kmap(s3dx, W, seed, steps):
+    """Kernel maps (mesh sentinel) on the 128^3 and 256^3 child sets of the
+    8-shell union, `steps` builds each, untimed."""
+    stream = s3dx.Stream()
+    c = W.shells_union(seed)
+    d = s3dx.DeviceArray.from_host(c, stream)
+    ch, _ = s3dx.subdivide2(d, c.shape[0], False, stream)
+    ch1, _ = s3dx.subdivide2(ch, 8 * c.shape[0], False, stream)
+    for cset, n in ((ch, 8 * c.shape[0]), (ch1, 64 * c.shape[0])):
+        km = s3dx.DeviceArray((n, 27), np.int32)
+        ws = s3dx.DeviceArray(s3dx.kmap_workspace_size(n), np.uint8)
+        for _ in range(steps):
+            s3dx.kmap_subm3(cset, n, -1, km, ws, stream)
+        stream.synchronize()
+        print(json.dumps({"profile_kmap_voxels": n, "builds": steps}), flush=True)
+
+
 def copy_calibration(s3dx):
     n = 64 * 1024 * 1024  # 256 MiB of f32
     a = s3dx.DeviceArray((n,), np.float32)
@@ -585,6 +605,9 @@ def main():
     W = s3dx.workloads
     if args.copy_calibration:
         copy_calibration(s3dx)
+        return
+    if args.profile_kmap:
+        profile_kmap(s3dx, W, args.seed, args.steps)
         return
     c = args.channels
     coords = W.shells_union(args.seed)
