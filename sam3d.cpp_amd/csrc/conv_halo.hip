@@ -818,15 +818,16 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
     };
     // Before chunk c's tasks its halo copy has landed and every wave is past
     // chunk c-1; with two buffers the copy of chunk c+1 then goes into the
-    // buffer chunk c-1 used.  NB weight loads were issued after the copy of
-    // chunk c (the first NB of the loop for c = 0, the last NB of chunk c-1's
-    // tasks otherwise), so vmcnt(NB) covers the copy; few_tasks: chunk c-1
-    // issued fewer than NB loads after the copy.
-    auto chunk_sync = [&](int c, auto nb, bool few_tasks, char *cur, char *nxt, const uint32_t *rows,
+    // buffer chunk c-1 used.  When NB weight loads were issued after the copy
+    // of chunk c (the first NB of the cursor for c = 0, the last NB of chunk
+    // c-1's tasks otherwise) vmcnt(NB) covers the copy; `few`: fewer were
+    // (the cursor ran past the last chunk, or chunk c-1 had fewer tasks), so
+    // wait for every load.
+    auto chunk_sync = [&](int c, auto nb, bool few, char *cur, char *nxt, const uint32_t *rows,
                           const char *xg) __attribute__((always_inline)) {
         constexpr int NB = decltype(nb)::value;
         if (dbl) {
-            if (c == 0 || !few_tasks) __builtin_amdgcn_s_waitcnt(vmcnt_imm(NB));
+            if (!few) __builtin_amdgcn_s_waitcnt(vmcnt_imm(NB));
             else __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
             __syncthreads();
             if (c + 1 < chunks) halo_copy(c + 1, nxt, rows, xg);
@@ -835,8 +836,10 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
                 __syncthreads();
                 halo_copy(c, cur, rows, xg);
                 __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
-            } else {
+            } else if (!few) {
                 __builtin_amdgcn_s_waitcnt(vmcnt_imm(NB));
+            } else {
+                __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
             }
             __syncthreads();
         }
@@ -882,7 +885,11 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
         }
         auto chunk = [&](int c, char *__restrict__ buf, char *__restrict__ nxt, const int32_t *__restrict__ tbl,
                          const uint32_t *__restrict__ rows, const char *__restrict__ xg) __attribute__((always_inline)) {
-            if constexpr (!GA) chunk_sync(c, std::integral_constant<int, 2 * R>{}, ntasks < R, buf, nxt, rows, xg);
+            // (loads after chunk c's copy: for c = 0 the cursor's first R
+            // sets, fewer when the tile has fewer than R (chunk, offset) tasks)
+            if constexpr (!GA)
+                chunk_sync(c, std::integral_constant<int, 2 * R>{}, c == 0 ? ntasks * chunks < R : ntasks < R, buf,
+                           nxt, rows, xg);
             const int kch = (c * 4 + ks) * 16 + half * 8;  // this lane's first channel of the A fragment
             auto load_idx = [&](int o, int (&ix)[4]) __attribute__((always_inline)) {
 #pragma unroll

@@ -70,6 +70,10 @@ def _sparse_points(step, pair):
 CASES = {
     # name: (coords builder, cin, cout, LayerNorm+SiLU+residual)
     "isolated_points_cin256": (lambda W: _sparse_points(3, False), 256, 128, True),  # fewer tasks than in flight
+    # one offset and one or two chunks: fewer weight loads than the wait
+    # before chunk 0 counts on (the copy must still have landed)
+    "isolated_points_cin128": (lambda W: _sparse_points(3, False), 128, 128, True),
+    "isolated_points_cin64": (lambda W: _sparse_points(3, False), 64, 128, False),
     "point_pairs_cin256": (lambda W: _sparse_points(4, True), 256, 128, False),
     "shells_union_28265": (lambda W: W.shells_union(0), 128, 128, True),
     "shells_union_3000_cin256": (lambda W: W.shells_union(1)[:3000], 256, 128, False),
