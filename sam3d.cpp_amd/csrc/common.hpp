@@ -150,6 +150,16 @@ __device__ inline void store_from_f32<uint16_t>(uint16_t *p, float v) {
     *p = f32_to_bf16(v);
 }
 
+// Workgroups are dealt round-robin over the 8 XCDs; workgroup `bid` of
+// `nblocks` takes logical index xcd_tile(bid, nblocks), so that each XCD runs a
+// contiguous run of logical indices (row tiles, voxel ranges) and neighbouring
+// accesses share its L2.
+__device__ __forceinline__ int xcd_tile(int bid, int nblocks) {
+    const int q = nblocks / 8, r = nblocks % 8;
+    const int xcd = bid % 8, local = bid / 8;
+    return xcd * q + min(xcd, r) + local;
+}
+
 // x * sigmoid(x) with the hardware exponential and reciprocal (a few ulp; a
 // large negative x gives exp = inf, rcp = 0, result -0).
 __device__ inline float silu(float v) { return v * __builtin_amdgcn_rcpf(1.0f + __expf(-v)); }

@@ -1250,7 +1250,7 @@ __device__ __forceinline__ void plan_tile(Fetch fetch, int64_t n_out, int64_t n_
     __shared__ __align__(16) uint32_t prefix[SM::BITWORDS];
     __shared__ __align__(16) uint32_t slot_row[SM::CAP];
     __shared__ __align__(16) int32_t misc[4 + NTH / 64];
-    const int tile = blockIdx.x, tid = threadIdx.x;
+    const int tile = xcd_tile(blockIdx.x, gridDim.x), tid = threadIdx.x;
     const int64_t m0 = static_cast<int64_t>(tile) * ROWS;
     const int tile_rows = static_cast<int>(min(static_cast<int64_t>(ROWS), n_out - m0));
     // The tables come back in entry order (row-major, 27 per row: no LDS

@@ -101,14 +101,6 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kMaxKvol = 27;
 
-// Workgroups are dealt round-robin over the 8 XCDs; give each XCD a
-// contiguous run of row tiles so neighbouring gathers share its L2.
-__device__ __forceinline__ int xcd_tile(int bid, int nblocks) {
-    const int q = nblocks / 8, r = nblocks % 8;
-    const int xcd = bid % 8, local = bid / 8;
-    return xcd * q + min(xcd, r) + local;
-}
-
 template <class T>
 struct Frag;
 template <>

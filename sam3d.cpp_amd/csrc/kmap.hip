@@ -61,7 +61,9 @@ __device__ __forceinline__ void kmap_hash_insert(const int4 *__restrict__ keys, 
 // i, or lower the row of the one already holding its key.
 __global__ void __launch_bounds__(kThreads)
 kmap_insert_kernel(const int4 *__restrict__ keys, int32_t n, KmapHash h) {
-    const int32_t i = blockIdx.x * kThreads + threadIdx.x;
+    // (voxel ranges per XCD as the lookups take them: their cells and rows
+    // stay in that XCD's L2)
+    const int32_t i = xcd_tile(blockIdx.x, gridDim.x) * kThreads + threadIdx.x;
     if (i >= n) return;
     const int4 c = keys[i];
     const int32_t cell = window_cell(c, h.wlog2);
@@ -92,7 +94,7 @@ kmap_insert_kernel(const int4 *__restrict__ keys, int32_t n, KmapHash h) {
 __global__ void __launch_bounds__(kThreads)
 kmap_lookup_kernel(const int4 *__restrict__ coords, int32_t n, KmapHash h, int32_t missing,
                    int32_t *__restrict__ kmap) {
-    const int32_t g = blockIdx.x * kThreads + threadIdx.x;
+    const int32_t g = xcd_tile(blockIdx.x, gridDim.x) * kThreads + threadIdx.x;
     if (g >= n * 27) return;
     const int32_t i = g / 27;
     kmap[g] = kmap_entry(h, coords, n, i, g - i * 27, missing, kmap_wide(h), kmap_dup(h));
