@@ -1290,69 +1290,7 @@ __global__ void __launch_bounds__(NTH) gather_plan_build_kernel(const int32_t *k
 
 // The tile's map slice computed by the lookups of the kernel map (and stored
 // into it) instead of read back: the map and its gather plan in one pass.
-struct SliceLookup {
-    const int4 *coords;
-    int32_t n, missing;
-    KmapHash h;
-    bool wide, dup;
-    int32_t *kmap;
-    __device__ __forceinline__ int4 operator()(int64_t m0, int u, int count) const {
-        // The four entries' loads go out together, step by step (coordinates,
-        // window cells, then the rows' coordinates that confirm them); an
-        // entry outside the window, or any entry when the set holds
-        // duplicates, takes the general kmap_entry instead.
-        int e[4], i[4], o[4], cell[4];
-        int4 c[4];
-        const int64_t g0 = m0 * kMaxKvol + 4 * u;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            const int64_t g = g0 + k;
-            i[k] = static_cast<int32_t>(g / kMaxKvol);
-            o[k] = static_cast<int32_t>(g - int64_t(i[k]) * kMaxKvol);
-        }
-#pragma unroll
-        for (int k = 0; k < 4; ++k) c[k] = 4 * u + k < count ? coords[i[k]] : make_int4(-1, 0, 0, 0);
-        unsigned long long v[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            int4 q = c[k];
-            cell[k] = -1;
-            if (add_fits(c[k].y, o[k] / 9 - 1, &q.y) && add_fits(c[k].z, (o[k] / 3) % 3 - 1, &q.z) &&
-                add_fits(c[k].w, o[k] % 3 - 1, &q.w))
-                cell[k] = window_cell(q, h.wlog2);
-            c[k] = q;
-            v[k] = cell[k] >= 0 ? h.cells[cell[k]] : 0ull;
-        }
-        int4 rc[4];
-        uint32_t r[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            r[k] = static_cast<uint32_t>(v[k]);
-            const bool tagged = cell[k] >= 0 && static_cast<uint32_t>(v[k] >> 32) ==
-                                                    tag_of(h.seed, static_cast<uint32_t>(cell[k]));
-            if (!tagged || r[k] >= static_cast<uint32_t>(n)) r[k] = 0xFFFFFFFFu;
-            rc[k] = r[k] != 0xFFFFFFFFu ? coords[r[k]] : make_int4(0, 0, 0, 0);
-        }
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            if (4 * u + k >= count) {
-                e[k] = -1;
-            } else if (dup || cell[k] < 0) {
-                e[k] = kmap_entry(h, coords, n, i[k], o[k], missing, wide, dup);
-            } else {
-                e[k] = r[k] != 0xFFFFFFFFu && same_key(rc[k], c[k]) ? static_cast<int32_t>(r[k]) : missing;
-            }
-        }
-        if (4 * u + 3 < count) {
-            *reinterpret_cast<int4 *>(kmap + g0) = make_int4(e[0], e[1], e[2], e[3]);
-        } else {
-#pragma unroll
-            for (int k = 0; k < 3; ++k)
-                if (4 * u + k < count) kmap[g0 + k] = e[k];
-        }
-        return make_int4(e[0], e[1], e[2], e[3]);
-    }
-};
+using SliceLookup = KmapLookup4;
 
 template <int MB, int NTH>
 __global__ void __launch_bounds__(NTH) kmap_plan_kernel(const int4 *coords, int32_t n, KmapHash h, int32_t missing,

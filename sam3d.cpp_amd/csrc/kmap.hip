@@ -100,6 +100,19 @@ kmap_lookup_kernel(const int4 *__restrict__ coords, int32_t n, KmapHash h, int32
     kmap[g] = kmap_entry(h, coords, n, i, g - i * 27, missing, kmap_wide(h), kmap_dup(h));
 }
 
+// Four map entries per thread (KmapLookup4): each thread's loads in flight
+// together (a lookup is a chain of three dependent loads) and one 16-byte
+// store.  kmap 16-byte aligned.
+__global__ void __launch_bounds__(kThreads)
+kmap_lookup4_kernel(const int4 *__restrict__ coords, int32_t n, KmapHash h, int32_t missing,
+                    int32_t *__restrict__ kmap) {
+    const int32_t u = xcd_tile(blockIdx.x, gridDim.x) * kThreads + threadIdx.x;
+    const int32_t count = n * 27;
+    if (int64_t(4) * u >= count) return;
+    const KmapLookup4 lookup{coords, n, missing, h, kmap_wide(h), kmap_dup(h), kmap};
+    lookup(0, u, count);
+}
+
 // ---- subdivide ------------------------------------------------------------
 // For child slot ch (bits bx,by,bz) and offset o, the neighbour lives in the
 // parent at parent-offset kAdjOffset and at child slot kAdjChild
@@ -215,8 +228,14 @@ void run_kmap(const int4 *coords, int32_t n, int32_t missing, int32_t *kmap, Kma
     h.seed = next_seed();
     kmap_insert_kernel<<<blocks_for(n), kThreads, 0, stream>>>(coords, n, h);
     launch_check("kmap_insert");
-    kmap_lookup_kernel<<<blocks_for(static_cast<int64_t>(n) * 27), kThreads, 0, stream>>>(coords, n, h, missing,
-                                                                                           kmap);
+    // (four entries a thread pays on large sets: 183 -> 174 us at 1.81M
+    // voxels; at 28k voxels one entry a thread is 2% faster)
+    if (aligned(kmap, 16) && n > (int32_t(1) << 17))
+        kmap_lookup4_kernel<<<blocks_for((static_cast<int64_t>(n) * 27 + 3) / 4), kThreads, 0, stream>>>(
+            coords, n, h, missing, kmap);
+    else
+        kmap_lookup_kernel<<<blocks_for(static_cast<int64_t>(n) * 27), kThreads, 0, stream>>>(coords, n, h, missing,
+                                                                                               kmap);
     launch_check("kmap_lookup");
 }
 
