@@ -145,8 +145,11 @@ S3DX_API s3dx_status s3dx_coarsen2_workspace_size(int64_t n, uint64_t *bytes, ch
  *   coarse_inv_count float [n]     (1/(count+1), the scatter-mean quirk)
  *   *nc_out         host int64
  * The coarse kernel map is s3dx_kmap_subm3(coarse_coords, nc, nc, ...)
- * (sparse_ops.cpp:142).  Sort-based: O(n log n) for any int32 coordinates
- * and bounding box.  Synchronizes `stream` once, to return nc. */
+ * (sparse_ops.cpp:142).  Sets of batch 0 in [0, 128)^3 with at most eight
+ * rows per coarse cell take a window (a bitmap of the coarse cells ranked by
+ * a scan, no sort) and synchronize `stream` once, to return nc; any other set
+ * is sorted (O(n log n) for any int32 coordinates and bounding box) after
+ * that synchronization and synchronizes once more. */
 S3DX_API s3dx_status s3dx_coarsen2(const int32_t *coords, int64_t n, int32_t *coarse_coords,
                                    int32_t *fine_to_coarse, int32_t *coarse_children,
                                    float *coarse_inv_count, int64_t *nc_out, void *workspace,

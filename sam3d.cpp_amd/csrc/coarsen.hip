@@ -12,6 +12,14 @@
 // flag per new key and a scan give every sorted row its coarse rank.  Any
 // int32 coordinates, any bounding box; O(n) work, one host synchronization
 // (to return nc).
+//
+// Sets of batch 0 in [0, 128)^3 (the SLat grids) take a window instead, with
+// no sort: their coarse cells index a 64^3 bitmap in (x, y, z) order -- the
+// std::map order of the keys -- so a popcount scan over the bitmap ranks
+// them; each fine row takes one of its coarse row's eight slots, and a pass
+// per coarse row sorts its slots (its rows ascending).  A coarse cell with
+// more than eight rows (duplicate coordinates) or a row outside the window
+// raises a flag read at the synchronization, and the sort runs instead.
 #include "coord_hash.hpp"
 
 #include <rocprim/device/device_radix_sort.hpp>
@@ -84,6 +92,122 @@ children_kernel(const int32_t *__restrict__ rows, const int32_t *__restrict__ st
     inv_count[r] = 1.0f / static_cast<float>(k + 1);
 }
 
+// ---- window path ----------------------------------------------------------
+constexpr int kCoarseWindowLog2 = 6;                                   // 64^3 coarse cells
+constexpr int kCoarseWords = (1 << (3 * kCoarseWindowLog2)) / 32;       // 8,192 bitmap words
+constexpr int kScanThreads = 1024;
+static_assert(kCoarseWords % kScanThreads == 0, "whole words per scan thread");
+enum { kOutside = 0, kOverflow = 1 };  // flag words
+
+// Zeroes the bitmap, the flags and the slot counters (n).
+__global__ void __launch_bounds__(kThreads)
+window_clear_kernel(uint32_t *__restrict__ bitmap, uint32_t *__restrict__ flags, int32_t *__restrict__ cnt,
+                    int32_t n) {
+    const int32_t i = blockIdx.x * kThreads + threadIdx.x;
+    if (i < kCoarseWords) bitmap[i] = 0u;
+    if (i < 2) flags[i] = 0u;
+    if (i < n) cnt[i] = 0;
+}
+
+__device__ __forceinline__ int32_t coarse_cell(int4 c) {
+    constexpr int kFine = 2 << kCoarseWindowLog2;  // 128
+    if (c.x != 0 || static_cast<uint32_t>(c.y) >= kFine || static_cast<uint32_t>(c.z) >= kFine ||
+        static_cast<uint32_t>(c.w) >= kFine)
+        return -1;
+    // (nonnegative: C++ truncation is the shift)
+    return ((((c.y >> 1) << kCoarseWindowLog2) + (c.z >> 1)) << kCoarseWindowLog2) + (c.w >> 1);
+}
+
+__global__ void __launch_bounds__(kThreads)
+window_mark_kernel(const int4 *__restrict__ coords, int32_t n, uint32_t *__restrict__ bitmap,
+                   uint32_t *__restrict__ flags) {
+    const int32_t i = blockIdx.x * kThreads + threadIdx.x;
+    if (i >= n) return;
+    const int32_t cell = coarse_cell(coords[i]);
+    if (cell < 0) atomicOr(&flags[kOutside], 1u);
+    else atomicOr(&bitmap[cell >> 5], 1u << (cell & 31));
+}
+
+// One workgroup: prefix[w] = occupied cells in words 0..w-1; *total = nc.
+__global__ void __launch_bounds__(kScanThreads)
+window_scan_kernel(const uint32_t *__restrict__ bitmap, uint32_t *__restrict__ prefix, int32_t *__restrict__ total) {
+    constexpr int WPT = kCoarseWords / kScanThreads;
+    __shared__ uint32_t wave_sums[kScanThreads / 64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    uint32_t cnt[WPT], mine = 0;
+#pragma unroll
+    for (int k = 0; k < WPT; ++k) {
+        cnt[k] = static_cast<uint32_t>(__popc(bitmap[tid * WPT + k]));
+        mine += cnt[k];
+    }
+    uint32_t incl = mine;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        const uint32_t t = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += t;
+    }
+    if (lane == 63) wave_sums[wave] = incl;
+    __syncthreads();
+    uint32_t base = 0, all = 0;
+#pragma unroll
+    for (int w = 0; w < kScanThreads / 64; ++w) {
+        base += w < wave ? wave_sums[w] : 0u;
+        all += wave_sums[w];
+    }
+    uint32_t run = base + incl - mine;
+#pragma unroll
+    for (int k = 0; k < WPT; ++k) {
+        prefix[tid * WPT + k] = run;
+        run += cnt[k];
+    }
+    if (tid == 0) *total = static_cast<int32_t>(all);
+}
+
+// Fine row i: its coarse rank, the coarse key, and one of the rank's eight slots.
+__global__ void __launch_bounds__(kThreads)
+window_assign_kernel(const int4 *__restrict__ coords, int32_t n, const uint32_t *__restrict__ bitmap,
+                     const uint32_t *__restrict__ prefix, uint32_t *__restrict__ flags, int32_t *__restrict__ f2c,
+                     int4 *__restrict__ coarse_coords, int32_t *__restrict__ cnt, int32_t *__restrict__ slots) {
+    const int32_t i = blockIdx.x * kThreads + threadIdx.x;
+    if (i >= n || flags[kOutside] != 0u) return;
+    const int4 c = coords[i];
+    const int32_t cell = coarse_cell(c);
+    const uint32_t w = static_cast<uint32_t>(cell) >> 5, bit = static_cast<uint32_t>(cell) & 31u;
+    const int32_t r = static_cast<int32_t>(prefix[w] + static_cast<uint32_t>(__popc(bitmap[w] & ((1u << bit) - 1u))));
+    f2c[i] = r;
+    coarse_coords[r] = make_int4(0, c.y >> 1, c.z >> 1, c.w >> 1);  // (every row of r writes the same key)
+    const int32_t k = atomicAdd(&cnt[r], 1);
+    if (k < 8) slots[static_cast<int64_t>(r) * 8 + k] = i;
+    else atomicOr(&flags[kOverflow], 1u);
+}
+
+// Per coarse row: its rows ascending (at most eight here), padded with n, and
+// 1 / (count + 1).
+__global__ void __launch_bounds__(kThreads)
+window_children_kernel(const int32_t *__restrict__ cnt, const int32_t *__restrict__ slots, const int32_t *nc_dev,
+                       const uint32_t *__restrict__ flags, int32_t n, int32_t *__restrict__ children,
+                       float *__restrict__ inv_count) {
+    const int32_t r = blockIdx.x * kThreads + threadIdx.x;
+    if (r >= *nc_dev || flags[kOutside] != 0u || flags[kOverflow] != 0u) return;
+    const int32_t k = cnt[r];
+    int32_t v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = j < k ? slots[static_cast<int64_t>(r) * 8 + j] : n;
+    // the slots in arrival order; an insertion sort of the eight puts the rows ascending
+#pragma unroll
+    for (int a = 1; a < 8; ++a)
+#pragma unroll
+        for (int b = a; b > 0; --b)
+            if (v[b] < v[b - 1]) {
+                const int32_t t = v[b];
+                v[b] = v[b - 1];
+                v[b - 1] = t;
+            }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) children[static_cast<int64_t>(r) * 8 + j] = v[j];
+    inv_count[r] = 1.0f / static_cast<float>(k + 1);
+}
+
 size_t sort_temp_bytes(int64_t n) {
     size_t bytes = 0;
     hip_check(rocprim::radix_sort_pairs(nullptr, bytes, static_cast<const uint64_t *>(nullptr),
@@ -98,6 +222,9 @@ struct CoarsenLayout {
     int32_t *rows0, *rows1, *rows2, *flag, *ex, *starts, *totals;
     void *sort_ws, *scan_ws;
     size_t sort_bytes;
+    // window path: bitmap, word prefixes, flags, slot counters and slots
+    uint32_t *bitmap, *prefix, *wflags;
+    int32_t *cnt, *slots;
 };
 template <class W>
 void coarsen_layout(W &w, int64_t n, CoarsenLayout *l) {
@@ -119,12 +246,22 @@ void coarsen_layout(W &w, int64_t n, CoarsenLayout *l) {
         l->sort_ws = w.template take<char>(sort_bytes);
         l->scan_ws = w.template take<char>(scan_workspace_bytes(n));
         l->sort_bytes = sort_bytes;
+        l->bitmap = w.template take<uint32_t>(kCoarseWords);
+        l->prefix = w.template take<uint32_t>(kCoarseWords);
+        l->wflags = w.template take<uint32_t>(2);
+        l->cnt = w.template take<int32_t>(un);
+        l->slots = w.template take<int32_t>(un * 8);
     } else {
         for (int k = 0; k < 5; ++k) w.template take<uint64_t>(un);
         for (int k = 0; k < 6; ++k) w.template take<int32_t>(un);
         w.template take<int32_t>(8);
         w.template take<char>(sort_bytes);
         w.template take<char>(scan_workspace_bytes(n));
+        w.template take<uint32_t>(kCoarseWords);
+        w.template take<uint32_t>(kCoarseWords);
+        w.template take<uint32_t>(2);
+        w.template take<int32_t>(un);
+        w.template take<int32_t>(un * 8);
     }
 }
 
@@ -167,6 +304,36 @@ S3DX_API s3dx_status s3dx_coarsen2(const int32_t *coords, int64_t n, int32_t *co
         CoarsenLayout l;
         coarsen_layout(w, n, &l);
         const unsigned blocks = blocks_for(ni);
+
+        // 0. the window path; its flags and nc come back at the one
+        // synchronization, and only a flag sends the set through the sort
+        window_clear_kernel<<<blocks_for(std::max<int64_t>(n, kCoarseWords)), kThreads, 0, s>>>(l.bitmap, l.wflags,
+                                                                                              l.cnt, ni);
+        launch_check("window_clear");
+        window_mark_kernel<<<blocks, kThreads, 0, s>>>(reinterpret_cast<const int4 *>(coords), ni, l.bitmap, l.wflags);
+        launch_check("window_mark");
+        window_scan_kernel<<<1, kScanThreads, 0, s>>>(l.bitmap, l.prefix, l.totals);
+        launch_check("window_scan");
+        window_assign_kernel<<<blocks, kThreads, 0, s>>>(reinterpret_cast<const int4 *>(coords), ni, l.bitmap,
+                                                         l.prefix, l.wflags, fine_to_coarse,
+                                                         reinterpret_cast<int4 *>(coarse_coords), l.cnt, l.slots);
+        launch_check("window_assign");
+        window_children_kernel<<<blocks, kThreads, 0, s>>>(l.cnt, l.slots, l.totals, l.wflags, ni, coarse_children,
+                                                           coarse_inv_count);
+        launch_check("window_children");
+        struct {
+            int32_t nc;
+            uint32_t flags[2];
+        } back{};
+        hip_check(hipMemcpyAsync(&back.nc, l.totals, sizeof(int32_t), hipMemcpyDeviceToHost, s), "hipMemcpyAsync nc");
+        hip_check(hipMemcpyAsync(back.flags, l.wflags, sizeof(back.flags), hipMemcpyDeviceToHost, s),
+                  "hipMemcpyAsync flags");
+        hip_check(hipStreamSynchronize(s), "hipStreamSynchronize");
+        if (back.flags[kOutside] == 0u && back.flags[kOverflow] == 0u) {
+            require(back.nc > 0 && back.nc <= ni, "coarse row count out of range");
+            *nc_out = back.nc;
+            return;
+        }
 
         // 1. the two key halves; rows 0..n-1
         coarse_key_halves_kernel<<<blocks, kThreads, 0, s>>>(reinterpret_cast<const int4 *>(coords), ni, l.hi0,

@@ -79,6 +79,48 @@ def test_random_sets_with_duplicates_and_batches(s3dx, O):
         assert np.array_equal(inv.download()[:nc], oinv)
 
 
+def _coarsen_cases():
+    """Sets for the window path of s3dx_coarsen2 (batch 0 in [0, 128)^3, at
+    most eight rows per coarse cell) and for each way out of it."""
+    rng = np.random.default_rng(91)
+    g = np.stack(np.meshgrid(*(np.arange(0, 128, 3),) * 3, indexing="ij"), -1).reshape(-1, 3)
+    base = np.concatenate([np.zeros((len(g), 1), np.int64), g], 1).astype(np.int32)
+    base = base[rng.permutation(len(base))]
+    edge = base.copy()
+    edge[:8, 1:] = [[0, 0, 0], [127, 127, 127], [0, 127, 0], [127, 0, 127],
+                    [126, 1, 0], [1, 126, 127], [64, 63, 64], [63, 64, 63]]
+    few_dups = np.concatenate([base, base[:500]])             # two rows on some fine cells: <= 8 a coarse cell
+    cube = np.stack(np.meshgrid(*(np.arange(10, 12),) * 3, indexing="ij"), -1).reshape(-1, 3)
+    full = np.concatenate([np.zeros((8, 1), np.int64), cube], 1).astype(np.int32)
+    overflow = np.concatenate([base, full, full[:1]])        # nine rows on one coarse cell
+    outside = base.copy()
+    outside[17] = [0, 128, 5, 5]                              # one row past the window
+    negative = base.copy()
+    negative[3] = [0, -1, 4, 4]                               # (-1 / 2 == 0: the same coarse cell as 0, 1)
+    batch1 = base.copy()
+    batch1[::97, 0] = 1                                       # a second batch
+    return {"window": base, "window_edges": edge, "window_duplicates": few_dups,
+            "nine_rows_one_cell": overflow, "outside_window": outside, "negative": negative,
+            "two_batches": batch1}
+
+
+@pytest.mark.parametrize("case", list(_coarsen_cases()))
+def test_coarsen_window_path(s3dx, O, case):
+    # The window path (a bitmap ranked by a popcount scan, eight slots a
+    # coarse row) and its fallback to the sort, byte-identical to the oracle
+    # on the tables SlatTables::build returns (sparse_ops.cpp:53-104).
+    c = np.ascontiguousarray(_coarsen_cases()[case])
+    n = c.shape[0]
+    nc, cc, f2c, ch, inv = s3dx.coarsen2(s3dx.DeviceArray.from_host(c), n)
+    onc, occ, of2c, och, oinv = O.coarsen2(c)
+    print(f"coarsen {case}: n={n} nc={nc}", flush=True)
+    assert nc == onc
+    assert np.array_equal(cc.download()[:nc], occ)
+    assert np.array_equal(f2c.download(), of2c)
+    assert np.array_equal(ch.download()[: 8 * nc], och)
+    assert np.array_equal(inv.download()[:nc].view(np.uint32), oinv.view(np.uint32))
+
+
 @pytest.mark.parametrize("n", [3000, 200000])
 def test_coarsen_wide_bbox(s3dx, O, n):
     # Coordinates spread over ~2^30 (negative ones too, two batches, half the
