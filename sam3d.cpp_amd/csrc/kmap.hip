@@ -161,6 +161,44 @@ child_kmap_kernel(const int32_t *__restrict__ parent_kmap, int32_t p, int32_t *_
     kmap[g] = t >= 0 ? t * 8 + cs : -1;
 }
 
+// Four entries per thread (32-bit indexes: 216 p below 2^31): the
+// (child slot, offset) -> (parent offset, child slot) table from LDS instead
+// of recomputed per entry, the four parent-map loads in flight together, one
+// 16-byte store; XCD-contiguous ranges of entries.  kmap 16-byte aligned.
+__global__ void __launch_bounds__(kThreads)
+child_kmap4_kernel(const int32_t *__restrict__ parent_kmap, int32_t p, int32_t *__restrict__ kmap) {
+    __shared__ uint8_t adj[8 * 27];  // parent offset | child slot << 5
+    if (threadIdx.x < 8 * 27) {
+        int po, cs;
+        adjacent(static_cast<int>(threadIdx.x) / 27, static_cast<int>(threadIdx.x) % 27, &po, &cs);
+        adj[threadIdx.x] = static_cast<uint8_t>(po | cs << 5);
+    }
+    __syncthreads();
+    const int32_t u = xcd_tile(blockIdx.x, gridDim.x) * kThreads + threadIdx.x;
+    const int32_t count = p * 8 * 27;
+    if (int64_t(4) * u >= count) return;
+    const int32_t g = 4 * u;
+    int32_t r = g / 27, o = g - r * 27;
+    int32_t e[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        e[k] = -1;
+        if (g + k < count) {
+            const uint32_t a = adj[(r & 7) * 27 + o];
+            const int32_t t = parent_kmap[(r >> 3) * 27 + static_cast<int32_t>(a & 31u)];
+            e[k] = t >= 0 ? t * 8 + static_cast<int32_t>(a >> 5) : -1;
+        }
+        if (++o == 27) o = 0, ++r;
+    }
+    if (g + 3 < count) {
+        *reinterpret_cast<int4 *>(kmap + g) = make_int4(e[0], e[1], e[2], e[3]);
+    } else {
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+            if (g + k < count) kmap[g + k] = e[k];
+    }
+}
+
 constexpr uint64_t kmap_capacity(int64_t n) {
     uint64_t cap = 256;
     while (cap < static_cast<uint64_t>(n) * 4) cap <<= 1;
@@ -389,8 +427,11 @@ S3DX_API s3dx_status s3dx_subdivide2(const int32_t *parent_coords, int64_t paren
             reinterpret_cast<const int4 *>(parent_coords), p, reinterpret_cast<int4 *>(child_coords));
         launch_check("child_coords");
         if (child_kmap) {
-            child_kmap_kernel<<<blocks_for(static_cast<int64_t>(p) * 8 * 27), kThreads, 0, s>>>(
-                l.parent_kmap, p, child_kmap);
+            const int64_t entries = static_cast<int64_t>(p) * 8 * 27;
+            if (aligned(child_kmap, 16) && entries < (int64_t(1) << 31) - 4)
+                child_kmap4_kernel<<<blocks_for((entries + 3) / 4), kThreads, 0, s>>>(l.parent_kmap, p, child_kmap);
+            else
+                child_kmap_kernel<<<blocks_for(entries), kThreads, 0, s>>>(l.parent_kmap, p, child_kmap);
             launch_check("child_kmap");
         }
         int32_t flags[2] = {0, 0};
