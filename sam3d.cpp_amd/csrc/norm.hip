@@ -207,12 +207,30 @@ layernorm_vec_kernel(const void *x, int64_t n, int32_t c, int32_t lpr_log2, floa
 constexpr int kStatBlocks = 1024;
 constexpr int kMaxGnChannels = 1024;
 
+// A piece as loaded (16 bytes, or one element when VE == 1) and its
+// widening to float, kept apart so several pieces' loads can be issued
+// before the first is widened.
+// (A single element is held zero-extended in 32 bits, so pieces never share
+// a register.)
 template <class T, int VE>
-__device__ __forceinline__ void load_piece(const void *x, int64_t off, float (&v)[VE]) {
+using RawPiece = std::conditional_t<(VE > 1), uint4, uint32_t>;
+
+template <class T, int VE>
+__device__ __forceinline__ RawPiece<T, VE> load_raw_piece(const void *x, int64_t off) {
     if constexpr (VE == 1) {
-        v[0] = ld<T>(x, off);
+        if constexpr (sizeof(T) == 2) return static_cast<const uint16_t *>(x)[off];
+        else return static_cast<const uint32_t *>(x)[off];
     } else {
-        const uint4 raw = *reinterpret_cast<const uint4 *>(static_cast<const T *>(x) + off);
+        return *reinterpret_cast<const uint4 *>(static_cast<const T *>(x) + off);
+    }
+}
+
+template <class T, int VE>
+__device__ __forceinline__ void widen_piece(const RawPiece<T, VE> &raw, float (&v)[VE]) {
+    if constexpr (VE == 1) {
+        if constexpr (sizeof(T) == 2) v[0] = bf16_to_f32(static_cast<uint16_t>(raw));
+        else v[0] = __builtin_bit_cast(float, raw);
+    } else {
         const uint32_t w4[4] = {raw.x, raw.y, raw.z, raw.w};
         if constexpr (sizeof(T) == 2) {
 #pragma unroll
@@ -244,7 +262,7 @@ gn_sums_kernel(const void *x, int64_t n, int32_t c, float *partials) {
 #pragma unroll
     for (int i = 0; i < MP; ++i) {
         const int p = p0 + i * tpr;
-        if (active && p < ppr) load_piece<T, VE>(x, static_cast<int64_t>(p) * VE, k[i]);
+        if (active && p < ppr) widen_piece<T, VE>(load_raw_piece<T, VE>(x, static_cast<int64_t>(p) * VE), k[i]);
 #pragma unroll
         for (int e = 0; e < VE; ++e) {
             s[i][e] = 0.0f;
@@ -252,14 +270,18 @@ gn_sums_kernel(const void *x, int64_t n, int32_t c, float *partials) {
         }
     }
     if (active) {
-#pragma unroll 4
-        for (int64_t r = r0 + roff; r < r1; r += rstep) {
+        // kRowsInFlight rows' loads are issued before the first is summed (the
+        // barrier stops the scheduler from pairing each load with its use);
+        // each accumulator still takes the rows in increasing order.  Rows
+        // past the run's end reread its last row and are not added.
+        constexpr int kRowsInFlight = 8;
+        using Raw = RawPiece<T, VE>;
+        auto add_row = [&](const Raw (&raw)[MP]) {
 #pragma unroll
             for (int i = 0; i < MP; ++i) {
-                const int p = p0 + i * tpr;
-                if (MP > 1 && p >= ppr) continue;
+                if (MP > 1 && p0 + i * tpr >= ppr) continue;
                 float v[VE];
-                load_piece<T, VE>(x, r * c + static_cast<int64_t>(p) * VE, v);
+                widen_piece<T, VE>(raw[i], v);
 #pragma unroll
                 for (int e = 0; e < VE; ++e) {
                     const float d = v[e] - k[i][e];
@@ -267,6 +289,23 @@ gn_sums_kernel(const void *x, int64_t n, int32_t c, float *partials) {
                     q[i][e] += d * d;
                 }
             }
+        };
+        auto load_row = [&](int64_t r, Raw (&raw)[MP]) {
+#pragma unroll
+            for (int i = 0; i < MP; ++i) {
+                const int p = p0 + i * tpr;
+                if (MP > 1 && p >= ppr) continue;
+                raw[i] = load_raw_piece<T, VE>(x, r * c + static_cast<int64_t>(p) * VE);
+            }
+        };
+        for (int64_t r = r0 + roff; r < r1; r += kRowsInFlight * rstep) {
+            Raw raw[kRowsInFlight][MP];
+#pragma unroll
+            for (int u = 0; u < kRowsInFlight; ++u) load_row(min(r + u * rstep, r1 - 1), raw[u]);
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int u = 0; u < kRowsInFlight; ++u)
+                if (r + u * rstep < r1) add_row(raw[u]);
         }
 #pragma unroll
         for (int i = 0; i < MP; ++i) {
@@ -292,48 +331,80 @@ gn_sums_kernel(const void *x, int64_t n, int32_t c, float *partials) {
     }
 }
 
-__device__ __forceinline__ double wave_sum_f64(double v) {
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) v += __shfl_xor(v, d, 64);
-    return v;
-}
-
-// One block per group: per-channel totals over the blocks (a wave per
-// channel), then the group mean and centred variance from the shifted sums
+// One block per group: per-channel totals over the stat blocks, then the
+// group mean and centred variance from the shifted sums
 //   sum_r (x - m)^2 = sum_r (x - K)^2 - 2 (m - K) sum_r (x - K) + n (m - K)^2,
 // then scale = gamma * rstd, shift = beta - m * gamma * rstd per channel.
+// The group's partials are 2 cg items a stat block (item j < cg: sum (x - K)
+// of channel j; item cg + j: sum (x - K)^2 of channel j), two runs of cg
+// floats.  A pass takes up to kFinalizeThreads items; thread t adds item
+// t mod w over stat blocks s, s + slots, ... (s = t / w, slots =
+// kFinalizeThreads / w), so one wave load covers consecutive channels of a
+// few stat blocks instead of 64 cache lines.  Loads go kFinalizeBatch at a
+// time (past the last stat block they reread it and add 0).  Slot totals meet
+// in LDS and are added in slot order: a fixed order whatever the timing.
+constexpr int kFinalizeThreads = 1024;
+constexpr int kFinalizeBatch = 16;
+static_assert(kMaxGnChannels <= kFinalizeThreads, "a thread per channel of a group");
 template <class T>
-__global__ void __launch_bounds__(256)
-gn_finalize_kernel(const void *x, const float *partials, int nblocks, int64_t n, int32_t c,
-                   int32_t cg, float eps, const float *gamma, const float *beta, float *scale,
-                   float *shift) {
-    __shared__ double t1[kMaxGnChannels], t2[kMaxGnChannels];
+__global__ void __launch_bounds__(kFinalizeThreads)
+gn_finalize_kernel(const void *x, const float *partials, int64_t n, int32_t c, int32_t cg, float eps,
+                   const float *gamma, const float *beta, float *scale, float *shift) {
+    __shared__ double slot_sum[kFinalizeThreads];
+    __shared__ double tot[2 * kMaxGnChannels];
+    __shared__ double kx[kMaxGnChannels];
     __shared__ double stats[2];
-    const int g = blockIdx.x;
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    for (int cl = wave; cl < cg; cl += 4) {
-        const int ch = g * cg + cl;
-        double a = 0.0, b = 0.0;
-        for (int blk = lane; blk < nblocks; blk += 64) {
-            a += static_cast<double>(partials[static_cast<int64_t>(blk) * 2 * c + ch]);
-            b += static_cast<double>(partials[static_cast<int64_t>(blk) * 2 * c + c + ch]);
+    const int g = blockIdx.x, tid = threadIdx.x;
+    // Thread cl < cg owns channel g cg + cl.  Its shift and affine values
+    // are loaded first, unconditionally (other threads reread the group's
+    // last channel; a NULL gamma or beta reads partials instead and is
+    // replaced by 1 or 0 at the use), so they land while the partials are
+    // added.
+    const bool own = tid < cg;
+    const int och = g * cg + min(tid, cg - 1);
+    const T kraw = static_cast<const T *>(x)[och];
+    const float graw = (gamma ? gamma : partials)[och];
+    const float braw = (beta ? beta : partials)[och];
+    const int items = 2 * cg;
+    for (int j0 = 0; j0 < items; j0 += kFinalizeThreads) {
+        const int w = min(items - j0, kFinalizeThreads);
+        const int slots = kFinalizeThreads / w;
+        const int slot = tid / w, jl = tid - slot * w, j = j0 + jl;
+        if (slot < slots) {
+            const float *p = partials + (j < cg ? g * cg + j : c + g * cg + (j - cg));
+            double a = 0.0;
+            for (int b = slot; b < kStatBlocks; b += kFinalizeBatch * slots) {
+                float v[kFinalizeBatch];
+#pragma unroll
+                for (int u = 0; u < kFinalizeBatch; ++u)
+                    v[u] = p[static_cast<int64_t>(min(b + u * slots, kStatBlocks - 1)) * 2 * c];
+                // Keeps the scheduler from pairing each load with its add.
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int u = 0; u < kFinalizeBatch; ++u)
+                    a += b + u * slots < kStatBlocks ? static_cast<double>(v[u]) : 0.0;
+            }
+            slot_sum[slot * w + jl] = a;
         }
-        a = wave_sum_f64(a);
-        b = wave_sum_f64(b);
-        if (lane == 0) {
-            t1[cl] = a;
-            t2[cl] = b;
+        __syncthreads();
+        if (tid < w) {
+            double a = 0.0;
+            for (int s = 0; s < slots; ++s) a += slot_sum[s * w + tid];
+            tot[j] = a;
         }
+        __syncthreads();
     }
+    if (own) kx[tid] = static_cast<double>(load_as_f32<T>(&kraw));
     __syncthreads();
-    if (threadIdx.x == 0) {
+    if (tid == 0) {
+        const double *t1 = tot, *t2 = tot + cg;
         const double dn = static_cast<double>(n);
         double sum = 0.0;
-        for (int cl = 0; cl < cg; ++cl) sum += static_cast<double>(ld<T>(x, g * cg + cl)) * dn + t1[cl];
+        for (int cl = 0; cl < cg; ++cl) sum += kx[cl] * dn + t1[cl];
         const double m = sum / (dn * cg);
         double ss = 0.0;
         for (int cl = 0; cl < cg; ++cl) {
-            const double dk = m - static_cast<double>(ld<T>(x, g * cg + cl));
+            const double dk = m - kx[cl];
             ss += t2[cl] - 2.0 * dk * t1[cl] + dn * dk * dk;
         }
         const double var = ss / (dn * cg);
@@ -341,12 +412,11 @@ gn_finalize_kernel(const void *x, const float *partials, int nblocks, int64_t n,
         stats[1] = 1.0 / sqrt((var > 0.0 ? var : 0.0) + static_cast<double>(eps));
     }
     __syncthreads();
-    for (int cl = threadIdx.x; cl < cg; cl += 256) {
-        const int ch = g * cg + cl;
-        const double ga = gamma ? gamma[ch] : 1.0;
-        const double be = beta ? beta[ch] : 0.0;
-        scale[ch] = static_cast<float>(ga * stats[1]);
-        shift[ch] = static_cast<float>(be - stats[0] * ga * stats[1]);
+    if (own) {
+        const double ga = gamma ? static_cast<double>(graw) : 1.0;
+        const double be = beta ? static_cast<double>(braw) : 0.0;
+        scale[och] = static_cast<float>(ga * stats[1]);
+        shift[och] = static_cast<float>(be - stats[0] * ga * stats[1]);
     }
 }
 
@@ -679,10 +749,10 @@ S3DX_API s3dx_status s3dx_groupnorm_stats(const void *x, int32_t x_dtype, int64_
             else gn_sums_kernel<float, 1, 4><<<kStatBlocks, 256, 0, s>>>(x, n, c, l.partials);
         }
         launch_check("gn_sums");
-        if (bf) gn_finalize_kernel<uint16_t><<<groups, 256, 0, s>>>(x, l.partials, kStatBlocks, n, c, cg, eps,
-                                                                     gamma, beta, scale, shift);
-        else gn_finalize_kernel<float><<<groups, 256, 0, s>>>(x, l.partials, kStatBlocks, n, c, cg, eps, gamma,
-                                                               beta, scale, shift);
+        if (bf) gn_finalize_kernel<uint16_t><<<groups, kFinalizeThreads, 0, s>>>(x, l.partials, n, c, cg, eps,
+                                                                                     gamma, beta, scale, shift);
+        else gn_finalize_kernel<float><<<groups, kFinalizeThreads, 0, s>>>(x, l.partials, n, c, cg, eps, gamma,
+                                                                                beta, scale, shift);
         launch_check("gn_finalize");
     });
 }
