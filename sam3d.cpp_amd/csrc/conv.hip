@@ -1104,6 +1104,9 @@ void conv_run_impl(const s3dx_conv *conv, const s3dx_gather_plan *gplan, const v
         }
         if (plan.mfma) {
             a.ln = plan.fused_ln;
+            // The three-term kernel has an instantiation that reads a residual
+            // (grid-stride over the same blocks, so the grid stands).
+            if (plan.split && a.residual) plan.fn = pick_linear_split(plan.nb, conv->cin / 16, true);
             hipLaunchKernelGGL(plan.fn, plan.grid, dim3(plan.threads), plan.smem, s, a);
             launch_check(plan.linear ? "conv_linear" : "conv_mfma");
         } else {

@@ -16,12 +16,12 @@ KernelFn pick_linear_f32(int nbt) { return pick_linear<float>(nbt); }
 
 KernelFn pick_linear_f32_bf16_rows(int nbt) { return pick_linear<float, true>(nbt); }
 
-KernelFn pick_linear_split(int nbt, int ksx) {
+KernelFn pick_linear_split(int nbt, int ksx, bool residual) {
     switch (nbt) {
-    case 1: return pick_linear_split_ks<1>(ksx);
-    case 2: return pick_linear_split_ks<2>(ksx);
-    case 3: return pick_linear_split_ks<3>(ksx);
-    case 4: return pick_linear_split_ks<4>(ksx);
+    case 1: return residual ? pick_linear_split_ks<1, true>(ksx) : pick_linear_split_ks<1, false>(ksx);
+    case 2: return residual ? pick_linear_split_ks<2, true>(ksx) : pick_linear_split_ks<2, false>(ksx);
+    case 3: return residual ? pick_linear_split_ks<3, true>(ksx) : pick_linear_split_ks<3, false>(ksx);
+    case 4: return residual ? pick_linear_split_ks<4, true>(ksx) : pick_linear_split_ks<4, false>(ksx);
     default: return nullptr;
     }
 }

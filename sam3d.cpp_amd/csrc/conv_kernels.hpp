@@ -92,7 +92,7 @@ constexpr int kGatherPlanRecord128 = 18432;  // 128-row tiles
 KernelFn pick_linear_f32_bf16_rows(int nbt);
 // The same on BF16 MFMAs with three-term split weights (Cin = 16 * ksx,
 // ksx in {2, 4, 6, 8}; nbt in 1..4), else nullptr.
-KernelFn pick_linear_split(int nbt, int ksx);
+KernelFn pick_linear_split(int nbt, int ksx, bool residual = false);
 
 namespace {
 
@@ -1486,7 +1486,10 @@ __global__ void __launch_bounds__(256) linear_kernel(ConvArgs a) {
 // exactly as the output rows (row * cout + col), so the block leaves as one
 // contiguous span of 16-byte streaming stores.  Two tiles alternate: one
 // barrier per block.
-template <int NBT, int KSX>
+// RES: a.residual is set (a separate instantiation: the residual loads of
+// the epilogue wait for every load in flight, so a kernel that has them
+// cannot keep the next block's rows in flight across the epilogue).
+template <int NBT, int KSX, bool RES>
 __global__ void __launch_bounds__(64 * NBT) __attribute__((amdgpu_waves_per_eu(KSX <= 6 ? 3 : 2)))
 linear_split_kernel(ConvArgs a) {
     __shared__ __align__(16) float tile[2][32 * 32 * NBT];
@@ -1512,15 +1515,37 @@ linear_split_kernel(ConvArgs a) {
         const int64_t r = blk * 32 + (lane & 31);
         const uint32_t base = r < a.n_out ? static_cast<uint32_t>(((r >> a.row_shift) * a.cin + half * 8) * 2)
                                           : 0x80000000u;
+        // Issued in k-step order everywhere (the barriers pin it): the wait
+        // before a k-step's MFMAs then counts the later loads and the stores
+        // as younger on every path into the loop.
 #pragma unroll
         for (int ks = 0; ks < KSX; ++ks) {
             const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, static_cast<int32_t>(base + ks * 32), 0, 0);
             f[ks] = make_uint4(v.x, v.y, v.z, v.w);
+            __builtin_amdgcn_sched_barrier(0);
         }
+    };
+    // Every block ends with kStores stores per thread, whatever its output
+    // type and row count (16-byte pieces, one single element, and for BF16
+    // output stores to an empty buffer, which the resource drops), and the
+    // first block's loads are followed by as many dropped stores (at
+    // distinct offsets, so none is merged away): on both paths into the loop
+    // each k-step's rows then have the same known number of younger memory
+    // operations, so its wait covers its own load and never the previous
+    // block's stores.
+    constexpr int kSpan = 32 * 32 * NBT;  // tile elements
+    constexpr int kStores = kSpan / 4 / (64 * NBT) + 1;  // FP32: 16-byte pieces, then one element
+    constexpr int kNontemporal = 2;  // buffer store cache policy: nt
+    const auto drop_rsrc = __builtin_amdgcn_make_buffer_rsrc(a.y, static_cast<short>(0), 0, 0x00020000);
+    auto dropped_stores = [&](auto count) __attribute__((always_inline)) {
+#pragma unroll
+        for (int k = 0; k < decltype(count)::value; ++k)
+            __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, drop_rsrc, 16 * k, 0, 0);
     };
     uint4 cur[KSX];
     int buf = 0;
     load_block(blockIdx.x, cur);
+    dropped_stores(std::integral_constant<int, kStores>{});
     for (int64_t blk = blockIdx.x; blk < nblk; blk += gridDim.x, buf ^= 1) {
         f32x16 acc = f32x16{};
         // Smallest terms first.
@@ -1540,7 +1565,7 @@ linear_split_kernel(ConvArgs a) {
             if (!col_ok || r >= rows) continue;
             float v = acc[j] + bias;
             if (a.silu) v = silu(v);
-            if (a.residual) {
+            if constexpr (RES) {
                 const int64_t roff = ((row0 + r) >> a.residual_shift) * cout + col;
                 v += a.y_bf16 ? bf16_to_f32(static_cast<const uint16_t *>(a.residual)[roff])
                               : static_cast<const float *>(a.residual)[roff];
@@ -1549,43 +1574,60 @@ linear_split_kernel(ConvArgs a) {
         }
         __syncthreads();
         // The block's rows are one span of rows * cout elements starting at
-        // row0 * cout (16-byte aligned: 32 * cout elements per block).
+        // row0 * cout (16-byte aligned: 32 * cout elements per block).  Every
+        // thread issues the same number of 16-byte buffer stores (a piece
+        // outside the span gets an offset the buffer resource drops), so the
+        // compiler can count them and the wait for the next block's rows,
+        // loaded before these stores, leaves the stores in flight (with a
+        // store count it cannot know it waits for them too).  A span that is
+        // not whole pieces (a last block only) ends with single elements.
         const int elems = rows * cout;
+        constexpr int kOut = int32_t(0x80000000);  // an offset every resource drops
         if (a.y_bf16) {
-            uint16_t *y = static_cast<uint16_t *>(a.y) + row0 * cout;
-            for (int i = tid; i * 8 < elems; i += 64 * NBT) {
-                if (i * 8 + 8 <= elems) {
-                    const float4 p = *reinterpret_cast<const float4 *>(tl + i * 8);
-                    const float4 q = *reinterpret_cast<const float4 *>(tl + i * 8 + 4);
-                    *reinterpret_cast<uint4 *>(y + i * 8) = make_uint4(
-                        pack_bf16x2(p.x, p.y), pack_bf16x2(p.z, p.w), pack_bf16x2(q.x, q.y),
-                        pack_bf16x2(q.z, q.w));
-                } else {
-                    for (int e = i * 8; e < elems; ++e) y[e] = f32_to_bf16(tl[e]);
-                }
+            const int pieces = elems / 8;
+            const auto y_rsrc = __builtin_amdgcn_make_buffer_rsrc(static_cast<uint16_t *>(a.y) + row0 * cout,
+                                                                  static_cast<short>(0), elems * 2, 0x00020000);
+#pragma unroll
+            for (int k = 0; k < kSpan / 8 / (64 * NBT); ++k) {
+                const int i = tid + k * 64 * NBT;
+                const float4 p = *reinterpret_cast<const float4 *>(tl + i * 8);
+                const float4 q = *reinterpret_cast<const float4 *>(tl + i * 8 + 4);
+                const u32x4 v = {pack_bf16x2(p.x, p.y), pack_bf16x2(p.z, p.w), pack_bf16x2(q.x, q.y),
+                                 pack_bf16x2(q.z, q.w)};
+                __builtin_amdgcn_raw_buffer_store_b128(v, y_rsrc, i < pieces ? i * 16 : kOut, 0, kNontemporal);
             }
+            dropped_stores(std::integral_constant<int, kStores - 1 - kSpan / 8 / (64 * NBT)>{});
+            // The span's last elems % 8 elements, one a thread.
+            const int e = pieces * 8 + tid;
+            __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(tl[min(e, kSpan - 1)]), y_rsrc,
+                                                  tid < 8 && e < elems ? e * 2 : kOut, 0, 0);
         } else {
-            float *y = static_cast<float *>(a.y) + row0 * cout;
-            for (int i = tid; i * 4 < elems; i += 64 * NBT) {
-                if (i * 4 + 4 <= elems) {
-                    const u32x4 v = *reinterpret_cast<const u32x4 *>(tl + i * 4);
-                    __builtin_nontemporal_store(v, reinterpret_cast<u32x4 *>(y + i * 4));
-                } else {
-                    for (int e = i * 4; e < elems; ++e) y[e] = tl[e];
-                }
+            const int pieces = elems / 4;
+            const auto y_rsrc = __builtin_amdgcn_make_buffer_rsrc(static_cast<float *>(a.y) + row0 * cout,
+                                                                  static_cast<short>(0), elems * 4, 0x00020000);
+#pragma unroll
+            for (int k = 0; k < kSpan / 4 / (64 * NBT); ++k) {
+                const int i = tid + k * 64 * NBT;
+                const u32x4 v = *reinterpret_cast<const u32x4 *>(tl + i * 4);
+                __builtin_amdgcn_raw_buffer_store_b128(v, y_rsrc, i < pieces ? i * 16 : kOut, 0, kNontemporal);
             }
+            dropped_stores(std::integral_constant<int, kStores - 1 - kSpan / 4 / (64 * NBT)>{});
+            // The span's last elems % 4 elements, one a thread.
+            const int e = pieces * 4 + tid;
+            __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, tl[min(e, kSpan - 1)]), y_rsrc,
+                                                  tid < 4 && e < elems ? e * 4 : kOut, 0, 0);
         }
     }
 }
 
 // Cin = 16 * ksx for ksx in {2, 4, 6, 8}; nbt column blocks in 1..4.
-template <int NBT>
+template <int NBT, bool RES>
 KernelFn pick_linear_split_ks(int ksx) {
     switch (ksx) {
-    case 2: return linear_split_kernel<NBT, 2>;
-    case 4: return linear_split_kernel<NBT, 4>;
-    case 6: return linear_split_kernel<NBT, 6>;
-    case 8: return linear_split_kernel<NBT, 8>;
+    case 2: return linear_split_kernel<NBT, 2, RES>;
+    case 4: return linear_split_kernel<NBT, 4, RES>;
+    case 6: return linear_split_kernel<NBT, 6, RES>;
+    case 8: return linear_split_kernel<NBT, 8, RES>;
     default: return nullptr;
     }
 }
