@@ -361,9 +361,10 @@ S3DX_API s3dx_status s3dx_conv_run_planned(const s3dx_conv *conv, const s3dx_gat
                                            void *y, int32_t y_dtype, s3dx_stream stream, char *error,
                                            uint64_t error_capacity);
 /* Describes, as one line of text, the kernel variant s3dx_conv_run launches
- * for n_in input and n_out output rows (buffers assumed 16-byte aligned),
- * e.g. "mfma tiling=11 split-k rows=128 cols=128 kc=128 xf=0 ln=fused
- * grid=221x1".  Host only, no device work.  No counterpart in the reference
+ * for n_in input and n_out output rows (buffers assumed 16-byte aligned,
+ * output in the layer's dtype, no residual: a BF16 1x1 layer's "linear pipe"
+ * kernel takes only those), e.g. "mfma tiling=11 split-k rows=128 cols=128
+ * kc=128 xf=0 ln=fused grid=221x1".  Host only, no device work.  No counterpart in the reference
  * (whose conv is a fixed GGML graph); it exists for tests and benchmarks. */
 S3DX_API s3dx_status s3dx_conv_plan(const s3dx_conv *conv, int64_t n_in, int64_t n_out, char *plan,
                                     uint64_t plan_capacity, char *error, uint64_t error_capacity);

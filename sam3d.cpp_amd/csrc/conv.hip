@@ -376,6 +376,7 @@ struct LaunchPlan {
     int nb = 0, kc = 0;     // 32-column blocks per workgroup, channels per task
     bool linear = false;    // the 1x1-layer kernel (weights resident in LDS)
     bool split = false;     // linear_split_kernel: BF16 rows, three-term BF16 weights
+    bool pipe = false;      // linear_pipe_kernel: BF16 layer, BF16 output, no residual
     bool half_chunk = false;  // halo kernel with a last chunk of 32 channels (64-row tiles only)
     unsigned smem = 0;      // dynamic LDS bytes
     unsigned threads = 256; // workgroup size
@@ -449,8 +450,10 @@ bool has_split_terms(const s3dx_conv *conv) {
 
 // bf16_rows: x holds BF16 rows for an FP32 layer; only the linear kernels
 // read them as they are (the caller converts them for any other plan).
+// allow_pipe: the output is BF16 and there is no residual (the pipelined
+// 1x1 kernel writes only that).
 LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bool aligned16,
-                       bool bf16_rows = false) {
+                       bool bf16_rows = false, bool allow_pipe = true) {
     LaunchPlan p;
     const bool bf = conv->dtype == S3DX_BF16;
     p.mfma = conv->mfma && aligned16;
@@ -468,6 +471,20 @@ LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bo
             p.nb = nbt;
             p.threads = 64 * nbt;
             p.grid = dim3(static_cast<unsigned>(std::min<int64_t>((n_out + 31) / 32, resident_blocks(split, 0, p.threads))));
+            return p;
+        }
+        // BF16 layers with Cin = 64, 128, 192 or 256: the pipelined kernel,
+        // persistent workgroups over the 32-row blocks.
+        KernelFn pipe = bf && allow_pipe && !conv->ln && conv->cin % 16 == 0 && conv->cout % 8 == 0 &&
+                                n_out * conv->cout * 2 < (int64_t(1) << 31)
+                            ? pick_linear_pipe_bf16(nbt, conv->cin / 16)
+                            : nullptr;
+        if (pipe && frags <= kLinearMaxFrags && !std::getenv("S3DX_CONV_TILING")) {
+            p.linear = p.pipe = true;
+            p.fn = pipe;
+            p.nb = nbt;
+            p.smem = static_cast<unsigned>(frags) * 16 + 4 * 8 * (nbt * 32 + 4) * 4;
+            p.grid = dim3(static_cast<unsigned>(std::min<int64_t>((n_out + 127) / 128, resident_blocks(pipe, p.smem))));
             return p;
         }
         if (fn && frags <= kLinearMaxFrags && !std::getenv("S3DX_CONV_TILING")) {
@@ -958,7 +975,8 @@ void describe_launch(const s3dx_conv *conv, const s3dx_gather_plan *gplan, int64
         char text[256];
         const bool halo = p.mfma && !p.linear && p.tl->id >= 20 && p.tl->id <= 22;  // the halo-staged kernels
         if (p.linear)
-            std::snprintf(text, sizeof(text), "linear cols=%d ksteps=%d%s ln=%s grid=%u", p.nb * 32,
+            std::snprintf(text, sizeof(text), "linear%s cols=%d ksteps=%d%s ln=%s grid=%u", p.pipe ? " pipe" : "",
+                          p.nb * 32,
                           conv->cin / (conv->dtype == S3DX_BF16 || p.split ? 16 : 8),
                           p.split ? " terms=3" : "", conv->ln ? "separate" : "none", p.grid.x);
         else if (p.mfma)
@@ -1070,7 +1088,8 @@ void conv_run_impl(const s3dx_conv *conv, const s3dx_gather_plan *gplan, const v
         a.mod_shift = conv->dmod_scale ? conv->dmod_shift : conv->mod_shift;
         // The MFMA kernel reads the map and writes rows with 16-byte accesses.
         const bool aligned16 = aligned(kmap, 16) && aligned(y, 16) && aligned(residual, 16);
-        LaunchPlan plan = plan_launch(conv, a.x_bytes, n_out, aligned16, bf16_rows);
+        LaunchPlan plan = plan_launch(conv, a.x_bytes, n_out, aligned16, bf16_rows,
+                                      residual == nullptr && y_dtype == S3DX_BF16);
         if (bf16_rows && !plan.linear) {
             // Other kernels read the layer's dtype: the rows are widened
             // (exactly) once, into the layer's buffer.

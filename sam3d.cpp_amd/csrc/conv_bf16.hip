@@ -15,4 +15,14 @@ KernelFn pick_mfma_bf16(int id, int kc, bool xf) {
 
 KernelFn pick_linear_bf16(int nbt) { return pick_linear<uint16_t>(nbt); }
 
+KernelFn pick_linear_pipe_bf16(int nbt, int ks) {
+    switch (nbt) {
+    case 1: return pick_linear_pipe_ks<1>(ks);
+    case 2: return pick_linear_pipe_ks<2>(ks);
+    case 3: return pick_linear_pipe_ks<3>(ks);
+    case 4: return pick_linear_pipe_ks<4>(ks);
+    default: return nullptr;
+    }
+}
+
 }  // namespace s3dx

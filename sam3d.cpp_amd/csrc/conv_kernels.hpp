@@ -67,6 +67,9 @@ KernelFn pick_mfma_bf16(int id, int kc, bool xf);
 KernelFn pick_mfma_f32(int id, int kc, bool xf);
 // 1x1-layer kernel for nbt 32-column blocks (1, 2, 3, 4, 6, 8), else nullptr.
 KernelFn pick_linear_bf16(int nbt);
+// linear_pipe_kernel for nbt column blocks and Cin = 16 * ks; nullptr for
+// other shapes.
+KernelFn pick_linear_pipe_bf16(int nbt, int ks);
 KernelFn pick_linear_f32(int nbt);
 // The halo-staged BF16 kernel for `rows`-row x (nb * 32)-column tiles
 // (tiling 20: 128 rows, 21: 64 rows; nb 4, or 3 for 64-row tiles; 64-channel
@@ -1466,6 +1469,120 @@ __global__ void __launch_bounds__(256) linear_kernel(ConvArgs a) {
     }
 }
 
+// BF16 1x1 layers with Cin = 16 * KS (KS in {4, 8, 12, 16}), Cout a multiple
+// of 8 and no residual, pipelined across a wave's row blocks.  Persistent
+// workgroups of 4 waves with the weights in LDS, as in linear_kernel; wave w
+// of G workgroups takes 32-row blocks w, w + 4G, ...  A wave holds all KS
+// A fragments of its block in registers and loads the next block's (a second
+// register set, the two used in turn) before the current block's MFMAs, so
+// after the first block no block waits for its rows.  Rows 8g..8g+7 of a
+// block go through this wave's 8 staging rows and leave as the same number
+// of 16-byte buffer stores for every group (slots past the span get an
+// offset the resource drops), and the first block's loads are followed by
+// as many dropped stores: the compiler's count of the memory operations
+// younger than a block's loads is then the same on every path, so the wait
+// for them never covers the previous block's stores.
+template <int NBT, int KS>
+__global__ void __launch_bounds__(256) linear_pipe_kernel(ConvArgs a) {
+    extern __shared__ uint4 wl[];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5;
+    constexpr int SLD = NBT * 32 + 4;                 // staging row stride (floats)
+    constexpr int KP = (NBT * 32 + 63) / 64;          // 16-byte slots a lane per 8-row group
+    constexpr int kStores = 4 * KP;                   // stores a block
+    constexpr int kOut = int32_t(0x80000000);         // an offset every resource drops
+    const int cout = a.cout;
+    const auto x_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(a.x), static_cast<short>(0),
+                                                          static_cast<int32_t>(a.x_bytes), 0x00020000);
+    const auto y_rsrc = __builtin_amdgcn_make_buffer_rsrc(a.y, static_cast<short>(0),
+                                                          static_cast<int32_t>(a.n_out * cout * 2), 0x00020000);
+    const auto drop_rsrc = __builtin_amdgcn_make_buffer_rsrc(a.y, static_cast<short>(0), 0, 0x00020000);
+    const int64_t nblk = (a.n_out + 31) / 32;
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * 4;
+    // Lane: row lane % 32 of the block, channels ks*16 + half*8 .. +8; rows
+    // past the end (blocks after the wave's last) read zeros.
+    auto load_block = [&](int64_t blk, uint4 (&f)[KS]) __attribute__((always_inline)) {
+        const int64_t r = blk * 32 + (lane & 31);
+        const uint32_t base = r < a.n_out ? static_cast<uint32_t>(((r >> a.row_shift) * a.cin + half * 8) * 2)
+                                          : 0x80000000u;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(x_rsrc, static_cast<int32_t>(base + ks * 32), 0, 0);
+            f[ks] = make_uint4(v.x, v.y, v.z, v.w);
+            __builtin_amdgcn_sched_barrier(0);  // k-step order on every path
+        }
+    };
+    // The bias first: the weight copy's waits then cover it, so no load
+    // issued before the loop is still pending inside it.
+    float bias[NBT];
+#pragma unroll
+    for (int cb = 0; cb < NBT; ++cb) {
+        const int col = cb * 32 + (lane & 31);
+        bias[cb] = a.bias && col < cout ? a.bias[col] : 0.0f;
+    }
+    const uint4 *wg = static_cast<const uint4 *>(a.w);
+    for (int f = tid; f < KS * NBT * 64; f += 256) wl[f] = wg[f];
+    // The first block's rows stay in flight across the barrier below.
+    int64_t blk = static_cast<int64_t>(blockIdx.x) * 4 + wave;
+    uint4 fa[KS], fb[KS];
+    load_block(blk, fa);
+#pragma unroll
+    for (int k = 0; k < kStores; ++k)
+        __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, drop_rsrc, 16 * k, 0, 0);
+    float *stg = reinterpret_cast<float *>(wl + KS * NBT * 64) + wave * 8 * SLD;
+    // Slot k of a lane: 16-byte piece i = lane + 64k of an 8-row group's span
+    // (8 * cout elements), at staging row i / (cout / 8), column 8 * (i % (cout / 8)).
+    const int ppr = cout / 8;
+    int soff[KP];
+#pragma unroll
+    for (int k = 0; k < KP; ++k) {
+        const int i = min(lane + 64 * k, 8 * ppr - 1);
+        soff[k] = (i / ppr) * SLD + (i % ppr) * 8;
+    }
+    __syncthreads();
+    auto run_block = [&](int64_t b, const uint4 (&f)[KS]) __attribute__((always_inline)) {
+        f32x16 acc[NBT];
+#pragma unroll
+        for (int cb = 0; cb < NBT; ++cb) acc[cb] = f32x16{};
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int cb = 0; cb < NBT; ++cb) acc[cb] = mfma_step<uint16_t>(f[ks], wl[(ks * NBT + cb) * 64 + lane], acc[cb]);
+        // D layout: lane l holds column l % 32; register j holds row
+        // 8*(j/4) + 4*(l/32) + j%4 of the block.
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int64_t row0 = b * 32 + 8 * g;
+#pragma unroll
+            for (int cb = 0; cb < NBT; ++cb)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    float v = acc[cb][4 * g + q] + bias[cb];
+                    if (a.silu) v = silu(v);
+                    stg[(4 * half + q) * SLD + cb * 32 + (lane & 31)] = v;
+                }
+            const int64_t left = a.n_out - row0;
+            const int pieces = static_cast<int>(left <= 0 ? 0 : left >= 8 ? 8 * ppr : left * ppr);
+#pragma unroll
+            for (int k = 0; k < KP; ++k) {
+                const int i = lane + 64 * k;
+                const float4 p = *reinterpret_cast<const float4 *>(stg + soff[k]);
+                const float4 q = *reinterpret_cast<const float4 *>(stg + soff[k] + 4);
+                const u32x4 v = {pack_bf16x2(p.x, p.y), pack_bf16x2(p.z, p.w), pack_bf16x2(q.x, q.y),
+                                 pack_bf16x2(q.z, q.w)};
+                __builtin_amdgcn_raw_buffer_store_b128(
+                    v, y_rsrc, i < pieces ? static_cast<int32_t>((row0 * cout + i * 8) * 2) : kOut, 0, 0);
+            }
+        }
+    };
+    for (; blk < nblk; blk += 2 * stride) {
+        load_block(blk + stride, fb);
+        run_block(blk, fa);
+        if (blk + stride >= nblk) break;
+        load_block(blk + 2 * stride, fa);
+        run_block(blk + stride, fb);
+    }
+}
+
 // FP32 1x1 layer fed BF16 rows, on BF16 MFMAs.  Each FP32 weight w is held as
 // three BF16 terms, w1 = bf16(w), w2 = bf16(w - w1), w3 = bf16(w - w1 - w2)
 // (each difference is exact in FP32), so w - (w1 + w2 + w3) is below
@@ -1617,6 +1734,17 @@ linear_split_kernel(ConvArgs a) {
             __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, tl[min(e, kSpan - 1)]), y_rsrc,
                                                   tid < 4 && e < elems ? e * 4 : kOut, 0, 0);
         }
+    }
+}
+
+template <int NBT>
+KernelFn pick_linear_pipe_ks(int ks) {
+    switch (ks) {
+    case 4: return linear_pipe_kernel<NBT, 4>;
+    case 8: return linear_pipe_kernel<NBT, 8>;
+    case 12: return linear_pipe_kernel<NBT, 12>;
+    case 16: return linear_pipe_kernel<NBT, 16>;
+    default: return nullptr;
     }
 }
 

@@ -141,7 +141,7 @@ CONFIG5_PLANS = {
         "mfma tiling=4 rows=64 cols=192 kc=64 xf=0 ln=none grid=442x1",
         "pre=rows mfma tiling=21 split-k halo rows=64 cols=96 kc=64 xf=0 ln=none grid=3534x2"),
     1: ("pre=rows parent-rows mfma tiling=21 split-k halo rows=64 cols=96 kc=64 xf=0 ln=none grid=28265x1",
-        "linear cols=96 ksteps=12 ln=none grid=768",
+        "linear pipe cols=96 ksteps=12 ln=none grid=512",
         "pre=rows mfma tiling=19 split-k rows=64 cols=96 kc=32 xf=0 ln=none grid=28265x1"),
 }
 

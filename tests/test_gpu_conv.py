@@ -199,6 +199,45 @@ def test_linear_kernel(s3dx, O, W, dtype, cin, cout, n, parent, res_parent, silu
     check_rel(got, ref, TOL[dtype])
 
 
+@pytest.mark.parametrize("cin,cout,n,parent,silu,bias", [
+    (192, 96, 226120, True, False, True),    # the mesh level-1 skip (parent rows); several blocks a wave
+    (256, 128, 28265, False, False, True),   # the SLat out-block skip
+    (128, 128, 100003, False, True, False),  # last block of 3 rows; SiLU, no bias
+    (64, 8, 33, False, True, True),          # one column block of 8 of 32 columns, a 1-row tail
+    (128, 40, 1, False, False, True),        # a single row
+    (192, 96, 4099, True, True, True),       # parent rows with a ragged last parent
+])
+def test_linear_pipe_kernel(s3dx, O, W, cin, cout, n, parent, silu, bias):
+    # BF16 1x1 layers with BF16 output and no residual run the pipelined
+    # kernel.  Its rows must equal, bit for bit, the plain linear kernel's
+    # FP32 output (same layer, same accumulation order) rounded to BF16, and
+    # match the oracle.
+    bf = s3dx.BF16
+    rows_in = (n + 7) // 8 if parent else n
+    x = W.normal_f32(19, 1, (rows_in, cin))
+    w = W.conv_weight(19, 2, cin, cout, kvol=1)
+    b = W.normal_f32(19, 3, (cout,)) if bias else None
+    conv = s3dx.SparseConv(cin, cout, 1, bf).set_weights(w, s3dx.WEIGHT_SLAT, b)
+    conv.set_gather_parent(parent).set_silu(silu)
+    plan = conv.plan(rows_in, n)
+    print(f"pipe cin={cin} cout={cout} n={n} parent={parent} silu={silu}: {plan}", flush=True)
+    assert plan.startswith(("parent-rows linear pipe", "linear pipe")), plan
+    xd = to_dev(s3dx, x, bf)
+    y = s3dx.DeviceArray((n, cout), np.uint16)
+    y32 = s3dx.DeviceArray((n, cout), np.float32)
+    conv.run(xd, rows_in, None, n, y, bf)
+    conv.run(xd, rows_in, None, n, y32, s3dx.F32)  # the plain kernel (FP32 output)
+    got = y.download()
+    assert np.array_equal(got, W.f32_to_bf16_bits(y32.download())), "pipe != plain kernel rounded"
+    rows = np.arange(n) if n <= 5000 else np.sort(np.random.default_rng(3).choice(n, 5000, replace=False))
+    xs = rnd(s3dx, x, bf)
+    xs = xs[rows >> 3] if parent else xs[rows]
+    h = O.conv(xs, None, len(rows), rnd(s3dx, w, bf), 0, cout, b, kvol=1)
+    if silu:
+        h = O.silu(h)
+    check_rel(W.bf16_bits_to_f32(got[rows]), h, TOL[bf])
+
+
 def test_transform_buffer_regrows(s3dx, O, W):
     # One layer object run on a small, a larger, then the small parent set:
     # the transformed-input buffer grows once and stays valid.
