@@ -178,8 +178,17 @@ struct KmapLookup4 {
             i[k] = static_cast<int32_t>(g / kOffsets);
             o[k] = static_cast<int32_t>(g - int64_t(i[k]) * kOffsets);
         }
+        // Every load of a stage is unconditional (an index that is not
+        // needed reads row 0 or window cell 0, both always present: a tile
+        // has rows and the window at least 2^18 cells) and its value is
+        // selected afterwards: a load under a condition compiles to a branch,
+        // and the compiler waits for each such load at its join, one round
+        // trip per entry.
 #pragma unroll
-        for (int k = 0; k < 4; ++k) c[k] = 4 * u + k < count ? coords[i[k]] : make_int4(-1, 0, 0, 0);
+        for (int k = 0; k < 4; ++k) c[k] = coords[min(i[k], n - 1)];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            if (4 * u + k >= count) c[k] = make_int4(-1, 0, 0, 0);
         unsigned long long v[4];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -189,8 +198,9 @@ struct KmapLookup4 {
                 add_fits(c[k].w, o[k] % 3 - 1, &q.w))
                 cell[k] = window_cell(q, h.wlog2);
             c[k] = q;
-            v[k] = cell[k] >= 0 ? h.cells[cell[k]] : 0ull;
         }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) v[k] = h.cells[cell[k] >= 0 ? cell[k] : 0];
         int4 rc[4];
         uint32_t r[4];
 #pragma unroll
@@ -199,8 +209,9 @@ struct KmapLookup4 {
             const bool tagged = cell[k] >= 0 && static_cast<uint32_t>(v[k] >> 32) ==
                                                     tag_of(h.seed, static_cast<uint32_t>(cell[k]));
             if (!tagged || r[k] >= static_cast<uint32_t>(n)) r[k] = 0xFFFFFFFFu;
-            rc[k] = r[k] != 0xFFFFFFFFu ? coords[r[k]] : make_int4(0, 0, 0, 0);
         }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) rc[k] = coords[r[k] != 0xFFFFFFFFu ? r[k] : 0u];
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             if (4 * u + k >= count) {
