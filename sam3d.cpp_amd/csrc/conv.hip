@@ -475,16 +475,22 @@ LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bo
         }
         // BF16 layers with Cin = 64, 128, 192 or 256: the pipelined kernel,
         // persistent workgroups over the 32-row blocks.
-        KernelFn pipe = bf && allow_pipe && !conv->ln && conv->cin % 16 == 0 && conv->cout % 8 == 0 &&
+        // Wider layers (a multiple of four column blocks): 128-column groups.
+        const int pnb = nbt <= 4 ? nbt : nbt % 4 == 0 ? 4 : 0;
+        KernelFn pipe = bf && allow_pipe && pnb && !conv->ln && conv->cin % 16 == 0 && conv->cout % 8 == 0 &&
                                 n_out * conv->cout * 2 < (int64_t(1) << 31)
-                            ? pick_linear_pipe_bf16(nbt, conv->cin / 16)
+                            ? pick_linear_pipe_bf16(pnb, conv->cin / 16)
                             : nullptr;
-        if (pipe && frags <= kLinearMaxFrags && !std::getenv("S3DX_CONV_TILING")) {
+        const int pfrags = conv->cin / 16 * pnb * 64;
+        if (pipe && pfrags <= kLinearMaxFrags && !std::getenv("S3DX_CONV_TILING")) {
             p.linear = p.pipe = true;
             p.fn = pipe;
-            p.nb = nbt;
-            p.smem = static_cast<unsigned>(frags) * 16 + 4 * 8 * (nbt * 32 + 4) * 4;
-            p.grid = dim3(static_cast<unsigned>(std::min<int64_t>((n_out + 127) / 128, resident_blocks(pipe, p.smem))));
+            p.nb = pnb;
+            p.smem = static_cast<unsigned>(pfrags) * 16 + 4 * 8 * (pnb * 32 + 4) * 4;
+            const int64_t groups = nbt / pnb;
+            const int64_t per_group = std::max<int64_t>(1, resident_blocks(pipe, p.smem) / groups);
+            p.grid = dim3(static_cast<unsigned>(std::min<int64_t>((n_out + 127) / 128, per_group)),
+                          static_cast<unsigned>(groups));
             return p;
         }
         if (fn && frags <= kLinearMaxFrags && !std::getenv("S3DX_CONV_TILING")) {
@@ -974,11 +980,13 @@ void describe_launch(const s3dx_conv *conv, const s3dx_gather_plan *gplan, int64
                                        p.fn == pick_halo_bf16_planned(64, 3));
         char text[256];
         const bool halo = p.mfma && !p.linear && p.tl->id >= 20 && p.tl->id <= 22;  // the halo-staged kernels
+        char groups[16] = "";
+        if (p.grid.y > 1) std::snprintf(groups, sizeof(groups), "x%u", p.grid.y);
         if (p.linear)
-            std::snprintf(text, sizeof(text), "linear%s cols=%d ksteps=%d%s ln=%s grid=%u", p.pipe ? " pipe" : "",
+            std::snprintf(text, sizeof(text), "linear%s cols=%d ksteps=%d%s ln=%s grid=%u%s", p.pipe ? " pipe" : "",
                           p.nb * 32,
                           conv->cin / (conv->dtype == S3DX_BF16 || p.split ? 16 : 8),
-                          p.split ? " terms=3" : "", conv->ln ? "separate" : "none", p.grid.x);
+                          p.split ? " terms=3" : "", conv->ln ? "separate" : "none", p.grid.x, groups);
         else if (p.mfma)
             std::snprintf(text, sizeof(text), "mfma tiling=%d%s%s rows=%d cols=%d kc=%d%s xf=%d ln=%s grid=%ux%u",
                           p.tl->id, p.tl->splitk ? " split-k" : "", halo ? " halo" : "", p.tl->rows(),

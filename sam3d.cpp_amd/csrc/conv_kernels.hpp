@@ -1482,10 +1482,14 @@ __global__ void __launch_bounds__(256) linear_kernel(ConvArgs a) {
 // as many dropped stores: the compiler's count of the memory operations
 // younger than a block's loads is then the same on every path, so the wait
 // for them never covers the previous block's stores.
+// Layers wider than NBT column blocks (NBT = 4, a multiple of 4 blocks) take
+// one group of NBT blocks per blockIdx.y, with that group's weights in LDS.
 template <int NBT, int KS>
 __global__ void __launch_bounds__(256) linear_pipe_kernel(ConvArgs a) {
     extern __shared__ uint4 wl[];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5;
+    const int nbtot = a.cout_pad / 32;       // column blocks of the layer
+    const int col0 = blockIdx.y * NBT * 32;  // this workgroup's first column
     constexpr int SLD = NBT * 32 + 4;                 // staging row stride (floats)
     constexpr int KP = (NBT * 32 + 63) / 64;          // 16-byte slots a lane per 8-row group
     constexpr int kStores = 4 * KP;                   // stores a block
@@ -1516,11 +1520,15 @@ __global__ void __launch_bounds__(256) linear_pipe_kernel(ConvArgs a) {
     float bias[NBT];
 #pragma unroll
     for (int cb = 0; cb < NBT; ++cb) {
-        const int col = cb * 32 + (lane & 31);
+        const int col = col0 + cb * 32 + (lane & 31);
         bias[cb] = a.bias && col < cout ? a.bias[col] : 0.0f;
     }
+    // The group's fragments: [ks][cb][64] of the layer's [ks][nbtot][64].
     const uint4 *wg = static_cast<const uint4 *>(a.w);
-    for (int f = tid; f < KS * NBT * 64; f += 256) wl[f] = wg[f];
+    for (int f = tid; f < KS * NBT * 64; f += 256) {
+        const int ks = f / (NBT * 64), rem = f - ks * (NBT * 64);
+        wl[f] = wg[(ks * nbtot + blockIdx.y * NBT) * 64 + rem];
+    }
     // The first block's rows stay in flight across the barrier below.
     int64_t blk = static_cast<int64_t>(blockIdx.x) * 4 + wave;
     uint4 fa[KS], fb[KS];
@@ -1529,14 +1537,16 @@ __global__ void __launch_bounds__(256) linear_pipe_kernel(ConvArgs a) {
     for (int k = 0; k < kStores; ++k)
         __builtin_amdgcn_raw_buffer_store_b128(u32x4{0u, 0u, 0u, 0u}, drop_rsrc, 16 * k, 0, 0);
     float *stg = reinterpret_cast<float *>(wl + KS * NBT * 64) + wave * 8 * SLD;
-    // Slot k of a lane: 16-byte piece i = lane + 64k of an 8-row group's span
-    // (8 * cout elements), at staging row i / (cout / 8), column 8 * (i % (cout / 8)).
-    const int ppr = cout / 8;
-    int soff[KP];
+    // Slot k of a lane: 16-byte piece i = lane + 64k of an 8-row group's
+    // columns col0 .. col0 + gcols, at staging row i / (gcols / 8), column
+    // 8 * (i % (gcols / 8)); goff is its element offset from the group's row 0.
+    const int ppr = min(cout - col0, NBT * 32) / 8;
+    int soff[KP], goff[KP];
 #pragma unroll
     for (int k = 0; k < KP; ++k) {
         const int i = min(lane + 64 * k, 8 * ppr - 1);
         soff[k] = (i / ppr) * SLD + (i % ppr) * 8;
+        goff[k] = (i / ppr) * cout + col0 + (i % ppr) * 8;
     }
     __syncthreads();
     auto run_block = [&](int64_t b, const uint4 (&f)[KS]) __attribute__((always_inline)) {
@@ -1570,7 +1580,7 @@ __global__ void __launch_bounds__(256) linear_pipe_kernel(ConvArgs a) {
                 const u32x4 v = {pack_bf16x2(p.x, p.y), pack_bf16x2(p.z, p.w), pack_bf16x2(q.x, q.y),
                                  pack_bf16x2(q.z, q.w)};
                 __builtin_amdgcn_raw_buffer_store_b128(
-                    v, y_rsrc, i < pieces ? static_cast<int32_t>((row0 * cout + i * 8) * 2) : kOut, 0, 0);
+                    v, y_rsrc, i < pieces ? static_cast<int32_t>((row0 * cout + goff[k]) * 2) : kOut, 0, 0);
             }
         }
     };

@@ -206,12 +206,19 @@ def test_linear_kernel(s3dx, O, W, dtype, cin, cout, n, parent, res_parent, silu
     (64, 8, 33, False, True, True),          # one column block of 8 of 32 columns, a 1-row tail
     (128, 40, 1, False, False, True),        # a single row
     (192, 96, 4099, True, True, True),       # parent rows with a ragged last parent
+    (128, 1024, 9503, False, False, True),   # the SLat 128->1024 skip: eight 128-column groups
+    (64, 512, 777, False, True, True),       # four groups, SiLU
+    (128, 1000, 301, False, False, True),    # eight groups, the last 104 columns wide
 ])
 def test_linear_pipe_kernel(s3dx, O, W, cin, cout, n, parent, silu, bias):
     # BF16 1x1 layers with BF16 output and no residual run the pipelined
-    # kernel.  Its rows must equal, bit for bit, the plain linear kernel's
-    # FP32 output (same layer, same accumulation order) rounded to BF16, and
-    # match the oracle.
+    # kernel.  Its rows must match the oracle and the same layer's FP32
+    # output rounded to BF16: bit for bit up to four column blocks, where
+    # that output comes from the plain linear kernel (same accumulation
+    # order); for wider layers, whose FP32 output comes from an MFMA tiling
+    # kernel that sums in another order, within BF16 rounding (2^-8
+    # relative) of it plus 1e-5 of its largest magnitude for the sums'
+    # FP32 differences.
     bf = s3dx.BF16
     rows_in = (n + 7) // 8 if parent else n
     x = W.normal_f32(19, 1, (rows_in, cin))
@@ -228,7 +235,6 @@ def test_linear_pipe_kernel(s3dx, O, W, cin, cout, n, parent, silu, bias):
     conv.run(xd, rows_in, None, n, y, bf)
     conv.run(xd, rows_in, None, n, y32, s3dx.F32)  # the plain kernel (FP32 output)
     got = y.download()
-    assert np.array_equal(got, W.f32_to_bf16_bits(y32.download())), "pipe != plain kernel rounded"
     rows = np.arange(n) if n <= 5000 else np.sort(np.random.default_rng(3).choice(n, 5000, replace=False))
     xs = rnd(s3dx, x, bf)
     xs = xs[rows >> 3] if parent else xs[rows]
@@ -236,6 +242,13 @@ def test_linear_pipe_kernel(s3dx, O, W, cin, cout, n, parent, silu, bias):
     if silu:
         h = O.silu(h)
     check_rel(W.bf16_bits_to_f32(got[rows]), h, TOL[bf])
+    f32 = y32.download()
+    if cout <= 128:
+        assert np.array_equal(got, W.f32_to_bf16_bits(f32)), "pipe != plain kernel rounded"
+    else:
+        d = np.abs(W.bf16_bits_to_f32(got) - f32)
+        assert np.all(d <= np.abs(f32) * 2.0 ** -8 + 1e-5 * np.abs(f32).max()), float(d.max())
+
 
 
 def test_transform_buffer_regrows(s3dx, O, W):
