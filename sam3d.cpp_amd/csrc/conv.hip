@@ -635,7 +635,9 @@ LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bo
             const bool nb3 = !nb4 && blocks % 3 == 0 && !conv->ln && tid != 20 && !(he && std::atoi(he) == 128);
             const int want = tid == 20 || tid == 21 ? tid : (he && std::atoi(he) == 128 ? 20 : 21);
             const bool chunks_ok = conv->cin % 64 == 0 || (conv->cin % 32 == 0 && tid == 21);
-            if (allowed && bf && conv->kvol == kMaxKvol && chunks_ok && (nb4 || nb3) && !p.xf && splitk_ok) {
+            // (the halo kernels read the map through a buffer resource: under 2 GiB)
+            const bool map_ok = n_out * kMaxKvol * 4 < (int64_t(1) << 31);
+            if (allowed && bf && conv->kvol == kMaxKvol && chunks_ok && (nb4 || nb3) && !p.xf && splitk_ok && map_ok) {
                 for (const Tiling &t : kTilings)
                     if (t.id == want) p.tl = &t;
                 p.nb = nb3 ? 3 : 4;
@@ -1171,6 +1173,8 @@ void gather_plan_build(s3dx_gather_plan *p, const s3dx_conv *conv, int64_t n_in,
                        int64_t n_out, s3dx_stream stream) {
     const Source src = source_of(conv, n_in);
     require(src.n_src <= INT32_MAX, "input rows exceed INT32_MAX");
+    // (the build reads the map through a buffer resource: under 2 GiB)
+    require(n_out * kMaxKvol * 4 < (int64_t(1) << 31), "kernel maps of 2 GiB or more have no gather plan");
     launch_gather_plan_build(p->rows, kmap, n_out, src.n_src, src.shift, p->d, as_stream(stream));
     launch_check("gather_plan_build");
     p->n_out = n_out;

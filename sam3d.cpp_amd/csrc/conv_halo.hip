@@ -140,21 +140,22 @@ struct TileDedupe {
     bool global_a;
 };
 // The tile's map slice read from memory: entries 4u..4u+3 of the tile
-// (16-byte aligned, ROWS * 108 bytes per tile); entries past `count` read
-// as -1.
+// (16-byte aligned, ROWS * 108 bytes per tile) by one unconditional 16-byte
+// buffer load, whose resource ends at the map's last entry: a buffer load
+// zero-fills each dword past the resource (checked on gfx950), and
+// dedupe_tile marks entries past `count` invalid whatever they read.  (A
+// load under a condition would compile to a branch, and the compiler waits
+// for each such load at its join.)
 struct SliceLoad {
     const int32_t *kmap;
-    __device__ __forceinline__ int4 operator()(int64_t m0, int u, int count) const {
-        const int4 *src = reinterpret_cast<const int4 *>(kmap + m0 * kMaxKvol);
-        int4 v = make_int4(-1, -1, -1, -1);
-        if (4 * u + 3 < count) {
-            v = src[u];
-        } else {
-            if (4 * u < count) v.x = kmap[m0 * kMaxKvol + 4 * u];
-            if (4 * u + 1 < count) v.y = kmap[m0 * kMaxKvol + 4 * u + 1];
-            if (4 * u + 2 < count) v.z = kmap[m0 * kMaxKvol + 4 * u + 2];
-        }
-        return v;
+    int32_t bytes;  // the map's size in bytes (rows * 108, under 2 GiB)
+    __device__ __forceinline__ int4 operator()(int64_t m0, int u, int) const {
+        const auto r = __builtin_amdgcn_make_buffer_rsrc(const_cast<int32_t *>(kmap), static_cast<short>(0), bytes,
+                                                         0x00020000);
+        const u32x4 v =
+            __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int32_t>((m0 * kMaxKvol + 4 * u) * 4), 0, 0);
+        return make_int4(static_cast<int32_t>(v.x), static_cast<int32_t>(v.y), static_cast<int32_t>(v.z),
+                         static_cast<int32_t>(v.w));
     }
 };
 
@@ -173,10 +174,13 @@ __device__ __forceinline__ TileDedupe dedupe_tile(Fetch fetch, int64_t n_src, in
     const int count = tile_rows * kMaxKvol;
     int sj[Q][4];
     {
+        // (slots past the slice fetch its last piece again and are marked
+        // invalid below: a fetch under `u < V4` would be a branch, and the
+        // compiler waits for each such load at its join)
 #pragma unroll
         for (int q = 0; q < Q; ++q) {
             const int u = tid + q * NTH;
-            const int4 v = u < V4 ? fetch(m0, u, count) : make_int4(-1, -1, -1, -1);
+            const int4 v = fetch(m0, min(u, V4 - 1), count);
             const int jv[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
@@ -386,8 +390,8 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_halo_kernel(ConvArg
         dd.distinct = __builtin_amdgcn_readfirstlane(hdr[1]);
         dd.mask = __builtin_amdgcn_readfirstlane(hdr[2]);
     } else {
-        dd = dedupe_tile<MB>(SliceLoad{a.kmap}, a.n_src, a.row_shift, m0, tile_rows, table, table32, bitmap, prefix, slot_row,
-                             misc);
+        dd = dedupe_tile<MB>(SliceLoad{a.kmap, static_cast<int32_t>(a.n_out * kMaxKvol * 4)}, a.n_src, a.row_shift, m0,
+                             tile_rows, table, table32, bitmap, prefix, slot_row, misc);
     }
     const uint32_t mask = dd.mask, distinct = dd.distinct;
     const bool global_a = dd.global_a;
@@ -1285,7 +1289,7 @@ __device__ __forceinline__ void plan_tile(Fetch fetch, int64_t n_out, int64_t n_
 template <int MB, int NTH>
 __global__ void __launch_bounds__(NTH) gather_plan_build_kernel(const int32_t *kmap, int64_t n_out, int64_t n_src,
                                                                 int32_t row_shift, char *plan) {
-    plan_tile<MB, NTH>(SliceLoad{kmap}, n_out, n_src, row_shift, plan);
+    plan_tile<MB, NTH>(SliceLoad{kmap, static_cast<int32_t>(n_out * kMaxKvol * 4)}, n_out, n_src, row_shift, plan);
 }
 
 // The tile's map slice computed by the lookups of the kernel map (and stored
