@@ -132,17 +132,35 @@ layernorm_vec_kernel(const void *x, int64_t n, int32_t c, int32_t lpr_log2, floa
     const bool active = row < n;
     float v[PPL][VE];
     float sum = 0.0f;
+    // The row's PPL pieces are loaded unconditionally (a piece or row past
+    // the end rereads the last one and is zeroed after) and widened only once
+    // all are issued: a load under a condition, or widened next to it, makes
+    // the compiler wait for each piece in turn.
+    {
+        const int64_t lrow = active ? row : n - 1;
+        uint4 raw[PPL];
 #pragma unroll
-    for (int p = 0; p < PPL; ++p) {
-        const int pi = p * lpr + sl;
-        if (active && pi < ppr) {
-            vload<TI, VE>(x, row * c + static_cast<int64_t>(pi) * VE, v[p]);
-        } else {
-#pragma unroll
-            for (int e = 0; e < VE; ++e) v[p][e] = 0.0f;
+        for (int p = 0; p < PPL; ++p) {
+            const int pi = min(p * lpr + sl, ppr - 1);
+            raw[p] = *reinterpret_cast<const uint4 *>(static_cast<const TI *>(x) + lrow * c +
+                                                      static_cast<int64_t>(pi) * VE);
         }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int e = 0; e < VE; ++e) sum += v[p][e];
+        for (int p = 0; p < PPL; ++p) {
+            const bool in = active && p * lpr + sl < ppr;
+            const uint32_t w4[4] = {raw[p].x, raw[p].y, raw[p].z, raw[p].w};
+#pragma unroll
+            for (int e = 0; e < VE; ++e) {
+                float f;
+                if constexpr (sizeof(TI) == 2)
+                    f = bf16_to_f32(static_cast<uint16_t>(e & 1 ? w4[e >> 1] >> 16 : w4[e >> 1] & 0xffffu));
+                else
+                    f = __builtin_bit_cast(float, w4[e]);
+                v[p][e] = in ? f : 0.0f;
+                sum += v[p][e];
+            }
+        }
     }
     for (int d = 1; d < lpr; d <<= 1) sum += __shfl_xor(sum, d, 64);
     const float mean = sum / static_cast<float>(c);
