@@ -219,6 +219,34 @@ __device__ __forceinline__ void load_residual(const ConvArgs &a, int64_t m0, int
     using RM = RowMap<TPR, BM, NTH>;
     const int cg = tid % TPR, rsub = tid / TPR;
     const int col0 = nb0 * 32 + cg * 8;
+    // Whole 16-byte pieces (cout % 8 == 0), a residual under 2 GiB and at
+    // most four passes (eight would spill in the 128-row split-K tiles): every
+    // pass issues the same two buffer loads whatever it finds (no residual:
+    // an empty resource; rows or columns outside the tile, and the second
+    // piece of BF16 rows: an offset the resource drops, reading zeros), so
+    // the passes' loads are in flight together -- with a load under a
+    // condition the compiler waits for each pass's at its join.
+    const int esz = a.y_bf16 ? 2 : 4;
+    const int64_t res_rows = (a.n_out + (int64_t(1) << a.residual_shift) - 1) >> a.residual_shift;
+    const int64_t res_bytes = a.residual ? res_rows * a.cout * esz : 0;
+    if (RM::PASSES <= 4 && a.cout % 8 == 0 && res_bytes < (int64_t(1) << 31)) {
+        const auto r_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(a.residual ? a.residual : a.y),
+                                                              static_cast<short>(0), static_cast<int32_t>(res_bytes),
+                                                              0x00020000);
+        constexpr int32_t kOut = int32_t(0x80000000);
+#pragma unroll
+        for (int p = 0; p < RM::PASSES; ++p) {
+            const int rl = p * RM::RPP + rsub;
+            const bool in = rsub < RM::RPP && rl < tile_rows && col0 < a.cout;
+            const int32_t off =
+                in ? static_cast<int32_t>((((m0 + rl) >> a.residual_shift) * a.cout + col0) * esz) : kOut;
+            const u32x4 v0 = __builtin_amdgcn_raw_buffer_load_b128(r_rsrc, off, 0, 0);
+            const u32x4 v1 = __builtin_amdgcn_raw_buffer_load_b128(r_rsrc, in && esz == 4 ? off + 16 : kOut, 0, 0);
+            res[p][0] = make_uint4(v0.x, v0.y, v0.z, v0.w);
+            res[p][1] = make_uint4(v1.x, v1.y, v1.z, v1.w);
+        }
+        return;
+    }
 #pragma unroll
     for (int p = 0; p < RM::PASSES; ++p) {
         res[p][0] = res[p][1] = make_uint4(0, 0, 0, 0);
