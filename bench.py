@@ -726,6 +726,8 @@ def main():
         "kmap_plan_ms": kmap_plan_ms,
         "block_ms": block_ms,
         "conv_kernel_ms": conv_ms,
+        "conv1_ms": statistics.mean(conv1_ms),
+        "conv2_ms": statistics.mean(conv2_ms),
         # The plan is per map (like the kernel map): this step amortizes it
         # over its two convs only, the SLat flow over every conv of a sample.
         "value_incl_gather_plan": 2 * flops / ((block_ms + gplan_ms) * 1e-3) / 1e12,
