@@ -354,8 +354,13 @@ S3DX_API s3dx_status s3dx_kmap_subm3_planned(const int32_t *coords, int64_t n, i
                                              char *error, uint64_t error_capacity);
 /* s3dx_conv_run with a gather plan built for the same kmap, n_out and source
  * rows (S3DX_INVALID_ARGUMENT when the sizes or the source setup differ).
- * Results are bit-identical to s3dx_conv_run; launches that do not use the
- * halo kernel ignore the plan. */
+ * Results are bit-identical to s3dx_conv_run, except for layers of at least
+ * 512 input channels whose 128-row tiles outnumber the CUs (e.g. 1024 -> 1024
+ * on 5,086 rows): with a 128-row plan those run in stream-K runs, equal runs
+ * of (tile, 64-channel chunk) units one per CU, and a tile split between
+ * runs adds its pieces in a fixed order, so results are deterministic but
+ * rounded differently from the unplanned run (within BF16 rounding).
+ * Launches that do not use the halo kernel ignore the plan. */
 S3DX_API s3dx_status s3dx_conv_run_planned(const s3dx_conv *conv, const s3dx_gather_plan *plan, const void *x,
                                            int64_t n_in, const int32_t *kmap, int64_t n_out, const void *residual,
                                            void *y, int32_t y_dtype, s3dx_stream stream, char *error,

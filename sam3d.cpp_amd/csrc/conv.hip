@@ -290,13 +290,17 @@ struct s3dx_conv {
     // output tile does not span the row), grown on demand like xin.
     mutable void *pre_ln = nullptr;
     mutable int64_t pre_ln_bytes = 0;
+    // Stream-K launches: two FP32 128 x 128 tiles per run for the pieces
+    // that are part of a tile, grown on demand like xin.
+    mutable void *sk_part = nullptr;
+    mutable int64_t sk_part_bytes = 0;
 
     bool transforms() const { return slot_offset != nullptr || pre_scale != nullptr; }
 
     ~s3dx_conv() {
         for (void *p : {w, w_split, static_cast<void *>(bias), static_cast<void *>(slot_offset),
                         static_cast<void *>(ln_w), static_cast<void *>(ln_b),
-                        static_cast<void *>(mod_scale), static_cast<void *>(mod_shift), xin, pre_ln})
+                        static_cast<void *>(mod_scale), static_cast<void *>(mod_shift), xin, pre_ln, sk_part})
             if (p) (void)hipFree(p);
     }
 };
@@ -378,6 +382,9 @@ struct LaunchPlan {
     bool split = false;     // linear_split_kernel: BF16 rows, three-term BF16 weights
     bool pipe = false;      // linear_pipe_kernel: BF16 layer, BF16 output, no residual
     bool half_chunk = false;  // halo kernel with a last chunk of 32 channels (64-row tiles only)
+    bool stream_k = false;    // the 8-wave kernel over equal runs of (group, tile, chunk) units
+    int64_t sk_units = 0;     // (column group, tile, chunk) units of a stream-K launch
+    int sk_groups = 0;        // its 128-column groups
     unsigned smem = 0;      // dynamic LDS bytes
     unsigned threads = 256; // workgroup size
     const Tiling *tl = nullptr;
@@ -657,10 +664,38 @@ LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bo
     return p;
 }
 
+// Runs of a stream-K launch of the 8-wave kernel (one workgroup per CU)
+// for a layer of Cin `cin` over `groups` 128-column groups, or 0 when whole
+// tiles suit it: fewer than 8 chunks of 64 channels (a piece would carry a
+// tile's fixed costs for little work), or no more tiles than CUs, or a tile
+// count the CUs divide.  With every tile in one pass over the CUs, whole
+// tiles walk the chunks in step, so an XCD's L2 holds one chunk's weights
+// at a time; runs starting at scattered chunks make it hold them all
+// (2048 -> 128 on 221 tiles: 289 us whole, 373 us in runs), which the
+// CUs left idle do not repay.  S3DX_STREAM_K=0 turns it off;
+// S3DX_STREAM_K_RUNS=<n> sets the run count (tests).
+int stream_k_runs(int cin, int64_t n_out, int64_t groups) {
+    if (const char *e = std::getenv("S3DX_STREAM_K"))
+        if (std::atoi(e) == 0) return 0;
+    const int64_t chunks = cin / 64;
+    if (cin % 64 != 0 || chunks < 8) return 0;
+    const int64_t tiles = (n_out + 127) / 128 * groups;
+    int64_t runs = device_cus();
+    bool forced = false;
+    if (const char *e = std::getenv("S3DX_STREAM_K_RUNS")) {
+        runs = std::atoi(e);
+        forced = true;
+    }
+    if (runs < 1 || runs > 65535 || tiles * chunks < 2 * runs) return 0;
+    if (!forced && (tiles <= runs || tiles % runs == 0)) return 0;
+    return static_cast<int>(runs);
+}
+
 // A planned launch: the halo kernel of the plan's tile height in place of
 // the unplanned halo kernel (64-row records: tiling 21 only; 128-row records:
-// tilings 20 and 21, on the 8-wave kernel).  Other launches are unchanged.
-void apply_gather_plan(LaunchPlan &p, const s3dx_gather_plan *g, int64_t n_out, bool bf16_rows) {
+// tilings 20 and 21, on the 8-wave kernel, in stream-K runs where those pay).
+// Other launches are unchanged.
+void apply_gather_plan(LaunchPlan &p, const s3dx_gather_plan *g, int64_t n_out, bool bf16_rows, int cin) {
     if (bf16_rows || !p.mfma || !p.tl || (p.tl->id != 20 && p.tl->id != 21)) return;
     if (g->rows == 64 && p.tl->id == 21) {
         p.fn = pick_halo_bf16_planned(64, p.nb);
@@ -669,7 +704,15 @@ void apply_gather_plan(LaunchPlan &p, const s3dx_gather_plan *g, int64_t n_out, 
             if (t.id == 22) p.tl = &t;
         p.fn = pick_halo_bf16_planned(128);
         p.threads = kHalo8Threads;
-        p.grid = dim3(static_cast<unsigned>((n_out + 127) / 128), p.grid.y);
+        const int64_t tiles = (n_out + 127) / 128;
+        p.grid = dim3(static_cast<unsigned>(tiles), p.grid.y);
+        if (const int runs = stream_k_runs(cin, n_out, p.grid.y)) {
+            p.fn = pick_halo8_stream_k();
+            p.stream_k = true;
+            p.sk_groups = static_cast<int>(p.grid.y);
+            p.sk_units = tiles * p.grid.y * (cin / 64);
+            p.grid = dim3(static_cast<unsigned>(runs), 1);
+        }
     }
 }
 
@@ -684,7 +727,7 @@ int gather_plan_rows(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out) {
     const LaunchPlan p = plan_launch(conv, x_bytes, n_out, true);
     if (!p.mfma || !p.tl || (p.tl->id != 20 && p.tl->id != 21) || p.nb != 4 || p.half_chunk) return 64;
     const int64_t tiles = (n_out + 127) / 128 * static_cast<int64_t>(p.grid.y);
-    return tiles <= device_cus() ? 128 : 64;
+    return tiles <= device_cus() || stream_k_runs(conv->cin, n_out, p.grid.y) ? 128 : 64;
 }
 
 float *upload_f32(const float *host, size_t count) {
@@ -976,10 +1019,10 @@ void describe_launch(const s3dx_conv *conv, const s3dx_gather_plan *gplan, int64
         if (gplan) {
             require(gplan->n_out == n_out && gplan->n_src == src.n_src && gplan->shift == src.shift,
                     "gather plan was built for another map size or source rows");
-            apply_gather_plan(p, gplan, n_out, bf16_rows);
+            apply_gather_plan(p, gplan, n_out, bf16_rows, conv->cin);
         }
         const bool planned = gplan && (p.fn == pick_halo_bf16_planned(64) || p.fn == pick_halo_bf16_planned(128) ||
-                                       p.fn == pick_halo_bf16_planned(64, 3));
+                                       p.fn == pick_halo_bf16_planned(64, 3) || p.stream_k);
         char text[256];
         const bool halo = p.mfma && !p.linear && p.tl->id >= 20 && p.tl->id <= 22;  // the halo-staged kernels
         char groups[16] = "";
@@ -990,8 +1033,9 @@ void describe_launch(const s3dx_conv *conv, const s3dx_gather_plan *gplan, int64
                           conv->cin / (conv->dtype == S3DX_BF16 || p.split ? 16 : 8),
                           p.split ? " terms=3" : "", conv->ln ? "separate" : "none", p.grid.x, groups);
         else if (p.mfma)
-            std::snprintf(text, sizeof(text), "mfma tiling=%d%s%s rows=%d cols=%d kc=%d%s xf=%d ln=%s grid=%ux%u",
-                          p.tl->id, p.tl->splitk ? " split-k" : "", halo ? " halo" : "", p.tl->rows(),
+            std::snprintf(text, sizeof(text), "mfma tiling=%d%s%s%s rows=%d cols=%d kc=%d%s xf=%d ln=%s grid=%ux%u",
+                          p.tl->id, p.tl->splitk ? " split-k" : "", halo ? " halo" : "",
+                          p.stream_k ? " stream-k" : "", p.tl->rows(),
                           halo ? p.nb * 32 : p.tl->cols(), p.kc, p.half_chunk ? "+32" : "",
                           p.xf ? 1 : 0, conv->ln ? (p.fused_ln ? "fused" : "separate") : "none", p.grid.x,
                           p.grid.y);
@@ -1115,9 +1159,9 @@ void conv_run_impl(const s3dx_conv *conv, const s3dx_gather_plan *gplan, const v
             require(gplan->n_out == n_out && gplan->n_src == src.n_src && gplan->shift == src.shift,
                     "gather plan was built for another map size or source rows");
             // Only the halo kernels read plans; other launches ignore it.
-            apply_gather_plan(plan, gplan, n_out, bf16_rows);
+            apply_gather_plan(plan, gplan, n_out, bf16_rows, conv->cin);
             if (plan.fn == pick_halo_bf16_planned(64) || plan.fn == pick_halo_bf16_planned(128) ||
-                plan.fn == pick_halo_bf16_planned(64, 3))
+                plan.fn == pick_halo_bf16_planned(64, 3) || plan.stream_k)
                 a.plan = gplan->d;
         }
         // A LayerNorm the epilogue cannot fuse runs as its own pass over the
@@ -1136,8 +1180,18 @@ void conv_run_impl(const s3dx_conv *conv, const s3dx_gather_plan *gplan, const v
             // The three-term kernel has an instantiation that reads a residual
             // (grid-stride over the same blocks, so the grid stands).
             if (plan.split && a.residual) plan.fn = pick_linear_split(plan.nb, conv->cin / 16, true);
+            if (plan.stream_k) {
+                a.sk_wgs = static_cast<int32_t>(plan.grid.x);
+                a.sk_units = plan.sk_units;
+                a.sk_partial = static_cast<float *>(layer_buffer(
+                    conv->sk_part, conv->sk_part_bytes, static_cast<int64_t>(plan.grid.x) * 2 * 128 * 128 * 4, s));
+            }
             hipLaunchKernelGGL(plan.fn, plan.grid, dim3(plan.threads), plan.smem, s, a);
             launch_check(plan.linear ? "conv_linear" : "conv_mfma");
+            if (plan.stream_k) {
+                launch_halo8_combine(a, (n_out + 127) / 128, plan.sk_groups, s);
+                launch_check("conv_halo8_combine");
+            }
         } else {
             a.ln = 0;
             if (bf) hipLaunchKernelGGL(conv_generic_kernel<uint16_t>, plan.grid, dim3(256), 0, s, a);

@@ -651,6 +651,16 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_halo_kernel(ConvArg
     finish_rows<TPR, ROWS, SM::STG_LD>(a, stg, part, m0, nb0, tile_rows, tid, res);
 }
 
+// Stream-K runs: run g takes units [sk_run_begin(g), sk_run_begin(g + 1)).
+__device__ __forceinline__ int64_t sk_run_begin(int64_t g, int64_t units, int32_t runs) { return g * units / runs; }
+// The run holding unit u (runs are non-empty when units >= runs).
+__device__ __forceinline__ int sk_run_of(int64_t u, int64_t units, int32_t runs) {
+    int g = static_cast<int>(min(static_cast<int64_t>(runs - 1), u * runs / units));
+    while (g + 1 < runs && sk_run_begin(g + 1, units, runs) <= u) ++g;
+    while (g > 0 && sk_run_begin(g, units, runs) > u) --g;
+    return g;
+}
+
 // 128-row x 128-column tiles read through 128-row gather-plan records: one
 // workgroup of 8 waves per CU, two waves per SIMD on the same tile.  Wave w
 // holds k-step ks = w % 4 of every 64-channel chunk for column half
@@ -667,7 +677,19 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_halo_kernel(ConvArg
 // k-step partials of column block c are summed as ((P_c + P_c+1) + P_c+2) +
 // P_c+3 (indices mod 4), the order of the 64-row kernel's reduction, so the
 // two kernels' results are bit-identical.
-__global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a) {
+//
+// Stream-K launches (SK, conv_halo8_sk_kernel): the (column group, tile,
+// chunk) units of the layer, column-group-major, are cut into sk_wgs equal
+// runs, one per workgroup (one workgroup per CU), so that every CU gets the
+// same number of chunk-units whatever the tile count.  A run covers pieces
+// of consecutive tiles: a piece that is a whole tile is finished here; a
+// piece that is part of a tile (at most the first and the last of a run)
+// leaves its FP32 tile in the run's partial slot 0 or 1, and
+// halo8_combine_kernel adds a tile's pieces in chunk order and finishes it.
+// A piece of chunks [c0, c1) reads x and the weights from chunk c0 on, so
+// the chunk loop is the whole-tile loop on a narrower input.
+template <bool SK>
+__device__ __forceinline__ void halo8_body(const ConvArgs &a) {
     constexpr int ROWS = 128;
     constexpr int STG_LD = 128;
     __shared__ __align__(16) char smem[kH8Bytes];
@@ -677,22 +699,34 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
     const int32_t *table32 = reinterpret_cast<const int32_t *>(rec + kPlan128Table);
     const uint32_t *slot_row = reinterpret_cast<const uint32_t *>(rec + kPlan128Slots);
 
-    const int tid = threadIdx.x, lane = tid & 63;
+    const int nbtot = a.cout_pad / 32;
+    const int ksteps_total = a.cin / 16;
+    const int chunks_all = a.cin / kHChunk;
+    auto piece = [&](const int tile, const int nb0, const int cbeg, const int cend, float *const part_out)
+        __attribute__((always_inline)) {
+    // (stream-K: the thread index passes an empty asm in each piece, so that
+    // what derives from it is computed per piece, as in the one-piece
+    // kernel, not hoisted out of the run's loop and held -- spilled -- across
+    // every piece)
+    int tid_v = static_cast<int>(threadIdx.x);
+    if constexpr (SK) asm volatile("" : "+v"(tid_v));
+    const int tid = tid_v, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ks = wave & 3, ch = wave >> 2;
     const int half = lane >> 5;
-    const int tile = xcd_tile(blockIdx.x, gridDim.x);
     const int64_t m0 = static_cast<int64_t>(tile) * ROWS;
-    const int nb0 = blockIdx.y * 4;
-    const int nbtot = a.cout_pad / 32;
-    const int ksteps_total = a.cin / 16;
-    const int chunks = a.cin / kHChunk;
+    const int chunks = cend - cbeg;
     const int tile_rows = static_cast<int>(min(static_cast<int64_t>(ROWS), a.n_out - m0));
-    const int32_t xbytes = static_cast<int32_t>(a.x_bytes < INT32_MAX ? a.x_bytes : INT32_MAX);
-    const int64_t w_bytes = static_cast<int64_t>(kMaxKvol) * a.cin * a.cout_pad * 2;
-    const auto w_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(a.w), static_cast<short>(0),
-                                                          static_cast<int32_t>(w_bytes), 0x00020000);
-    const auto x_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(a.x), static_cast<short>(0),
+    // x and the weights from chunk cbeg on
+    const char *const xbase = static_cast<const char *>(a.x) + static_cast<int64_t>(cbeg) * kHRowBytes;
+    const int64_t x_rest = a.x_bytes - static_cast<int64_t>(cbeg) * kHRowBytes;
+    const int32_t xbytes = static_cast<int32_t>(x_rest < INT32_MAX ? x_rest : INT32_MAX);
+    const int64_t w_skip = static_cast<int64_t>(cbeg) * 4 * nbtot * 1024;
+    const int64_t w_bytes = static_cast<int64_t>(kMaxKvol) * a.cin * a.cout_pad * 2 - w_skip;
+    const auto w_rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char *>(static_cast<const char *>(a.w) + w_skip), static_cast<short>(0),
+        static_cast<int32_t>(w_bytes), 0x00020000);
+    const auto x_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(xbase), static_cast<short>(0),
                                                           xbytes, 0x00020000);
 
     // ---- 1. the tile's plan record, straight into LDS (1 KiB per instruction)
@@ -881,7 +915,7 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
     #pragma unroll
                     for (int k = 0; k < R; ++k) bq[k][0] = t[(k + r) % R][0], bq[k][1] = t[(k + r) % R][1];
         };
-        if constexpr (!GA) halo_copy(0, halo, slot_row, static_cast<const char *>(a.x));
+        if constexpr (!GA) halo_copy(0, halo, slot_row, xbase);
 #pragma unroll
         for (int k = 0; k < R; ++k) {
             next_b(bq[k]);
@@ -968,7 +1002,7 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
             rotate_b(left);
         };
         for (int c = 0; c < chunks; ++c)
-            chunk(c, buf_of(c), buf_of(c + 1), table32, slot_row, static_cast<const char *>(a.x));
+            chunk(c, buf_of(c), buf_of(c + 1), table32, slot_row, xbase);
     };
 
     // Two-buffer halo tiles whose rows have neighbours at all 27 offsets
@@ -1019,7 +1053,7 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
         uint4 bf[RF][2];
         int32_t wb = w_first;  // weights of the next task to request
         {
-            const auto x_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(a.x), static_cast<short>(0),
+            const auto x_rsrc = __builtin_amdgcn_make_buffer_rsrc(const_cast<char *>(xbase), static_cast<short>(0),
                                                                   xbytes, 0x00020000);
 #pragma unroll
             for (int j = 0; j < kPieces; ++j) piece(x_rsrc, j, 0, piece_off[j], halo + piece_group[j] * 1024);
@@ -1076,7 +1110,7 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
             // buffer of chunk c-1
             __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * RF));
             __syncthreads();
-            chunk(c, buf_of(c), buf_of(c + 1), table32, static_cast<const char *>(a.x));
+            chunk(c, buf_of(c), buf_of(c + 1), table32, xbase);
         }
     };
     if (dbl && !global_a && mask == (1u << kMaxKvol) - 1u) {
@@ -1224,7 +1258,93 @@ __global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a
         }
         write_stg();
     }
+    if (SK && part_out) {
+        // part of a tile: its FP32 tile, rows in order, to the partial slot
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < ROWS * STG_LD / 4 / kHalo8Threads; ++k) {
+            const int pc = tid + k * kHalo8Threads, row = pc >> 5, col = (pc & 31) * 4;
+            reinterpret_cast<float4 *>(part_out)[pc] =
+                *reinterpret_cast<const float4 *>(stg + row * STG_LD + (col ^ (((row >> 2) & 1) << 5)));
+        }
+    } else {
+        load_row_mod(a, nb0 * 32 + (tid % 16) * 8, params);
+        uint4 res[RowMap<16, ROWS, kHalo8Threads>::PASSES][2];
+        load_residual<16, ROWS, kHalo8Threads>(a, m0, nb0, tile_rows, tid, res);
+        __syncthreads();
+        finish_rows<16, ROWS, STG_LD, kHalo8Threads, true>(a, stg, stg, m0, nb0, tile_rows, tid, res, params);
+    }
+    };
+    if constexpr (!SK) {
+        piece(xcd_tile(blockIdx.x, gridDim.x), blockIdx.y * 4, 0, chunks_all, nullptr);
+    } else {
+        const int64_t tiles = (a.n_out + ROWS - 1) / ROWS;
+        const int g = xcd_tile(blockIdx.x, gridDim.x);  // XCD-contiguous runs
+        const int64_t u1 = sk_run_begin(g + 1, a.sk_units, a.sk_wgs);
+        int slot = 0;
+        for (int64_t u = sk_run_begin(g, a.sk_units, a.sk_wgs); u < u1;) {
+            const int64_t gt = u / chunks_all;  // column group * tiles + tile
+            const int cb = static_cast<int>(u - gt * chunks_all);
+            const int ce = static_cast<int>(min(static_cast<int64_t>(chunks_all), cb + (u1 - u)));
+            const int grp = static_cast<int>(gt / tiles);
+            const bool whole = cb == 0 && ce == chunks_all;
+            __syncthreads();  // the previous piece is done with LDS
+            piece(static_cast<int>(gt - grp * tiles), grp * 4, cb, ce,
+                  whole ? nullptr : a.sk_partial + (static_cast<int64_t>(g) * 2 + slot) * (ROWS * STG_LD));
+            slot += whole ? 0 : 1;
+            u += ce - cb;
+        }
+    }
+}
+
+__global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_kernel(ConvArgs a) { halo8_body<false>(a); }
+__global__ void __launch_bounds__(kHalo8Threads, 1) conv_halo8_sk_kernel(ConvArgs a) { halo8_body<true>(a); }
+
+// The tiles that stream-K runs left in parts: the pieces' FP32 tiles added
+// in chunk order (the runs in order), then the epilogue of the whole-tile
+// path.  One workgroup per (tile, column group); tiles that one run covers
+// whole were finished by the conv kernel and are skipped.
+__global__ void __launch_bounds__(kHalo8Threads, 1) halo8_combine_kernel(ConvArgs a) {
+    constexpr int ROWS = 128, STG_LD = 128;
+    __shared__ __align__(16) float stg[ROWS * STG_LD];
+    const int tid = threadIdx.x;
+    const int64_t tiles = gridDim.x;
+    const int tile = blockIdx.x, nb0 = blockIdx.y * 4;
+    const int chunks = a.cin / kHChunk;
+    const int64_t uf = (static_cast<int64_t>(blockIdx.y) * tiles + tile) * chunks, ul = uf + chunks - 1;
+    const int gf = sk_run_of(uf, a.sk_units, a.sk_wgs), gl = sk_run_of(ul, a.sk_units, a.sk_wgs);
+    if (gf == gl) return;
+    const int64_t m0 = static_cast<int64_t>(tile) * ROWS;
+    const int tile_rows = static_cast<int>(min(static_cast<int64_t>(ROWS), a.n_out - m0));
+    RowParams params;
+    load_row_params(a, nb0 * 32 + (tid % 16) * 8, params);
     load_row_mod(a, nb0 * 32 + (tid % 16) * 8, params);
+    constexpr int K = ROWS * STG_LD / 4 / kHalo8Threads;
+    float4 sum[K];
+    for (int g = gf; g <= gl; ++g) {
+        // this tile's piece is run g's second partial one when the run began
+        // in the middle of an earlier tile
+        const int64_t b = sk_run_begin(g, a.sk_units, a.sk_wgs);
+        const int slot = b < uf && b % chunks != 0 ? 1 : 0;
+        const float4 *src = reinterpret_cast<const float4 *>(a.sk_partial + (static_cast<int64_t>(g) * 2 + slot) * (ROWS * STG_LD));
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            const float4 v = src[tid + k * kHalo8Threads];
+            if (g == gf) {
+                sum[k] = v;
+            } else {
+                sum[k].x += v.x;
+                sum[k].y += v.y;
+                sum[k].z += v.z;
+                sum[k].w += v.w;
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int pc = tid + k * kHalo8Threads, row = pc >> 5, col = (pc & 31) * 4;
+        *reinterpret_cast<float4 *>(stg + row * STG_LD + (col ^ (((row >> 2) & 1) << 5))) = sum[k];
+    }
     uint4 res[RowMap<16, ROWS, kHalo8Threads>::PASSES][2];
     load_residual<16, ROWS, kHalo8Threads>(a, m0, nb0, tile_rows, tid, res);
     __syncthreads();
@@ -1323,6 +1443,13 @@ void launch_kmap_plan(int rows, const int32_t *coords, int64_t n, int32_t missin
 KernelFn pick_halo_bf16(int rows, int nb) {
     if (nb == 3) return rows == 64 ? conv_halo_kernel<2, false, 3> : nullptr;
     return rows == 128 ? conv_halo_kernel<4, false> : rows == 64 ? conv_halo_kernel<2, false> : nullptr;
+}
+
+KernelFn pick_halo8_stream_k() { return conv_halo8_sk_kernel; }
+
+void launch_halo8_combine(const ConvArgs &a, int64_t tiles, int groups, hipStream_t stream) {
+    hipLaunchKernelGGL(halo8_combine_kernel, dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(groups)),
+                       dim3(kHalo8Threads), 0, stream, a);
 }
 
 KernelFn pick_halo_bf16_planned(int rows, int nb) {

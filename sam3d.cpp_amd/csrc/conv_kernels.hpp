@@ -34,6 +34,12 @@ struct ConvArgs {
     const float *mod_shift;
     int32_t silu;
     const void *plan;  // per-tile gather plan records (halo kernel), or nullptr
+    // Stream-K launches of the 8-wave halo kernel: sk_wgs equal runs over the
+    // sk_units (column group, tile, chunk) units, and two FP32 128 x 128 tile
+    // slots per run for the pieces that are part of a tile.
+    int32_t sk_wgs;
+    int64_t sk_units;
+    float *sk_partial;
 };
 
 using KernelFn = void (*)(ConvArgs);
@@ -83,6 +89,11 @@ KernelFn pick_halo_bf16(int rows, int nb = 4);
 // record's bytes.
 KernelFn pick_halo_bf16_planned(int rows, int nb = 4);
 constexpr int kHalo8Threads = 512;
+// The 8-wave kernel's stream-K variant (grid: a.sk_wgs runs of one
+// workgroup, kHalo8Threads threads), and the pass that finishes the tiles its
+// runs left in parts (after it, on the same stream).
+KernelFn pick_halo8_stream_k();
+void launch_halo8_combine(const ConvArgs &a, int64_t tiles, int groups, hipStream_t stream);
 void launch_gather_plan_build(int rows, const int32_t *kmap, int64_t n_out, int64_t n_src, int32_t row_shift,
                               void *plan, hipStream_t stream);
 // Kernel map of coords (insert, then one workgroup per plan tile computing

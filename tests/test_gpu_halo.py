@@ -133,24 +133,93 @@ def test_planned_run_equals_unplanned(s3dx, O, W, monkeypatch, case):
     check_rel(_host(W, y1), _oracle(O, W, x, kmap, n, cin, cout, 40, ln, res), 1e-2, case)
 
 
-def test_planned_config3_rows(s3dx, O, W):
-    # 1024 -> 1024 on the 5,086 coarse rows: eight column blocks share each
-    # tile's plan record.
+def test_planned_config3_rows(s3dx, O, W, monkeypatch):
+    # 1024 -> 1024 on the 5,086 coarse rows.  40 x 8 128-row tiles are more
+    # than the CUs: the planned run takes stream-K runs of the 8-wave kernel
+    # (equal runs of (column group, tile, chunk) units, one per CU), the same
+    # bits on every run and within BF16 rounding of the oracle.  With
+    # stream-K off it takes 64-row records and equals the unplanned run bit
+    # for bit, as every other planned run does.
     fine = W.shells_union(0)
     nc, coarse, _, _, _ = O.coarsen2(fine)
     coarse = np.ascontiguousarray(coarse[:nc])
     kmap = O.kmap_subm3(coarse, nc)
     c = 1024
-    conv = s3dx.SparseConv(c, c, 27, s3dx.BF16).set_weights(W.conv_weight(0, 301, c, c), s3dx.WEIGHT_SLAT, None)
-    xd, kd = _bf(s3dx, W, W.round_bf16(W.normal_f32(0, 300, (nc, c)))), s3dx.DeviceArray.from_host(kmap)
+    w = W.conv_weight(0, 301, c, c)
+    conv = s3dx.SparseConv(c, c, 27, s3dx.BF16).set_weights(w, s3dx.WEIGHT_SLAT, None)
+    x = W.round_bf16(W.normal_f32(0, 300, (nc, c)))
+    xd, kd = _bf(s3dx, W, x), s3dx.DeviceArray.from_host(kmap)
     gp = conv.gather_plan(nc, kd, nc)
     planned = conv.plan(nc, nc, gp)
-    # 40 x 8 128-row tiles would need two passes over 256 CUs: 64-row records
-    assert planned.startswith("mfma tiling=21 split-k halo rows=64") and planned.endswith("grid=80x8 plan=64"), planned
-    y0, y1 = s3dx.DeviceArray((nc, c), np.uint16), s3dx.DeviceArray((nc, c), np.uint16)
+    print(f"config 3 planned: {planned}", flush=True)
+    assert planned.startswith("mfma tiling=22 split-k halo stream-k rows=128 cols=128") and \
+        planned.endswith(" plan=128"), planned
+    y0, y1, y2 = (s3dx.DeviceArray((nc, c), np.uint16) for _ in range(3))
     conv.run(xd, nc, kd, nc, y0, s3dx.BF16)
     conv.run(xd, nc, kd, nc, y1, s3dx.BF16, plan=gp)
-    assert np.array_equal(y0.download(), y1.download())
+    conv.run(xd, nc, kd, nc, y2, s3dx.BF16, plan=gp)
+    assert np.array_equal(y1.download(), y2.download()), "stream-K runs differ between launches"
+    rows = np.sort(np.random.default_rng(3).choice(nc, 600, replace=False))
+    ref = O.conv(x, kmap[rows], nc, W.round_bf16(w), 0, c, None)
+    check_rel(_host(W, y1)[rows], ref, 1e-2, "config 3 stream-K")
+    check_rel(_host(W, y0)[rows], ref, 1e-2, "config 3 unplanned")
+    monkeypatch.setenv("S3DX_STREAM_K", "0")
+    gp64 = conv.gather_plan(nc, kd, nc)
+    planned = conv.plan(nc, nc, gp64)
+    assert planned.startswith("mfma tiling=21 split-k halo rows=64") and planned.endswith("grid=80x8 plan=64"), planned
+    conv.run(xd, nc, kd, nc, y2, s3dx.BF16, plan=gp64)
+    assert np.array_equal(y0.download(), y2.download())
+
+
+# Stream-K runs forced to a run count that cuts tiles at many places: runs
+# that end mid-tile, runs covering several whole tiles, runs that fall
+# inside one tile (a tile in four or more pieces), tiles in global-gather
+# mode, two column groups with a residual, and the LayerNorm + modulate +
+# SiLU epilogue after the pieces are added.  Each against the float64 oracle
+# on sampled rows, and the same bits on a second launch.
+STREAM_K = {
+    # name: (coords builder, cin, cout, LayerNorm+modulate+SiLU, residual, runs)
+    "shells_3000_cin512_ln_7runs": (lambda W: W.shells_union(1)[:3000], 512, 128, True, False, 7),
+    "shells_3000_cin512_cout256_res_13runs": (lambda W: W.shells_union(1)[:3000], 512, 256, False, True, 13),
+    "shells_3000_cin1024_100runs": (lambda W: W.shells_union(1)[:3000], 1024, 128, False, False, 100),
+    "shuffled_cube_13824_cin512_ln_9runs": (lambda W: _dense_cube(24, 0), 512, 128, True, True, 9),
+    "tiny_200_cin1024_res_3runs": (lambda W: W.shells_union(2)[:200], 1024, 128, False, True, 3),
+}
+
+
+@pytest.mark.parametrize("case", list(STREAM_K))
+def test_stream_k_runs(s3dx, O, W, monkeypatch, case):
+    build, cin, cout, ln, with_res, runs = STREAM_K[case]
+    coords = build(W)
+    n = coords.shape[0]
+    kmap = O.kmap_subm3(coords, n)
+    seed = 90 + runs
+    w, b = W.conv_weight(seed, 2, cin, cout), W.normal_f32(seed, 3, (cout,), 0.1)
+    conv = s3dx.SparseConv(cin, cout, 27, s3dx.BF16).set_weights(w, s3dx.WEIGHT_SLAT, b)
+    scale, shift = W.normal_f32(seed, 4, (cout,), 0.3), W.normal_f32(seed, 5, (cout,), 0.3)
+    if ln:
+        conv.set_layernorm(True, 1e-6).set_modulate(s3dx.DeviceArray.from_host(scale),
+                                                     s3dx.DeviceArray.from_host(shift)).set_silu(True)
+    x = W.round_bf16(W.normal_f32(seed, 1, (n, cin)))
+    res = W.round_bf16(W.normal_f32(seed, 6, (n, cout))) if with_res else None
+    xd, kd = _bf(s3dx, W, x), s3dx.DeviceArray.from_host(kmap)
+    rd = _bf(s3dx, W, res) if with_res else None
+    monkeypatch.setenv("S3DX_STREAM_K_RUNS", str(runs))
+    gp = conv.gather_plan(n, kd, n)
+    plan = conv.plan(n, n, gp)
+    print(f"{case}: {plan}", flush=True)
+    assert " stream-k " in plan and f"grid={runs}x1" in plan and plan.endswith(" plan=128"), plan
+    y1, y2 = s3dx.DeviceArray((n, cout), np.uint16), s3dx.DeviceArray((n, cout), np.uint16)
+    conv.run(xd, n, kd, n, y1, s3dx.BF16, rd, plan=gp)
+    conv.run(xd, n, kd, n, y2, s3dx.BF16, rd, plan=gp)
+    assert np.array_equal(y1.download(), y2.download()), "stream-K runs differ between launches"
+    rows = np.sort(np.random.default_rng(seed).choice(n, min(n, 500), replace=False))
+    h = O.conv(x, kmap[rows], n, W.round_bf16(w), 0, cout, b)
+    if ln:
+        h = O.silu(O.modulate(O.layernorm(h, 1e-6), scale, shift))
+    if with_res:
+        h = h + res[rows]
+    check_rel(_host(W, y1)[rows], h, 1e-2, case)
 
 
 # Layers whose columns come in 96 but not 128 (the mesh decoder's 192 and 96
