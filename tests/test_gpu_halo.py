@@ -178,18 +178,22 @@ def test_planned_config3_rows(s3dx, O, W, monkeypatch):
 # SiLU epilogue after the pieces are added.  Each against the float64 oracle
 # on sampled rows, and the same bits on a second launch.
 STREAM_K = {
-    # name: (coords builder, cin, cout, LayerNorm+modulate+SiLU, residual, runs)
-    "shells_3000_cin512_ln_7runs": (lambda W: W.shells_union(1)[:3000], 512, 128, True, False, 7),
-    "shells_3000_cin512_cout256_res_13runs": (lambda W: W.shells_union(1)[:3000], 512, 256, False, True, 13),
-    "shells_3000_cin1024_100runs": (lambda W: W.shells_union(1)[:3000], 1024, 128, False, False, 100),
-    "shuffled_cube_13824_cin512_ln_9runs": (lambda W: _dense_cube(24, 0), 512, 128, True, True, 9),
-    "tiny_200_cin1024_res_3runs": (lambda W: W.shells_union(2)[:200], 1024, 128, False, True, 3),
+    # name: (coords builder, cin, cout, LayerNorm+modulate+SiLU, residual, runs, FP32 output)
+    "shells_3000_cin512_ln_7runs": (lambda W: W.shells_union(1)[:3000], 512, 128, True, False, 7, False),
+    "shells_3000_cin512_cout256_res_13runs": (lambda W: W.shells_union(1)[:3000], 512, 256, False, True, 13, False),
+    "shells_3000_cin1024_100runs": (lambda W: W.shells_union(1)[:3000], 1024, 128, False, False, 100, False),
+    "shuffled_cube_13824_cin512_ln_9runs": (lambda W: _dense_cube(24, 0), 512, 128, True, True, 9, False),
+    "tiny_200_cin1024_res_3runs": (lambda W: W.shells_union(2)[:200], 1024, 128, False, True, 3, False),
+    # FP32 rows out of both passes: a LayerNorm wider than the tile (its own
+    # pass over the conv's FP32 rows), and FP32 output asked of a BF16 layer
+    "shells_3000_cin512_cout512_ln_11runs": (lambda W: W.shells_union(1)[:3000], 512, 512, True, True, 11, False),
+    "shells_3000_cin768_f32out_res_17runs": (lambda W: W.shells_union(1)[:3000], 768, 128, False, True, 17, True),
 }
 
 
 @pytest.mark.parametrize("case", list(STREAM_K))
 def test_stream_k_runs(s3dx, O, W, monkeypatch, case):
-    build, cin, cout, ln, with_res, runs = STREAM_K[case]
+    build, cin, cout, ln, with_res, runs, f32_out = STREAM_K[case]
     coords = build(W)
     n = coords.shape[0]
     kmap = O.kmap_subm3(coords, n)
@@ -203,15 +207,18 @@ def test_stream_k_runs(s3dx, O, W, monkeypatch, case):
     x = W.round_bf16(W.normal_f32(seed, 1, (n, cin)))
     res = W.round_bf16(W.normal_f32(seed, 6, (n, cout))) if with_res else None
     xd, kd = _bf(s3dx, W, x), s3dx.DeviceArray.from_host(kmap)
-    rd = _bf(s3dx, W, res) if with_res else None
+    # (the residual comes in the output's dtype)
+    rd = None if not with_res else (s3dx.DeviceArray.from_host(np.ascontiguousarray(res, np.float32)) if f32_out
+                                    else _bf(s3dx, W, res))
     monkeypatch.setenv("S3DX_STREAM_K_RUNS", str(runs))
     gp = conv.gather_plan(n, kd, n)
     plan = conv.plan(n, n, gp)
     print(f"{case}: {plan}", flush=True)
     assert " stream-k " in plan and f"grid={runs}x1" in plan and plan.endswith(" plan=128"), plan
-    y1, y2 = s3dx.DeviceArray((n, cout), np.uint16), s3dx.DeviceArray((n, cout), np.uint16)
-    conv.run(xd, n, kd, n, y1, s3dx.BF16, rd, plan=gp)
-    conv.run(xd, n, kd, n, y2, s3dx.BF16, rd, plan=gp)
+    ydt, ystore = (s3dx.F32, np.float32) if f32_out else (s3dx.BF16, np.uint16)
+    y1, y2 = s3dx.DeviceArray((n, cout), ystore), s3dx.DeviceArray((n, cout), ystore)
+    conv.run(xd, n, kd, n, y1, ydt, rd, plan=gp)
+    conv.run(xd, n, kd, n, y2, ydt, rd, plan=gp)
     assert np.array_equal(y1.download(), y2.download()), "stream-K runs differ between launches"
     rows = np.sort(np.random.default_rng(seed).choice(n, min(n, 500), replace=False))
     h = O.conv(x, kmap[rows], n, W.round_bf16(w), 0, cout, b)
@@ -219,7 +226,8 @@ def test_stream_k_runs(s3dx, O, W, monkeypatch, case):
         h = O.silu(O.modulate(O.layernorm(h, 1e-6), scale, shift))
     if with_res:
         h = h + res[rows]
-    check_rel(_host(W, y1)[rows], h, 1e-2, case)
+    got = y1.download() if f32_out else _host(W, y1)
+    check_rel(got[rows], h, 1e-2, case)
 
 
 # Layers whose columns come in 96 but not 128 (the mesh decoder's 192 and 96
