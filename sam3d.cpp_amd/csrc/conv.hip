@@ -385,6 +385,7 @@ struct LaunchPlan {
     bool stream_k = false;    // the 8-wave kernel over equal runs of (group, tile, chunk) units
     int64_t sk_units = 0;     // (column group, tile, chunk) units of a stream-K launch
     int sk_groups = 0;        // its 128-column groups
+    bool sk_splitk = false;   // the stream-K runs are the FP32 split-K kernel's (64-row tiles)
     unsigned smem = 0;      // dynamic LDS bytes
     unsigned threads = 256; // workgroup size
     const Tiling *tl = nullptr;
@@ -657,6 +658,30 @@ LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bo
         require(p.fn != nullptr, "no MFMA kernel for this shape");
         const int64_t mt = (n_out + p.tl->rows() - 1) / p.tl->rows();
         p.grid = dim3(static_cast<unsigned>(mt), static_cast<unsigned>(blocks / p.nb));
+        // FP32 tiling 18 over long tiles that take more than one pass at two
+        // workgroups per CU: stream-K runs, two per CU (the workgroups are
+        // latency-bound, so a pass costs about the same however full it is:
+        // 1024 -> 1024 on 5,086 rows, 640 workgroups, ran 1.52x the time of
+        // the 512 of 4,096 rows).  S3DX_STREAM_K=0 turns it off.
+        if (p.tl->id == 18 && !bf && p.kc == 32 && p.nb == 4 && !p.xf && conv->kvol == kMaxKvol) {
+            const char *off = std::getenv("S3DX_STREAM_K");
+            const int64_t wgs = mt * p.grid.y, ntf = int64_t(kMaxKvol) * (conv->cin / 32);
+            int64_t runs = 2 * device_cus();
+            bool forced = false;
+            if (const char *e = std::getenv("S3DX_STREAM_K_RUNS")) {
+                runs = std::atoi(e);
+                forced = true;
+            }
+            const bool want = forced ? true : wgs > runs && wgs % runs != 0 && ntf >= 256;
+            if (!(off && std::atoi(off) == 0) && want && runs >= 1 && runs <= 65535 && wgs * ntf >= 2 * runs) {
+                p.stream_k = true;
+                p.sk_splitk = true;
+                p.sk_groups = static_cast<int>(p.grid.y);
+                p.sk_units = wgs * ntf;
+                p.fn = pick_splitk_stream_k_f32();
+                p.grid = dim3(static_cast<unsigned>(runs), 1);
+            }
+        }
     } else {
         p.grid = dim3(static_cast<unsigned>((n_out + kGM - 1) / kGM),
                       static_cast<unsigned>((conv->cout + kGN - 1) / kGN));
@@ -1188,7 +1213,10 @@ void conv_run_impl(const s3dx_conv *conv, const s3dx_gather_plan *gplan, const v
             }
             hipLaunchKernelGGL(plan.fn, plan.grid, dim3(plan.threads), plan.smem, s, a);
             launch_check(plan.linear ? "conv_linear" : "conv_mfma");
-            if (plan.stream_k) {
+            if (plan.stream_k && plan.sk_splitk) {
+                launch_splitk_combine_f32(a, (n_out + 63) / 64, plan.sk_groups, s);
+                launch_check("conv_splitk_combine");
+            } else if (plan.stream_k) {
                 launch_halo8_combine(a, (n_out + 127) / 128, plan.sk_groups, s);
                 launch_check("conv_halo8_combine");
             }

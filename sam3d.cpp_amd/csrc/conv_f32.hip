@@ -12,6 +12,13 @@ KernelFn pick_mfma_f32(int id, int kc, bool xf) {
     }
 }
 
+KernelFn pick_splitk_stream_k_f32() { return conv_splitk_sk_kernel<float, 4, 32, 0, 1, 2>; }
+
+void launch_splitk_combine_f32(const ConvArgs &a, int64_t tiles, int groups, hipStream_t stream) {
+    hipLaunchKernelGGL(HIP_KERNEL_NAME(splitk_combine_kernel<float, 4, 32, 2>),
+                       dim3(static_cast<unsigned>(tiles), static_cast<unsigned>(groups)), dim3(256), 0, stream, a);
+}
+
 KernelFn pick_linear_f32(int nbt) { return pick_linear<float>(nbt); }
 
 KernelFn pick_linear_f32_bf16_rows(int nbt) { return pick_linear<float, true>(nbt); }

@@ -651,16 +651,6 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_halo_kernel(ConvArg
     finish_rows<TPR, ROWS, SM::STG_LD>(a, stg, part, m0, nb0, tile_rows, tid, res);
 }
 
-// Stream-K runs: run g takes units [sk_run_begin(g), sk_run_begin(g + 1)).
-__device__ __forceinline__ int64_t sk_run_begin(int64_t g, int64_t units, int32_t runs) { return g * units / runs; }
-// The run holding unit u (runs are non-empty when units >= runs).
-__device__ __forceinline__ int sk_run_of(int64_t u, int64_t units, int32_t runs) {
-    int g = static_cast<int>(min(static_cast<int64_t>(runs - 1), u * runs / units));
-    while (g + 1 < runs && sk_run_begin(g + 1, units, runs) <= u) ++g;
-    while (g > 0 && sk_run_begin(g, units, runs) > u) --g;
-    return g;
-}
-
 // 128-row x 128-column tiles read through 128-row gather-plan records: one
 // workgroup of 8 waves per CU, two waves per SIMD on the same tile.  Wave w
 // holds k-step ks = w % 4 of every 64-channel chunk for column half

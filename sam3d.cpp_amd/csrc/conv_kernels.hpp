@@ -94,6 +94,11 @@ constexpr int kHalo8Threads = 512;
 // runs left in parts (after it, on the same stream).
 KernelFn pick_halo8_stream_k();
 void launch_halo8_combine(const ConvArgs &a, int64_t tiles, int groups, hipStream_t stream);
+// The same for the FP32 split-K kernel of tiling 18 (64-row x 128-column
+// tiles, 32-channel tasks, two workgroups per CU): its stream-K variant and
+// the pass over its split tiles (tiles of 64 rows).
+KernelFn pick_splitk_stream_k_f32();
+void launch_splitk_combine_f32(const ConvArgs &a, int64_t tiles, int groups, hipStream_t stream);
 void launch_gather_plan_build(int rows, const int32_t *kmap, int64_t n_out, int64_t n_src, int32_t row_shift,
                               void *plan, hipStream_t stream);
 // Kernel map of coords (insert, then one workgroup per plan tile computing
@@ -840,11 +845,27 @@ struct SplitSmem {
     static constexpr int TOTAL = REGION0 + ROWS_BYTES + 128;
 };
 
+// Stream-K runs: run g takes units [sk_run_begin(g), sk_run_begin(g + 1)).
+__device__ __forceinline__ int64_t sk_run_begin(int64_t g, int64_t units, int32_t runs) { return g * units / runs; }
+// The run holding unit u (runs are non-empty when units >= runs).
+__device__ __forceinline__ int sk_run_of(int64_t u, int64_t units, int32_t runs) {
+    int g = static_cast<int>(min(static_cast<int64_t>(runs - 1), u * runs / units));
+    while (g + 1 < runs && sk_run_begin(g + 1, units, runs) <= u) ++g;
+    while (g > 0 && sk_run_begin(g, units, runs) > u) --g;
+    return g;
+}
+
 // SUB > 1: a task is SUB consecutive sub-tasks (offset, KC/SUB-channel
 // chunk), so that Cin of 96 (32-channel chunks) or 192 (64) still gives each
 // wave whole k-steps of a 128-channel task.
-template <class T, int NB, int KC, int XF, int SUB, int MB>
-__global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_splitk_kernel(ConvArgs a) {
+//
+// SK (conv_splitk_sk_kernel, SUB 1): stream-K runs over the (column group,
+// tile, task) units, tasks counted over all kvol offsets of a tile, as the
+// 8-wave halo kernel's (equal runs, whole tiles finished here, parts of a
+// tile left as FP32 tiles in the run's two slots for splitk_combine_kernel).
+template <class T, int NB, int KC, int XF, int SUB, int MB, bool SK>
+__device__ __forceinline__ void splitk_body(const ConvArgs &a) {
+    static_assert(!SK || SUB == 1, "stream-K runs walk single-chunk tasks");
     using SM = SplitSmem<T, NB, KC, MB>;
     constexpr int RPH = SM::RPH;
     constexpr int E = Frag<T>::E;
@@ -868,13 +889,21 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_splitk_kernel(ConvA
     char *abuf = smem;
     int32_t *rows = reinterpret_cast<int32_t *>(smem + SM::REGION0);
     uint32_t *omask = reinterpret_cast<uint32_t *>(rows + BM * kMaxKvol);
+    const int chunks_all = a.cin / (KC / SUB);  // sub-task chunks per offset
 
-    const int tid = threadIdx.x, lane = tid & 63;
+    // One tile's tasks [tb0, tb1) (all of them: 0, INT32_MAX), finished into
+    // y, or with part_out its FP32 tile left there.
+    auto piece = [&](const int tile, const int nb0, const int tb0, const int tb1, float *const part_out)
+        __attribute__((always_inline)) {
+    // (stream-K: the thread index passes an empty asm in each piece, so that
+    // what derives from it is computed per piece, not hoisted out of the
+    // run's loop and held -- spilled -- across every piece)
+    int tid_v = static_cast<int>(threadIdx.x);
+    if constexpr (SK) asm volatile("" : "+v"(tid_v));
+    const int tid = tid_v, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
     const int half = lane >> 5;
-    const int tile = xcd_tile(blockIdx.x, gridDim.x);
     const int64_t m0 = static_cast<int64_t>(tile) * BM;
-    const int nb0 = blockIdx.y * NB;
     const int nbtot = a.cout_pad / 32;
     const int kvol = a.kvol;
     const int ksteps_total = a.cin / CPK;
@@ -1204,10 +1233,13 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_splitk_kernel(ConvA
     const uint32_t mask = __builtin_amdgcn_readfirstlane(*omask);
     const int nsub = __popc(mask) * chunks;
     const int ntasks = (nsub + SUB - 1) / SUB;
+    // this piece's tasks [tb, tb + cnt) (a stream-K range over the nominal
+    // kvol * chunks tasks holds fewer where offsets are absent)
+    const int tb = min(tb0, ntasks), cnt = min(tb1, ntasks) - tb;
 
     // ---- main loop.  Entering task t: A(t)'s fragments in registers, A(t+1)
     // on its way into ra, B(t) and B(t+1) in registers or on their way.
-    if (ntasks > 0) {
+    if (cnt > 0) {
         char *buf0 = abuf, *buf1 = abuf + BM * SM::A_LD;
         uint4 b0[KSW][NB], b1[KSW][NB];
         uint4 fx[KSW][4], fy[KSW][4];
@@ -1215,8 +1247,19 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_splitk_kernel(ConvA
         // An odd task count peels task 0 before the loop, so the loop always
         // runs whole pairs; the peel's weights and fragments then live in the
         // other register sets, and the two LDS buffers swap roles.
-        const bool odd = ntasks & 1;
+        const bool odd = cnt & 1;
         Cursor cur{mask, -1, chunks - 1};
+        if constexpr (SK) {
+            // the cursor as task tb - 1 leaves it: its offset is the r-th
+            // present one, its chunk (tb - 1) % chunks
+            if (tb > 0) {
+                const int r = (tb - 1) / chunks;
+                uint32_t rest = mask;
+                for (int k = 0; k < r; ++k) rest &= rest - 1u;
+                const int o = __builtin_ctz(rest | 0x80000000u);
+                cur = Cursor{rest & (rest - 1u), o, (tb - 1) - r * chunks};
+            }
+        }
         int left = nsub;
         Task nx;
         next_task(cur, left, nx);  // task 0
@@ -1248,7 +1291,7 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_splitk_kernel(ConvA
         } else {
             read_frags(buf0, fx);
         }
-        for (int t = odd ? 1 : 0; t < ntasks; t += 2) {
+        for (int t = odd ? 1 : 0; t < cnt; t += 2) {
             body(fx, fy, b0, buf1, ra, nx, cur, left);
             body(fy, fx, b1, buf0, ra, nx, cur, left);
         }
@@ -1347,6 +1390,101 @@ __global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_splitk_kernel(ConvA
 #pragma unroll
             for (int r = 0; r < 16; ++r) stg[(rb + 8 * (r >> 2) + (r & 3)) * SM::STG_LD + col] = fin[p][i][r];
         }
+    if (SK && part_out) {
+        // part of a tile: its FP32 tile, rows in order, to the partial slot
+        constexpr int C4 = SM::NT / 4;
+        static_assert(BM * C4 % 256 == 0, "whole 16-byte pieces per thread");
+        __syncthreads();
+#pragma unroll
+        for (int k = 0; k < BM * C4 / 256; ++k) {
+            const int pc = tid + k * 256, row = pc / C4, c4 = pc - row * C4;
+            reinterpret_cast<float4 *>(part_out)[pc] =
+                *reinterpret_cast<const float4 *>(stg + row * SM::STG_LD + 4 * c4);
+        }
+    } else {
+        uint4 res[RowMap<SM::TPR, BM>::PASSES][2];
+        load_residual<SM::TPR, BM>(a, m0, nb0, tile_rows, tid, res);
+        __syncthreads();
+        finish_rows<SM::TPR, BM, SM::STG_LD>(a, stg, part, m0, nb0, tile_rows, tid, res);
+    }
+    };
+    if constexpr (!SK) {
+        piece(xcd_tile(blockIdx.x, gridDim.x), blockIdx.y * NB, 0, INT32_MAX, nullptr);
+    } else {
+        const int64_t tiles = (a.n_out + BM - 1) / BM;
+        const int64_t ntf = static_cast<int64_t>(a.kvol) * chunks_all;  // nominal tasks per tile
+        const int g = xcd_tile(blockIdx.x, gridDim.x);  // XCD-contiguous runs
+        const int64_t u1 = sk_run_begin(g + 1, a.sk_units, a.sk_wgs);
+        int slot = 0;
+        for (int64_t u = sk_run_begin(g, a.sk_units, a.sk_wgs); u < u1;) {
+            const int64_t gt = u / ntf;  // column group * tiles + tile
+            const int t0 = static_cast<int>(u - gt * ntf);
+            const int t1 = static_cast<int>(min(ntf, t0 + (u1 - u)));
+            const int grp = static_cast<int>(gt / tiles);
+            const bool whole = t0 == 0 && t1 == ntf;
+            __syncthreads();  // the previous piece is done with LDS
+            piece(static_cast<int>(gt - grp * tiles), grp * NB, t0, t1,
+                  whole ? nullptr : a.sk_partial + (static_cast<int64_t>(g) * 2 + slot) * (BM * SM::NT));
+            slot += whole ? 0 : 1;
+            u += t1 - t0;
+        }
+    }
+}
+
+template <class T, int NB, int KC, int XF, int SUB, int MB>
+__global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_splitk_kernel(ConvArgs a) {
+    splitk_body<T, NB, KC, XF, SUB, MB, false>(a);
+}
+template <class T, int NB, int KC, int XF, int SUB, int MB>
+__global__ void __launch_bounds__(256, MB == 4 ? 1 : 2) conv_splitk_sk_kernel(ConvArgs a) {
+    splitk_body<T, NB, KC, XF, SUB, MB, true>(a);
+}
+
+// The tiles that a split-K kernel's stream-K runs left in parts: the pieces'
+// FP32 tiles added in task order (the runs in order), then the epilogue of
+// the whole-tile path.  One workgroup per (tile, column group); tiles one
+// run covers whole were finished by the conv kernel and are skipped.
+template <class T, int NB, int KC, int MB>
+__global__ void __launch_bounds__(256) splitk_combine_kernel(ConvArgs a) {
+    using SM = SplitSmem<T, NB, KC, MB>;
+    constexpr int BM = SM::BM, C4 = SM::NT / 4, K = BM * C4 / 256;
+    __shared__ __align__(16) char smem[SM::STG_BYTES + SM::PART_BYTES];
+    float *stg = reinterpret_cast<float *>(smem);
+    float *part = reinterpret_cast<float *>(smem + SM::STG_BYTES);
+    const int tid = threadIdx.x;
+    const int64_t tiles = gridDim.x;
+    const int tile = blockIdx.x, nb0 = blockIdx.y * NB;
+    const int64_t ntf = static_cast<int64_t>(a.kvol) * (a.cin / KC);
+    const int64_t uf = (static_cast<int64_t>(blockIdx.y) * tiles + tile) * ntf, ul = uf + ntf - 1;
+    const int gf = sk_run_of(uf, a.sk_units, a.sk_wgs), gl = sk_run_of(ul, a.sk_units, a.sk_wgs);
+    if (gf == gl) return;
+    const int64_t m0 = static_cast<int64_t>(tile) * BM;
+    const int tile_rows = static_cast<int>(min(static_cast<int64_t>(BM), a.n_out - m0));
+    float4 sum[K];
+    for (int g = gf; g <= gl; ++g) {
+        // this tile's piece is run g's second partial one when the run began
+        // in the middle of an earlier tile
+        const int64_t b = sk_run_begin(g, a.sk_units, a.sk_wgs);
+        const int slot = b < uf && b % ntf != 0 ? 1 : 0;
+        const float4 *src = reinterpret_cast<const float4 *>(a.sk_partial + (static_cast<int64_t>(g) * 2 + slot) * (BM * SM::NT));
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            const float4 v = src[tid + k * 256];
+            if (g == gf) {
+                sum[k] = v;
+            } else {
+                sum[k].x += v.x;
+                sum[k].y += v.y;
+                sum[k].z += v.z;
+                sum[k].w += v.w;
+            }
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int pc = tid + k * 256, row = pc / C4, c4 = pc - row * C4;
+        *reinterpret_cast<float4 *>(stg + row * SM::STG_LD + 4 * c4) = sum[k];
+    }
     uint4 res[RowMap<SM::TPR, BM>::PASSES][2];
     load_residual<SM::TPR, BM>(a, m0, nb0, tile_rows, tid, res);
     __syncthreads();

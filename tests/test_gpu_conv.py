@@ -519,3 +519,78 @@ def test_bf16_rows_three_term_epilogue(s3dx, W, y_dtype, cin, cout, p):
     h = h / (1.0 + np.exp(-h)) + res
     ref = np.repeat(h, 8, axis=0)
     check_rel(got, ref, 1e-6 if y_dtype == s3dx.F32 else 4e-3)
+
+
+# FP32 split-K layers with long tiles (at least 256 tasks a tile) that take
+# more than one pass over the CUs run in stream-K runs: equal runs of
+# (column group, tile, task) units, two per CU, and a pass that adds the
+# pieces of tiles split between runs.  Forced run counts cut tiles in many
+# places (runs inside a tile, across several, the tail tile); the fused
+# LayerNorm + SiLU, the residual and a LayerNorm pass over 512 columns come
+# after the pieces are added.  FP32 gate against the oracle on sampled rows,
+# the same bits on a second launch, and the 5,086-row 1024 -> 1024 layer
+# picks the runs by itself.
+SPLITK_STREAM_K = {
+    # name: (set, cin, cout, LayerNorm+SiLU, residual, runs); "fine": the
+    # 28,265-row config-2 set, "coarse": its 5,086 coarse rows (tail tile of 30)
+    "fine_cin512_ln_300runs": ("fine", 512, 128, True, False, 300),
+    "fine_cin512_res_97runs": ("fine", 512, 128, False, True, 97),
+    "coarse_cin512_cout1024_res_1000runs": ("coarse", 512, 1024, False, True, 1000),  # runs inside tiles
+    "coarse_cin512_cout512_ln_7runs": ("coarse", 512, 512, True, True, 7),  # LayerNorm as its own pass
+}
+
+
+@pytest.mark.parametrize("case", list(SPLITK_STREAM_K))
+def test_splitk_stream_k_runs(s3dx, O, W, monkeypatch, case):
+    which, cin, cout, ln, with_res, runs = SPLITK_STREAM_K[case]
+    coords = W.shells_union(0)
+    if which == "coarse":
+        nc, coarse, _, _, _ = O.coarsen2(coords)
+        coords = np.ascontiguousarray(coarse[:nc])
+    n = coords.shape[0]
+    kmap = O.kmap_subm3(coords, n)
+    seed = 70 + runs % 50
+    w, b = W.conv_weight(seed, 2, cin, cout), W.normal_f32(seed, 3, (cout,), 0.1)
+    conv = s3dx.SparseConv(cin, cout, 27, s3dx.F32).set_weights(w, s3dx.WEIGHT_SLAT, b)
+    if ln:
+        conv.set_layernorm(True, 1e-6).set_silu(True)
+    x = W.normal_f32(seed, 1, (n, cin))
+    res = W.normal_f32(seed, 6, (n, cout)) if with_res else None
+    xd, kd = to_dev(s3dx, x, s3dx.F32), s3dx.DeviceArray.from_host(kmap)
+    rd = to_dev(s3dx, res, s3dx.F32) if with_res else None
+    monkeypatch.setenv("S3DX_STREAM_K_RUNS", str(runs))
+    plan = conv.plan(n, n)
+    print(f"{case}: {plan}", flush=True)
+    assert plan.startswith("mfma tiling=18 split-k stream-k rows=64") and f"grid={runs}x1" in plan, plan
+    y1, y2 = s3dx.DeviceArray((n, cout), np.float32), s3dx.DeviceArray((n, cout), np.float32)
+    conv.run(xd, n, kd, n, y1, s3dx.F32, rd)
+    conv.run(xd, n, kd, n, y2, s3dx.F32, rd)
+    assert np.array_equal(y1.download(), y2.download()), "stream-K runs differ between launches"
+    rows = np.sort(np.concatenate([np.random.default_rng(seed).choice(n - 64, 300, replace=False), np.arange(n - 64, n)]))
+    h = O.conv(x, kmap[rows], n, w, 0, cout, b)
+    if ln:
+        h = O.silu(O.layernorm(h, 1e-6))
+    if with_res:
+        h = h + res[rows]
+    check_rel(y1.download()[rows], h, TOL[0], case)
+
+
+def test_splitk_stream_k_config3_fp32(s3dx, O, W, monkeypatch):
+    fine = W.shells_union(0)
+    nc, coarse, _, _, _ = O.coarsen2(fine)
+    coarse = np.ascontiguousarray(coarse[:nc])
+    kmap = O.kmap_subm3(coarse, nc)
+    c = 1024
+    w = W.conv_weight(0, 311, c, c)
+    conv = s3dx.SparseConv(c, c, 27, s3dx.F32).set_weights(w, s3dx.WEIGHT_SLAT, None)
+    plan = conv.plan(nc, nc)
+    print(f"FP32 config 3: {plan}", flush=True)
+    assert plan.startswith("mfma tiling=18 split-k stream-k rows=64 cols=128") and plan.endswith("grid=512x1"), plan
+    x = W.normal_f32(0, 310, (nc, c))
+    xd, kd = to_dev(s3dx, x, s3dx.F32), s3dx.DeviceArray.from_host(kmap)
+    y = s3dx.DeviceArray((nc, c), np.float32)
+    conv.run(xd, nc, kd, nc, y, s3dx.F32)
+    rows = np.sort(np.random.default_rng(5).choice(nc, 300, replace=False))
+    check_rel(y.download()[rows], O.conv(x, kmap[rows], nc, w, 0, c, None), TOL[0], "FP32 1024 -> 1024 stream-K")
+    monkeypatch.setenv("S3DX_STREAM_K", "0")
+    assert not " stream-k" in conv.plan(nc, nc)
