@@ -658,11 +658,16 @@ LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bo
         require(p.fn != nullptr, "no MFMA kernel for this shape");
         const int64_t mt = (n_out + p.tl->rows() - 1) / p.tl->rows();
         p.grid = dim3(static_cast<unsigned>(mt), static_cast<unsigned>(blocks / p.nb));
-        // FP32 tiling 18 over long tiles that take more than one pass at two
-        // workgroups per CU: stream-K runs, two per CU (the workgroups are
-        // latency-bound, so a pass costs about the same however full it is:
-        // 1024 -> 1024 on 5,086 rows, 640 workgroups, ran 1.52x the time of
-        // the 512 of 4,096 rows).  S3DX_STREAM_K=0 turns it off.
+        // FP32 tiling 18 whose tiles do not fill whole passes at two
+        // workgroups per CU: stream-K runs, two per CU.  The workgroups are
+        // latency-bound, so a pass costs about the same however full it is
+        // (1024 -> 1024 on 5,086 rows, 640 workgroups, ran 1.52x the time of
+        // the 512 of 4,096 rows), and equal runs shorten even one pass
+        // (2048 -> 128 on 442 tiles: 3,143 -> 2,824 us; no L2 penalty at
+        // FP32's MFMA rate).  Tiles of at least 200 tasks (Cin 256 and up:
+        // at 128 -> 128, 108 tasks a tile, the combine pass takes what the
+        // balance gives) and half a pass of them at least, so that pieces
+        // stay long.  S3DX_STREAM_K=0 turns it off.
         if (p.tl->id == 18 && !bf && p.kc == 32 && p.nb == 4 && !p.xf && conv->kvol == kMaxKvol) {
             const char *off = std::getenv("S3DX_STREAM_K");
             const int64_t wgs = mt * p.grid.y, ntf = int64_t(kMaxKvol) * (conv->cin / 32);
@@ -672,7 +677,7 @@ LaunchPlan plan_launch(const s3dx_conv *conv, int64_t x_bytes, int64_t n_out, bo
                 runs = std::atoi(e);
                 forced = true;
             }
-            const bool want = forced ? true : wgs > runs && wgs % runs != 0 && ntf >= 256;
+            const bool want = forced ? true : wgs % runs != 0 && 2 * wgs >= runs && ntf >= 200;
             if (!(off && std::atoi(off) == 0) && want && runs >= 1 && runs <= 65535 && wgs * ntf >= 2 * runs) {
                 p.stream_k = true;
                 p.sk_splitk = true;
