@@ -307,7 +307,11 @@ S3DX_API s3dx_status s3dx_conv_set_input_dtype(s3dx_conv *conv, int32_t dtype, c
 /* Runs the layer.  x [n_in or n_in parents][cin] in the layer's input dtype; kmap
  * [n_out][kvol] (NULL only for kvol 1, where output row i reads input row i,
  * so n_out may not exceed the input rows); residual [n_out][cout] in y_dtype
- * or NULL; y [n_out][cout] in y_dtype.  Asynchronous on `stream`. */
+ * or NULL; y [n_out][cout] in y_dtype.  Asynchronous on `stream`.  Launches
+ * in stream-K runs (see s3dx_conv_run_planned; FP32 layers of Cin >= 256 as
+ * well) keep their partial tiles in another buffer the layer owns (up to
+ * 64 MiB): as with the transform buffer, runs of one layer object on
+ * different streams must not overlap. */
 S3DX_API s3dx_status s3dx_conv_run(const s3dx_conv *conv, const void *x, int64_t n_in,
                                    const int32_t *kmap, int64_t n_out, const void *residual,
                                    void *y, int32_t y_dtype, s3dx_stream stream, char *error,
