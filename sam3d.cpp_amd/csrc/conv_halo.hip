@@ -692,14 +692,20 @@ __device__ __forceinline__ void halo8_body(const ConvArgs &a) {
     const int nbtot = a.cout_pad / 32;
     const int ksteps_total = a.cin / 16;
     const int chunks_all = a.cin / kHChunk;
+    const int wave_run = SK ? __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x) >> 6) : 0;
     auto piece = [&](const int tile, const int nb0, const int cbeg, const int cend, float *const part_out)
         __attribute__((always_inline)) {
-    // (stream-K: the thread index passes an empty asm in each piece, so that
-    // what derives from it is computed per piece, as in the one-piece
-    // kernel, not hoisted out of the run's loop and held -- spilled -- across
-    // every piece)
+    // (stream-K: each piece forms the thread index from the wave index and an
+    // mbcnt over an empty asm's zero, and the weight offset stride, the zero
+    // row's value and 1/cout pass empty asms too, so that none of them, nor
+    // what derives from them, is hoisted out of the run's loop and held --
+    // spilled -- across every piece)
     int tid_v = static_cast<int>(threadIdx.x);
-    if constexpr (SK) asm volatile("" : "+v"(tid_v));
+    if constexpr (SK) {
+        int zero = 0;
+        asm volatile("" : "+s"(zero));
+        tid_v = wave_run * 64 + static_cast<int>(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, zero)));
+    }
     const int tid = tid_v, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int ks = wave & 3, ch = wave >> 2;
@@ -758,7 +764,7 @@ __device__ __forceinline__ void halo8_body(const ConvArgs &a) {
         const int b = tid / (kHRowBytes / 16);
         if (b == 0 || dbl)
             reinterpret_cast<uint4 *>(halo + (b * kH8BufRows + zrow) * kHRowBytes)[tid % (kHRowBytes / 16)] =
-                make_uint4(0, 0, 0, 0);
+                make_uint4(opaque_scalar<SK>(0), 0, 0, 0);
     }
 
     // Chunk c of every distinct row into its slot of `buf` (lane L of a
@@ -815,7 +821,7 @@ __device__ __forceinline__ void halo8_body(const ConvArgs &a) {
     // Fragment (k-step, column block) of the packed weights sits at byte
     // ((kstep * nbtot + cb) * 64 + lane) * 16: for (chunk c, offset o) this
     // wave's two fragments start at w_first + c * w_chunk + o * w_offset.
-    const int32_t w_offset = ksteps_total * nbtot * 1024;
+    const int32_t w_offset = opaque_scalar<SK>(ksteps_total * nbtot * 1024);
     const int32_t w_chunk = 4 * nbtot * 1024;
     const int32_t w_first = (ks * nbtot + nb0 + 2 * ch) * 1024;
     // (voff_extra 0x80000000 puts the loads out of range: zeros, no memory read)
@@ -1262,7 +1268,14 @@ __device__ __forceinline__ void halo8_body(const ConvArgs &a) {
         uint4 res[RowMap<16, ROWS, kHalo8Threads>::PASSES][2];
         load_residual<16, ROWS, kHalo8Threads>(a, m0, nb0, tile_rows, tid, res);
         __syncthreads();
-        finish_rows<16, ROWS, STG_LD, kHalo8Threads, true>(a, stg, stg, m0, nb0, tile_rows, tid, res, params);
+        // (stream-K: 1/cout formed per piece, not held across the run)
+        float inv_cout = 0.0f;
+        if constexpr (SK) {
+            inv_cout = 1.0f / static_cast<float>(opaque_scalar<SK>(a.cout));
+            __builtin_assume(inv_cout != 0.0f);
+        }
+        finish_rows<16, ROWS, STG_LD, kHalo8Threads, true>(a, stg, stg, m0, nb0, tile_rows, tid, res, params,
+                                                           inv_cout);
     }
     };
     if constexpr (!SK) {
@@ -1273,10 +1286,14 @@ __device__ __forceinline__ void halo8_body(const ConvArgs &a) {
         const int64_t u1 = sk_run_begin(g + 1, a.sk_units, a.sk_wgs);
         int slot = 0;
         for (int64_t u = sk_run_begin(g, a.sk_units, a.sk_wgs); u < u1;) {
-            const int64_t gt = u / chunks_all;  // column group * tiles + tile
-            const int cb = static_cast<int>(u - gt * chunks_all);
-            const int ce = static_cast<int>(min(static_cast<int64_t>(chunks_all), cb + (u1 - u)));
-            const int grp = static_cast<int>(gt / tiles);
+            // (divisors opaque per piece: their reciprocals are not held
+            // in vector registers across the run)
+            int64_t ca = chunks_all, nt = tiles;
+            asm volatile("" : "+s"(ca), "+s"(nt));
+            const int64_t gt = u / ca;  // column group * tiles + tile
+            const int cb = static_cast<int>(u - gt * ca);
+            const int ce = static_cast<int>(min(ca, cb + (u1 - u)));
+            const int grp = static_cast<int>(gt / nt);
             const bool whole = cb == 0 && ce == chunks_all;
             __syncthreads();  // the previous piece is done with LDS
             piece(static_cast<int>(gt - grp * tiles), grp * 4, cb, ce,

@@ -338,19 +338,28 @@ __device__ __forceinline__ void load_row_mod(const ConvArgs &a, int col0, RowPar
     load_cols8(a.mod_shift, col0, a.cout, 0.0f, q.mh);
 }
 
+// v, through an empty asm when ON: a value the compiler cannot hoist out of
+// a loop around the caller.
+template <bool ON>
+__device__ __forceinline__ int opaque_scalar(int v) {
+    if constexpr (ON) asm volatile("" : "+s"(v));
+    return v;
+}
+
 // SWZ: the tile's 16-byte group q of row r sits at q ^ 8 when r & 4.
 template <int TPR, int BM, int STG_LD, int NTH = 256, bool SWZ = false>
 __device__ __forceinline__ void finish_rows(const ConvArgs &a, const float *stg, float *part, int64_t m0,
                                             int nb0, int tile_rows, int tid,
                                             const uint4 (&res)[RowMap<TPR, BM, NTH>::PASSES][2],
-                                            const RowParams &q) {
+                                            const RowParams &q, float inv_cout = 0.0f) {
     using RM = RowMap<TPR, BM, NTH>;
     constexpr int RPP = RM::RPP;
     constexpr int PASSES = RM::PASSES;
     const int cg = tid % TPR, rsub = tid / TPR;
     const bool active = rsub < RPP;
     const int col0 = nb0 * 32 + cg * 8;  // global column of this thread's 8 values
-    const float inv_c = 1.0f / static_cast<float>(a.cout);
+    // (inv_cout: 1/cout formed by the caller, or 0 to form it here)
+    const float inv_c = inv_cout != 0.0f ? inv_cout : 1.0f / static_cast<float>(a.cout);
     // Padded columns are not stored.  Rows of a cout that is not a multiple
     // of 8 are not 16-byte aligned: element stores.
     const bool ragged = a.cout % 8 != 0;
